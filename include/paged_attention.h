@@ -1,0 +1,143 @@
+/*
+ * C ABI of the gfx950 paged-attention library (libpaged_attention.so).
+ *
+ * It replaces the device work behind simpissa/vllm-jax's attention seam
+ * (vllm/model/qwen3.py:172-218): the KV-cache scatter, the Pallas prefill
+ * kernel and the Pallas decode kernel.  Conventions:
+ *
+ *   - every pointer argument except `stream` is a device pointer;
+ *   - bf16 tensors are passed as uint16_t bit patterns;
+ *   - strides are in elements; the innermost (head_dim) stride is always 1;
+ *   - a KV pool is addressed as (page, slot-in-page, kv-head, dim) with
+ *     caller-given strides, so both the engine's native layout
+ *     kv_cache[i] = [num_pages, page_size, Hkv, d] (model_runner.py:190-199)
+ *     and the reference kernels' k_pages = [Hkv, num_pages, page_size, d]
+ *     (prefill_paged_attention.py:186, decode_paged_attention.py:323-324)
+ *     are accepted without a copy;
+ *   - `stream` is a hipStream_t (NULL = the default stream); calls are
+ *     asynchronous and stream-ordered, allocate nothing and never
+ *     synchronise the host;
+ *   - return value 0 = success, negative = error; pa_last_error() describes
+ *     the last error of the calling thread.
+ *
+ * Device-side metadata is never trusted to be in range: negative block-table
+ * entries read page 0 (as qwen3.py:179-180,198-199 sanitise them), entries
+ * past the pool are clamped into it, and slots outside [0, pages*page_size)
+ * are skipped by the KV store.
+ *
+ * Supported shapes: head_dim == 128, num_heads % num_kv_heads == 0,
+ * num_heads / num_kv_heads <= 16 for decode and <= 128 for prefill.
+ */
+#ifndef VLLM_JAX_AMD_PAGED_ATTENTION_H_
+#define VLLM_JAX_AMD_PAGED_ATTENTION_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PA_OK 0
+#define PA_ERR_INVALID_ARGUMENT (-1)
+#define PA_ERR_UNSUPPORTED (-2)
+#define PA_ERR_WORKSPACE (-3)
+#define PA_ERR_LAUNCH (-4)
+
+/* Message for the last non-zero return code on this thread ("" if none). */
+const char* pa_last_error(void);
+
+/* ABI version; bumped on any signature change. */
+int pa_abi_version(void);
+
+/*
+ * KV store: k_cache[slot[t]] = k[t], v_cache[slot[t]] = v[t] for every token
+ * t whose slot lies in [0, num_pages*page_size); other tokens are skipped.
+ * Slot s addresses page s / page_size, in-page slot s % page_size.
+ * Replaces _update_kv_cache (vllm/model/qwen3.py:105-111), in place.
+ * k: [num_tokens, Hkv, d] with strides (k_tok_stride, k_head_stride, 1);
+ * v likewise.  Slots must be unique (the reference leaves the winner of a
+ * duplicate unspecified).
+ */
+int pa_kv_store(const uint16_t* k, int64_t k_tok_stride, int64_t k_head_stride,
+                const uint16_t* v, int64_t v_tok_stride, int64_t v_head_stride,
+                const int32_t* slot_mapping, int32_t num_tokens,
+                int32_t num_kv_heads, int32_t head_dim,
+                uint16_t* k_cache, uint16_t* v_cache,
+                int32_t num_pages, int32_t page_size,
+                int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                void* stream);
+
+/*
+ * Block-table gather (test/debug entry): out[b, j] = cache[bt[b, j / page_size],
+ * j % page_size] for j < lengths[b], zero for j >= lengths[b].
+ * out: contiguous [batch, pages_per_seq * page_size, Hkv, d].
+ * This is the address arithmetic of prefill_paged_attention.py:79-82 and
+ * decode_paged_attention.py:69-71 (dense form: qwen3.py:114-134).
+ */
+int pa_gather_kv(const uint16_t* cache, int32_t num_pages, int32_t page_size,
+                 int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                 const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                 const int32_t* lengths, int32_t batch,
+                 int32_t num_kv_heads, int32_t head_dim, uint16_t* out, void* stream);
+
+/*
+ * Decode workspace in bytes for a launch of `batch` sequences whose block
+ * tables are `pages_per_seq` wide (f32 split partials + their max/sum).
+ */
+size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_dim,
+                                int32_t pages_per_seq, int32_t page_size);
+
+/*
+ * Split-K paged GQA decode: for each sequence b and q head h,
+ *   out[b, h] = softmax_j(scale * q[b, h] . k_j) v_j,  j < lengths[b],
+ * with k_j / v_j of kv head h / (num_heads / num_kv_heads) read through
+ * block_tables[b].  lengths[b] == 0 gives a zero row.  soft_cap > 0 applies
+ * soft_cap * tanh(logit / soft_cap).
+ * Replaces decode_paged_attention (decode_paged_attention.py:300-397); that
+ * entry expects q pre-scaled (qwen3.py:207), i.e. scale = 1.
+ * q: [batch, H, d] strides (q_batch_stride, q_head_stride, 1);
+ * out: [batch, H, d] strides (out_batch_stride, out_head_stride, 1).
+ */
+int pa_decode(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
+              const uint16_t* k_cache, const uint16_t* v_cache,
+              int32_t num_pages, int32_t page_size,
+              int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+              const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+              const int32_t* lengths, int32_t batch,
+              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+              float scale, float soft_cap,
+              uint16_t* out, int64_t out_batch_stride, int64_t out_head_stride,
+              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Ragged causal GQA paged prefill.  Sequence b owns q rows
+ * [cu_seqlens_q[b], cu_seqlens_q[b+1]) and kv indices [0, Lk_b) with
+ * Lk_b = cu_seqlens_k[b+1] - cu_seqlens_k[b] (cu_seqlens_k == NULL: Lk_b is
+ * the q length, the reference's rule).  kv index j has position
+ * j + input_positions[cu_seqlens_q[b]] - (Lk_b - Lq_b) and is visible to row
+ * i iff that position <= input_positions[i].  Rows outside every sequence
+ * are written as zeros.  max_seqlen_q bounds every q length (the reference's
+ * static max_seqlen_bucket may be passed).
+ * Replaces prefill_paged_attention (prefill_paged_attention.py:407-453),
+ * which scales q by 1/sqrt(d) itself (prefill_paged_attention.py:60).
+ * q/out: [num_tokens, H, d] with (tok, head) strides.
+ */
+int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+               const uint16_t* k_cache, const uint16_t* v_cache,
+               int32_t num_pages, int32_t page_size,
+               int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+               const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+               const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+               const int32_t* input_positions,
+               int32_t batch, int32_t num_tokens, int32_t max_seqlen_q,
+               int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+               float scale, float soft_cap,
+               uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
+               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VLLM_JAX_AMD_PAGED_ATTENTION_H_ */

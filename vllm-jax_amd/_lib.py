@@ -1,0 +1,111 @@
+"""ctypes binding of libpaged_attention.so (the gfx950 C ABI).
+
+The signatures mirror ``include/paged_attention.h``.  Loading fails loudly:
+there is no CPU or PyTorch fallback for any entry point.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+from . import build as _build
+
+_LOCK = threading.Lock()
+_LIB = None
+
+c_i32, c_i64, c_f32, c_sz, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "pa_last_error": (ctypes.c_char_p, []),
+    "pa_abi_version": (ctypes.c_int, []),
+    "pa_kv_store": (ctypes.c_int, [
+        c_vp, c_i64, c_i64,            # k, k_tok_stride, k_head_stride
+        c_vp, c_i64, c_i64,            # v, ...
+        c_vp, c_i32,                   # slot_mapping, num_tokens
+        c_i32, c_i32,                  # num_kv_heads, head_dim
+        c_vp, c_vp,                    # k_cache, v_cache
+        c_i32, c_i32,                  # num_pages, page_size
+        c_i64, c_i64, c_i64,           # page/slot/head strides
+        c_vp,                          # stream
+    ]),
+    "pa_gather_kv": (ctypes.c_int, [
+        c_vp, c_i32, c_i32, c_i64, c_i64, c_i64,
+        c_vp, c_i64, c_i32,
+        c_vp, c_i32,
+        c_i32, c_i32, c_vp, c_vp,
+    ]),
+    "pa_decode_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "pa_decode": (ctypes.c_int, [
+        c_vp, c_i64, c_i64,            # q
+        c_vp, c_vp, c_i32, c_i32,      # caches, num_pages, page_size
+        c_i64, c_i64, c_i64,           # strides
+        c_vp, c_i64, c_i32,            # block_tables, bt_stride, pages_per_seq
+        c_vp, c_i32,                   # lengths, batch
+        c_i32, c_i32, c_i32,           # heads, kv heads, head_dim
+        c_f32, c_f32,                  # scale, soft_cap
+        c_vp, c_i64, c_i64,            # out
+        c_vp, c_sz, c_vp,              # workspace, bytes, stream
+    ]),
+    "pa_prefill": (ctypes.c_int, [
+        c_vp, c_i64, c_i64,            # q
+        c_vp, c_vp, c_i32, c_i32,      # caches, num_pages, page_size
+        c_i64, c_i64, c_i64,           # strides
+        c_vp, c_i64, c_i32,            # block_tables, bt_stride, pages_per_seq
+        c_vp, c_vp, c_vp,              # cu_seqlens_q, cu_seqlens_k, input_positions
+        c_i32, c_i32, c_i32,           # batch, num_tokens, max_seqlen_q
+        c_i32, c_i32, c_i32,           # heads, kv heads, head_dim
+        c_f32, c_f32,                  # scale, soft_cap
+        c_vp, c_i64, c_i64,            # out
+        c_vp,                          # stream
+    ]),
+}
+
+
+class PagedAttentionError(RuntimeError):
+    """A non-zero return code from the C ABI."""
+
+    def __init__(self, func: str, code: int, message: str):
+        super().__init__(f"{func} returned {code}: {message}")
+        self.code = code
+
+
+def lib_path() -> str:
+    return _build.LIB_PATH
+
+
+def load():
+    """Load (once) and return the ctypes library handle.
+
+    Raises ``RuntimeError`` if the library has not been built.
+    """
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    with _LOCK:
+        if _LIB is not None:
+            return _LIB
+        path = lib_path()
+        if not os.path.exists(path):
+            raise RuntimeError(
+                f"{path} is missing: build the gfx950 library first "
+                "(python vllm-jax_amd/build.py or __graft_entry__.build())")
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _LIB = lib
+    return _LIB
+
+
+def check(func: str, code: int) -> None:
+    if code != 0:
+        msg = load().pa_last_error().decode(errors="replace")
+        raise PagedAttentionError(func, code, msg)
+
+
+def call(func: str, *args) -> None:
+    """Call a C-ABI entry point and raise on a non-zero return code."""
+    check(func, getattr(load(), func)(*args))

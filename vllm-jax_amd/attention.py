@@ -1,0 +1,132 @@
+"""The layer seam: ``attention(kv_cache, q, k, v, metadata) -> (kv_cache, out)``.
+
+Drop-in for ``vllm/model/qwen3.py:attention`` (qwen3.py:172-218) and its
+metadata types (qwen3.py:17-37), with torch tensors on a HIP device.
+Per layer it (1) stores the new K/V tokens into the paged pool through the
+slot mapping (``_update_kv_cache``, qwen3.py:105-111) and (2) runs the paged
+prefill or decode kernel.  Differences from the reference, all deliberate:
+
+* the pool is updated in place and the same tensor is returned (the
+  reference is functional and copies the pool every step without donation);
+* no ``[NB, BS, Hkv, d] -> [Hkv, NB, BS, d]`` transpose (qwen3.py:177-178,
+  196-197): the kernels read the native layout through strides;
+* decode folds ``1/bf16(sqrt(d))`` into the kernel instead of pre-scaling q
+  in bf16 (qwen3.py:207);
+* prefill passes ``cu_seqlens_k`` so a cached prefix can precede the new
+  tokens (with ``cu_seqlens_k == cu_seqlens_q``, the engine's case, the
+  semantics are the reference's).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Tuple, Union
+
+import torch
+
+from . import _lib
+from .kernels._common import bf16_round, require_bf16, require_device, stream_handle
+from .kernels.decode_paged_attention import decode_paged_attention
+from .kernels.prefill_paged_attention import prefill_paged_attention
+
+USE_DECODE_PAGED_ATTENTION_KERNEL = True
+USE_PREFILL_PAGED_ATTENTION_KERNEL = True
+
+
+@dataclass
+class DecodeAttentionMetadata:
+    """qwen3.py:17-22."""
+    input_positions: torch.Tensor
+    slot_mapping: torch.Tensor
+    block_tables: torch.Tensor
+    context_lens: torch.Tensor
+
+
+@dataclass
+class PrefillAttentionMetadata:
+    """qwen3.py:25-34 (``max_seqlen_bucket`` is static in the reference)."""
+    input_positions: torch.Tensor
+    slot_mapping: torch.Tensor
+    block_tables: torch.Tensor
+    cu_seqlens_q: torch.Tensor
+    cu_seqlens_k: torch.Tensor
+    max_seqlen_q: torch.Tensor
+    max_seqlen_k: torch.Tensor
+    max_seqlen_bucket: int = field(default=0)
+
+
+AttentionMetadata = Union[DecodeAttentionMetadata, PrefillAttentionMetadata]
+
+
+def update_kv_cache(kv_cache: torch.Tensor, slot_mapping: torch.Tensor, k: torch.Tensor,
+                    v: torch.Tensor) -> torch.Tensor:
+    """In-place KV store: ``kv_cache[0].flat[slot[t]] = k[t]``, same for v.
+
+    ``kv_cache`` is ``[2, NB, BS, Hkv, d]`` (model_runner.py:195); ``k``/``v``
+    are ``[T, Hkv, d]``.  Slots < 0 (padding tokens) and slots past the pool
+    are skipped (qwen3.py:109-110 uses ``mode="drop"``).
+    """
+    for name, t in (("kv_cache", kv_cache), ("slot_mapping", slot_mapping), ("k", k), ("v", v)):
+        require_device(name, t)
+    require_bf16("kv_cache", kv_cache)
+    require_bf16("k", k)
+    require_bf16("v", v)
+    if kv_cache.dim() != 5 or kv_cache.shape[0] != 2:
+        raise ValueError(f"kv_cache must be [2, NB, BS, Hkv, d], got {tuple(kv_cache.shape)}")
+    _, nb, bs, hkv, d = kv_cache.shape
+    if k.dim() != 3 or tuple(k.shape[1:]) != (hkv, d) or tuple(v.shape) != tuple(k.shape):
+        raise ValueError(f"k/v must be [T, {hkv}, {d}], got {tuple(k.shape)} and {tuple(v.shape)}")
+    if slot_mapping.dtype != torch.int32 or tuple(slot_mapping.shape) != (k.shape[0],):
+        raise ValueError("slot_mapping must be int32 of shape [T]")
+    kc, vc = kv_cache[0], kv_cache[1]
+    sm = slot_mapping if slot_mapping.is_contiguous() else slot_mapping.contiguous()
+    _lib.call(
+        "pa_kv_store",
+        k.data_ptr(), k.stride(0), k.stride(1),
+        v.data_ptr(), v.stride(0), v.stride(1),
+        sm.data_ptr(), k.shape[0], hkv, d,
+        kc.data_ptr(), vc.data_ptr(), nb, bs,
+        kc.stride(0), kc.stride(1), kc.stride(2),
+        stream_handle(k))
+    return kv_cache
+
+
+# reference name (qwen3.py:105)
+_update_kv_cache = update_kv_cache
+
+
+def attention(kv_cache: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+              metadata: AttentionMetadata) -> Tuple[torch.Tensor, torch.Tensor]:
+    """qwen3.py:172-218 on gfx950 kernels; returns ``(kv_cache, out)``."""
+    if not (USE_PREFILL_PAGED_ATTENTION_KERNEL and USE_DECODE_PAGED_ATTENTION_KERNEL):
+        raise NotImplementedError("the dense fallbacks of qwen3.py:120-169 are not part of this library")
+    kv_cache = update_kv_cache(kv_cache, metadata.slot_mapping, k, v)
+    k_pages = kv_cache[0].permute(2, 0, 1, 3)   # [Hkv, NB, BS, d] view
+    v_pages = kv_cache[1].permute(2, 0, 1, 3)
+    if isinstance(metadata, PrefillAttentionMetadata):
+        outputs = prefill_paged_attention(
+            q, k_pages, v_pages, metadata.block_tables, metadata.cu_seqlens_q,
+            metadata.slot_mapping, metadata.input_positions,
+            max_seqlen_bucket=metadata.max_seqlen_bucket,
+            cu_seqlens_k=metadata.cu_seqlens_k)
+    else:
+        head_dim = q.shape[-1]
+        outputs = decode_paged_attention(
+            q, k_pages, v_pages, metadata.block_tables, metadata.context_lens,
+            scale=1.0 / bf16_round(float(head_dim) ** 0.5))
+    return kv_cache, outputs
+
+
+def gather_kv(cache: torch.Tensor, block_tables: torch.Tensor, lengths: torch.Tensor) -> torch.Tensor:
+    """Dense ``[B, P*BS, Hkv, d]`` context of each sequence through its block
+    table (test/debug helper; the address math of prefill...:79-82)."""
+    for name, t in (("cache", cache), ("block_tables", block_tables), ("lengths", lengths)):
+        require_device(name, t)
+    require_bf16("cache", cache)
+    nb, bs, hkv, d = cache.shape
+    b, p = block_tables.shape
+    bt = block_tables.contiguous()
+    ln = lengths.contiguous()
+    out = torch.empty((b, p * bs, hkv, d), dtype=cache.dtype, device=cache.device)
+    _lib.call("pa_gather_kv", cache.data_ptr(), nb, bs, cache.stride(0), cache.stride(1), cache.stride(2),
+              bt.data_ptr(), bt.stride(0), p, ln.data_ptr(), b, hkv, d, out.data_ptr(), stream_handle(cache))
+    return out

@@ -1,0 +1,147 @@
+// KV-cache store (scatter of new tokens into pages) and block-table gather.
+//
+// Both are pure data movement bound by HBM: one thread moves one 16-byte
+// chunk (8 bf16) of a token's [Hkv, d] row, so a wave moves 1 KiB of
+// consecutive source bytes per instruction.
+#include "pa_common.h"
+#include "pa_errors.h"
+
+namespace pa {
+
+// k/v rows are [Hkv, d]; one token = Hkv*d/8 chunks of 16 bytes.
+__global__ void __launch_bounds__(256)
+kv_store_vec_kernel(const uint16_t* __restrict__ k, int64_t k_ts, int64_t k_hs,
+                    const uint16_t* __restrict__ v, int64_t v_ts, int64_t v_hs,
+                    const int32_t* __restrict__ slot_mapping, int32_t num_tokens,
+                    int32_t chunks_per_head, int32_t chunks_per_token,
+                    uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+                    int64_t num_slots, int32_t page_size,
+                    int64_t page_stride, int64_t slot_stride, int64_t head_stride) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t t = gid / chunks_per_token;
+  if (t >= num_tokens) return;
+  const int32_t c = (int32_t)(gid - t * chunks_per_token);
+  const int64_t slot = slot_mapping[t];
+  if (slot < 0 || slot >= num_slots) return;  // padding token or dropped slot
+  const int32_t h = c / chunks_per_head;
+  const int32_t e = (c - h * chunks_per_head) * 8;
+  const int64_t page = slot / page_size;
+  const int64_t dst = page * page_stride + (slot - page * page_size) * slot_stride + h * head_stride + e;
+  const u32x4 kv = ld16(k + t * k_ts + h * k_hs + e);
+  const u32x4 vv = ld16(v + t * v_ts + h * v_hs + e);
+  st16(k_cache + dst, kv);
+  st16(v_cache + dst, vv);
+}
+
+// Element-wise fallback for operands that are not 16-byte aligned.
+__global__ void __launch_bounds__(256)
+kv_store_scalar_kernel(const uint16_t* __restrict__ k, int64_t k_ts, int64_t k_hs,
+                       const uint16_t* __restrict__ v, int64_t v_ts, int64_t v_hs,
+                       const int32_t* __restrict__ slot_mapping, int32_t num_tokens,
+                       int32_t head_dim, int32_t elems_per_token,
+                       uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache,
+                       int64_t num_slots, int32_t page_size,
+                       int64_t page_stride, int64_t slot_stride, int64_t head_stride) {
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t t = gid / elems_per_token;
+  if (t >= num_tokens) return;
+  const int32_t c = (int32_t)(gid - t * elems_per_token);
+  const int64_t slot = slot_mapping[t];
+  if (slot < 0 || slot >= num_slots) return;
+  const int32_t h = c / head_dim;
+  const int32_t e = c - h * head_dim;
+  const int64_t page = slot / page_size;
+  const int64_t dst = page * page_stride + (slot - page * page_size) * slot_stride + h * head_stride + e;
+  k_cache[dst] = k[t * k_ts + h * k_hs + e];
+  v_cache[dst] = v[t * v_ts + h * v_hs + e];
+}
+
+// out[b, j] = cache[page(b, j / page_size), j % page_size] for j < len[b], else 0.
+__global__ void __launch_bounds__(256)
+gather_kv_kernel(const uint16_t* __restrict__ cache, int32_t num_pages, int32_t page_size,
+                 int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                 const int32_t* __restrict__ block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                 const int32_t* __restrict__ lengths, int32_t batch,
+                 int32_t head_dim, int32_t elems_per_token, uint16_t* __restrict__ out) {
+  const int64_t tokens_per_seq = (int64_t)pages_per_seq * page_size;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = gid / elems_per_token;  // b * tokens_per_seq + j
+  if (row >= (int64_t)batch * tokens_per_seq) return;
+  const int32_t c = (int32_t)(gid - row * elems_per_token);
+  const int32_t b = (int32_t)(row / tokens_per_seq);
+  const int32_t j = (int32_t)(row - (int64_t)b * tokens_per_seq);
+  uint16_t val = 0;
+  if (j < lengths[b]) {
+    const int32_t page = safe_page(block_tables + (int64_t)b * bt_stride, j / page_size, num_pages);
+    const int32_t h = c / head_dim;
+    const int32_t e = c - h * head_dim;
+    val = cache[(int64_t)page * page_stride + (int64_t)(j % page_size) * slot_stride + h * head_stride + e];
+  }
+  out[gid] = val;
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace pa
+
+using namespace pa;
+
+extern "C" int pa_kv_store(const uint16_t* k, int64_t k_tok_stride, int64_t k_head_stride,
+                           const uint16_t* v, int64_t v_tok_stride, int64_t v_head_stride,
+                           const int32_t* slot_mapping, int32_t num_tokens,
+                           int32_t num_kv_heads, int32_t head_dim,
+                           uint16_t* k_cache, uint16_t* v_cache,
+                           int32_t num_pages, int32_t page_size,
+                           int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                           void* stream) {
+  if (num_tokens < 0 || num_kv_heads <= 0 || head_dim <= 0 || num_pages <= 0 || page_size <= 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "pa_kv_store: bad sizes (num_tokens=%d, num_kv_heads=%d, head_dim=%d, num_pages=%d, page_size=%d)",
+                num_tokens, num_kv_heads, head_dim, num_pages, page_size);
+  if (num_tokens == 0) return PA_OK;
+  if (!k || !v || !slot_mapping || !k_cache || !v_cache)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_kv_store: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t num_slots = (int64_t)num_pages * page_size;
+  const bool vec = head_dim % 8 == 0 && aligned16(k) && aligned16(v) && aligned16(k_cache) &&
+                   aligned16(v_cache) && k_tok_stride % 8 == 0 && k_head_stride % 8 == 0 &&
+                   v_tok_stride % 8 == 0 && v_head_stride % 8 == 0 && page_stride % 8 == 0 &&
+                   slot_stride % 8 == 0 && head_stride % 8 == 0;
+  if (vec) {
+    const int32_t cph = head_dim / 8;
+    const int32_t cpt = cph * num_kv_heads;
+    const int64_t threads = (int64_t)num_tokens * cpt;
+    const int64_t blocks = (threads + 255) / 256;
+    kv_store_vec_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+        k, k_tok_stride, k_head_stride, v, v_tok_stride, v_head_stride, slot_mapping, num_tokens,
+        cph, cpt, k_cache, v_cache, num_slots, page_size, page_stride, slot_stride, head_stride);
+  } else {
+    const int32_t ept = head_dim * num_kv_heads;
+    const int64_t threads = (int64_t)num_tokens * ept;
+    const int64_t blocks = (threads + 255) / 256;
+    kv_store_scalar_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(
+        k, k_tok_stride, k_head_stride, v, v_tok_stride, v_head_stride, slot_mapping, num_tokens,
+        head_dim, ept, k_cache, v_cache, num_slots, page_size, page_stride, slot_stride, head_stride);
+  }
+  return launch_status("pa_kv_store");
+}
+
+extern "C" int pa_gather_kv(const uint16_t* cache, int32_t num_pages, int32_t page_size,
+                            int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                            const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                            const int32_t* lengths, int32_t batch,
+                            int32_t num_kv_heads, int32_t head_dim, uint16_t* out, void* stream) {
+  if (batch < 0 || pages_per_seq < 0 || num_kv_heads <= 0 || head_dim <= 0 || num_pages <= 0 ||
+      page_size <= 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_gather_kv: bad sizes");
+  if (batch == 0 || pages_per_seq == 0) return PA_OK;
+  if (!cache || !block_tables || !lengths || !out)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_gather_kv: null pointer");
+  const int32_t ept = head_dim * num_kv_heads;
+  const int64_t threads = (int64_t)batch * pages_per_seq * page_size * ept;
+  const int64_t blocks = (threads + 255) / 256;
+  gather_kv_kernel<<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(
+      cache, num_pages, page_size, page_stride, slot_stride, head_stride, block_tables, bt_stride,
+      pages_per_seq, lengths, batch, head_dim, ept, out);
+  return launch_status("pa_gather_kv");
+}

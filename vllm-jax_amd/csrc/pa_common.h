@@ -1,0 +1,95 @@
+// Shared device helpers for the gfx950 paged-attention kernels.
+//
+// Lane layouts of the bf16 MFMA instructions used here (checked on gfx950 by
+// comparing against a host matmul):
+//   v_mfma_f32_16x16x32_bf16: A[m][k]: lane l holds m = l%16, k = 8*(l/16)+i
+//                             B[k][n]: lane l holds n = l%16, k = 8*(l/16)+i
+//                             C[m][n]: lane l holds n = l%16, m = 4*(l/16)+i
+//   v_mfma_f32_32x32x16_bf16: A: m = l%32, k = 8*(l/32)+i
+//                             B: n = l%32, k = 8*(l/32)+i
+//                             C: n = l%32, m = 8*(i/4) + 4*(l/32) + i%4
+// The reduction index k only has to agree between A and B, so kernels are
+// free to permute which data sits in which k slot.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pa {
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
+typedef __attribute__((__vector_size__(16 * sizeof(float)))) float f32x16;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4;
+typedef __attribute__((__vector_size__(2 * sizeof(uint32_t)))) uint32_t u32x2;
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short s16x4;
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// 16-byte global load / store through plain vector memory instructions.
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void st16(void* p, const u32x4& v) {
+  *reinterpret_cast<u32x4*>(p) = v;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) {
+  return __builtin_bit_cast(bf16x8, v);
+}
+__device__ __forceinline__ u32x4 as_u32x4(const bf16x8& v) {
+  return __builtin_bit_cast(u32x4, v);
+}
+
+// bf16 bit pattern <-> float.  The float->bf16 direction rounds to nearest
+// even (the hardware conversion of the __bf16 type on gfx950).
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  __bf16 a = static_cast<__bf16>(lo);
+  __bf16 b = static_cast<__bf16>(hi);
+  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+}
+
+// Value of `x` in lane l^32 / l^16 combined with the own value.  permlane
+// swaps exchange halves of two registers; passing the same register twice
+// yields (own, partner) in some order in every lane.
+__device__ __forceinline__ float max_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float max_xor16(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Physical page of logical page `lp` of a sequence: negative ids (padding
+// entries of the block table) read page 0, ids past the pool are clamped so
+// that no access leaves the pool.
+__device__ __forceinline__ int32_t safe_page(const int32_t* __restrict__ bt_row, int lp, int num_pages) {
+  int32_t p = bt_row[lp];
+  p = p < 0 ? 0 : p;
+  return p >= num_pages ? num_pages - 1 : p;
+}
+
+}  // namespace pa

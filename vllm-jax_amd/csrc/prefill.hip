@@ -1,0 +1,404 @@
+// Ragged causal GQA paged prefill for gfx950.
+//
+// Workgroup = (q tile, sequence, kv head); 4 waves x 32 rows = 128 rows, where
+// a row is a (query token, q head of this kv head) pair: row n of the tile is
+// token n / G, head n % G (G = q heads per kv head).  Packing the G heads into
+// the MFMA dimension makes every K/V tile staged in LDS serve G x tokens rows.
+//
+// Per 64-token KV tile (double-buffered in LDS, loaded through the block table
+// with 16-byte global loads; tokens past the kv length are zero-filled):
+//   S^T[t][n] = K[t][:] . Q[n][:]      v_mfma_f32_32x32x16_bf16, K rows read
+//                                       with ds_read_b128, Q^T kept in VGPRs
+//   online softmax per row n            row n = lane % 32, so the row max needs
+//                                       one permlane32 swap and the rescale of
+//                                       O is lane-local
+//   O^T[d][n] += V^T[d][t] . P^T[t][n]  V^T operand read from the row-major V
+//                                       tile with ds_read_tr16_b64 (gfx950's
+//                                       transposing LDS read), P^T straight
+//                                       from the S^T accumulator registers
+// KV tiles entirely above the causal diagonal of the q tile are never loaded;
+// the mask is evaluated only on tiles that straddle it or the kv length.
+// Workgroups are dispatched from the last q tile down so the longest causal
+// rows start first.
+#include "pa_common.h"
+#include "pa_errors.h"
+
+namespace pa {
+
+constexpr int kPHeadDim = 128;
+constexpr int kRows = 128;       // rows per workgroup
+constexpr int kTileN = 64;       // kv tokens per tile
+constexpr int kKStride = 136;    // K tile row stride in elements (272 B)
+constexpr int kVStride = 160;    // V tile row stride in elements (320 B)
+constexpr int kKTile = kTileN * kKStride;
+constexpr int kVTile = kTileN * kVStride;
+
+struct PrefillParams {
+  const uint16_t* q;
+  int64_t q_ts, q_hs;
+  const uint16_t* k_cache;
+  const uint16_t* v_cache;
+  int32_t num_pages, page_size;
+  int64_t page_stride, slot_stride, head_stride;
+  const int32_t* block_tables;
+  int64_t bt_stride;
+  int32_t pages_per_seq;
+  const int32_t* cu_q;
+  const int32_t* cu_k;  // may be null
+  const int32_t* positions;
+  int32_t batch, num_tokens, num_heads, num_kv_heads, group, tile_tokens, n_qtiles, max_seqlen_q;
+  float logit_scale;  // scale*log2e (soft cap off) or scale
+  float soft_cap;
+  uint16_t* out;
+  int64_t o_ts, o_hs;
+};
+
+typedef s16x4 __attribute__((address_space(3))) * lds_s16x4_ptr;
+
+// Transposing 8-byte LDS read (ds_read_b64_tr_b16).  `lds` must point into
+// __shared__ memory; the cast is an address-space cast, not a reinterpretation.
+__device__ __forceinline__ s16x4 ds_read_tr16(const uint16_t* lds) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(lds));
+}
+
+__global__ void __launch_bounds__(256)
+prefill_kernel(PrefillParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kKTile];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][kVTile];
+  __shared__ int red_max[4], red_min[4];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int hkv = p.num_kv_heads;
+  const int kvh = blockIdx.x % hkv;
+  const int rest = blockIdx.x / hkv;
+  const int b = rest % p.batch;
+  const int qt = p.n_qtiles - 1 - rest / p.batch;
+
+  const int q0 = p.cu_q[b];
+  const int lq = p.cu_q[b + 1] - q0;
+  // rows past max_seqlen_q are left to the zero pass; rows past the token
+  // count (malformed cu_seqlens) are never touched
+  const int lq_rows = (q0 < 0 || q0 >= p.num_tokens) ? 0 : min(min(lq, p.max_seqlen_q), p.num_tokens - q0);
+  const int tok0 = qt * p.tile_tokens;
+  if (tok0 >= lq_rows) return;  // uniform across the workgroup
+  // kv lengths past the block table's span are clamped to it
+  const int lk = min(p.cu_k ? p.cu_k[b + 1] - p.cu_k[b] : lq, p.pages_per_seq * p.page_size);
+  const int kv_pos_off = p.positions[q0] - (lk - lq);
+
+  // ---- this lane's row
+  const int n = lane & 31;
+  const int h = lane >> 5;
+  const int row = wave * 32 + n;
+  const int rtok = tok0 + row / p.group;
+  const int rhead = row % p.group;
+  const bool row_ok = row < p.tile_tokens * p.group && rtok < lq_rows;
+  const int qpos = row_ok ? p.positions[q0 + rtok] : 0;
+
+  // ---- q tile position range -> kv tile range
+  {
+    int mx = row_ok ? qpos : INT_MIN;
+    int mn = row_ok ? qpos : INT_MAX;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      mx = max(mx, __shfl_xor(mx, o));
+      mn = min(mn, __shfl_xor(mn, o));
+    }
+    if (lane == 0) {
+      red_max[wave] = mx;
+      red_min[wave] = mn;
+    }
+  }
+
+  // Q^T operand (B of S^T): k-step ks covers d = 16ks + 8h .. +8.
+  bf16x8 qt_op[8];
+  {
+    const uint16_t* qrow = p.q + (int64_t)(q0 + (row_ok ? rtok : 0)) * p.q_ts +
+                           (int64_t)(kvh * p.group + rhead) * p.q_hs + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+      qt_op[ks] = as_bf16x8(row_ok ? ld16(qrow + 16 * ks) : u32x4{0, 0, 0, 0});
+  }
+  __syncthreads();
+  const int qpos_max = max(max(red_max[0], red_max[1]), max(red_max[2], red_max[3]));
+  const int qpos_min = min(min(red_min[0], red_min[1]), min(red_min[2], red_min[3]));
+  // kv index j is visible to some row iff j < lk and j + kv_pos_off <= qpos_max
+  const int64_t kv_hi64 = min((int64_t)lk, (int64_t)qpos_max - kv_pos_off + 1);
+  const int kv_hi = kv_hi64 < 0 ? 0 : (int)kv_hi64;
+  const int n_tiles = (kv_hi + kTileN - 1) / kTileN;
+
+  // ---- cooperative tile loader: thread -> (token tid/16 + 16i, chunk tid%16)
+  const int ld_chunk = tid & 15;
+  const int ld_tok = tid >> 4;
+  const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
+  const int64_t head_off = (int64_t)kvh * p.head_stride + 8 * ld_chunk;
+  u32x4 kr[4], vr[4];
+  auto load_tile = [&](int j0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = j0 + ld_tok + 16 * i;
+      if (j < lk) {
+        const int lp = j / p.page_size;
+        const int32_t page = safe_page(bt_row, lp, p.num_pages);
+        const int64_t off = (int64_t)page * p.page_stride + (int64_t)(j - lp * p.page_size) * p.slot_stride + head_off;
+        kr[i] = ld16(p.k_cache + off);
+        vr[i] = ld16(p.v_cache + off);
+      } else {
+        kr[i] = u32x4{0, 0, 0, 0};
+        vr[i] = u32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = ld_tok + 16 * i;
+      *reinterpret_cast<u32x4*>(&k_lds[buf][t * kKStride + 8 * ld_chunk]) = kr[i];
+      *reinterpret_cast<u32x4*>(&v_lds[buf][t * kVStride + 8 * ld_chunk]) = vr[i];
+    }
+  };
+
+  f32x16 acc_o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc_o[dt][i] = 0.f;
+  float m_run = -1e30f;
+  float l_run = 0.f;
+
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  // ds_read_tr16 addressing of the V^T operand (see header comment):
+  // lane = 16*gamma + s; reads row (tokbase + 4h + s/4 [+8]), column
+  // 32dt + 16(gamma%2) + 4(s%4).
+  const int tr_s = lane & 15;
+  const int tr_gamma = lane >> 4;
+  const int tr_row = 4 * h + (tr_s >> 2);
+  const int tr_col = 16 * (tr_gamma & 1) + 4 * (tr_s & 3);
+
+  for (int it = 0; it < n_tiles; ++it) {
+    const int buf = it & 1;
+    const int j0 = it * kTileN;
+    if (it + 1 < n_tiles) load_tile(j0 + kTileN);
+
+    const uint16_t* kt = k_lds[buf];
+    const uint16_t* vt = v_lds[buf];
+
+    // ---- S^T for tokens j0 + 32mt + (0..31)
+    f32x16 s_acc[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s_acc[mt][i] = 0.f;
+      const uint16_t* krow = kt + (32 * mt + n) * kKStride + 8 * h;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(krow + 16 * ks));
+        s_acc[mt] = mfma32(a, qt_op[ks], s_acc[mt]);
+      }
+    }
+
+    // ---- logits, mask, online softmax (row n = lane % 32)
+    // s_acc[mt][i] = S[row n][token j0 + 32mt + 8(i/4) + 4h + i%4]
+    const bool need_mask = (j0 + kTileN > lk) || (j0 + kTileN - 1 + kv_pos_off > qpos_min);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float v = s_acc[mt][i];
+        if (p.soft_cap > 0.f) v = p.soft_cap * tanhf(v * p.logit_scale / p.soft_cap) * kLog2e;
+        else v = v * p.logit_scale;
+        if (need_mask) {
+          const int j = j0 + 32 * mt + 8 * (i >> 2) + 4 * h + (i & 3);
+          const bool vis = j < lk && j + kv_pos_off <= qpos;
+          v = vis ? v : -INFINITY;
+        }
+        s_acc[mt][i] = v;
+        mx = fmaxf(mx, v);
+      }
+    mx = max_xor32(mx);
+    const float m_new = fmaxf(m_run, mx);
+    const float corr = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    float psum = 0.f;
+    bf16x8 pt[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int mt = u >> 1;
+      const int base = 8 * (u & 1);
+      u32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = fast_exp2(s_acc[mt][base + 2 * e] - m_new);
+        const float c = fast_exp2(s_acc[mt][base + 2 * e + 1] - m_new);
+        psum += a + c;
+        w[e] = pack_bf16x2(a, c);
+      }
+      pt[u] = as_bf16x8(w);
+    }
+    l_run = l_run * corr + psum;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc_o[dt] = acc_o[dt] * corr;
+
+    // ---- O^T += V^T . P^T ; k-step u covers tokens 32(u/2) + 16(u%2) + {4h + r, 8 + 4h + r}
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int tokbase = 32 * (u >> 1) + 16 * (u & 1);
+      const uint16_t* r0 = vt + (tokbase + tr_row) * kVStride + tr_col;
+      const uint16_t* r1 = r0 + 8 * kVStride;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const s16x4 lo = ds_read_tr16(r0 + 32 * dt);
+        const s16x4 hi = ds_read_tr16(r1 + 32 * dt);
+        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
+        const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
+        const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
+        acc_o[dt] = mfma32(as_bf16x8(a), pt[u], acc_o[dt]);
+      }
+    }
+
+    if (it + 1 < n_tiles) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: row n = (token rtok, head rhead); acc_o[dt][i] holds
+  // d = 32dt + 8(i/4) + 4h + i%4
+  l_run = sum_xor32(l_run);
+  if (row_ok) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    uint16_t* orow = p.out + (int64_t)(q0 + rtok) * p.o_ts + (int64_t)(kvh * p.group + rhead) * p.o_hs + 4 * h;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        u32x2 w;
+        w[0] = pack_bf16x2(acc_o[dt][4 * i4] * inv, acc_o[dt][4 * i4 + 1] * inv);
+        w[1] = pack_bf16x2(acc_o[dt][4 * i4 + 2] * inv, acc_o[dt][4 * i4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4) = w;
+      }
+  }
+}
+
+// Zero every output row the prefill kernel does not write: rows outside all
+// sequences (before cu_q[0], from cu_q[batch] on) and rows at offset >=
+// max_seqlen_q inside their sequence (the reference drops those too: its
+// scatter only covers the first max_seqlen_bucket rows, prefill...:384-388).
+// One wave per token row.
+__global__ void __launch_bounds__(256)
+prefill_zero_rows_kernel(const int32_t* __restrict__ cu_q, int32_t batch, int32_t num_tokens,
+                         int32_t max_seqlen_q, int32_t num_heads, uint16_t* __restrict__ out,
+                         int64_t o_ts, int64_t o_hs) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= num_tokens) return;
+  bool covered = false;
+  if (t >= cu_q[0] && t < cu_q[batch]) {
+    // last b with cu_q[b] <= t
+    int lo = 0, hi = batch;  // invariant: cu_q[lo] <= t < cu_q[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (cu_q[mid] <= t) lo = mid;
+      else hi = mid;
+    }
+    covered = t - cu_q[lo] < max_seqlen_q;
+  }
+  if (covered) return;
+  const int chunks_per_head = kPHeadDim / 8;
+  for (int c = lane; c < num_heads * chunks_per_head; c += 64) {
+    const int hh = c / chunks_per_head;
+    const int e = (c - hh * chunks_per_head) * 8;
+    st16(out + t * o_ts + hh * o_hs + e, u32x4{0, 0, 0, 0});
+  }
+}
+
+}  // namespace pa
+
+using namespace pa;
+
+extern "C" int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                          const uint16_t* k_cache, const uint16_t* v_cache,
+                          int32_t num_pages, int32_t page_size,
+                          int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                          const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                          const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                          const int32_t* input_positions,
+                          int32_t batch, int32_t num_tokens, int32_t max_seqlen_q,
+                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                          float scale, float soft_cap,
+                          uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
+                          void* stream) {
+  if (batch < 0 || num_tokens < 0 || max_seqlen_q < 0 || num_heads <= 0 || num_kv_heads <= 0 ||
+      num_pages <= 0 || page_size <= 0 || pages_per_seq < 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "pa_prefill: bad sizes (batch=%d, num_tokens=%d, max_seqlen_q=%d, num_heads=%d, "
+                "num_kv_heads=%d, num_pages=%d, page_size=%d, pages_per_seq=%d)",
+                batch, num_tokens, max_seqlen_q, num_heads, num_kv_heads, num_pages, page_size,
+                pages_per_seq);
+  if (num_heads % num_kv_heads != 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "pa_prefill: Number of Q heads must be divisible by number of KV heads. Got %d and %d.",
+                num_heads, num_kv_heads);
+  if (head_dim != kPHeadDim)
+    return fail(PA_ERR_UNSUPPORTED, "pa_prefill: head_dim %d not supported (only %d)", head_dim, kPHeadDim);
+  const int group = num_heads / num_kv_heads;
+  if (group > kRows)
+    return fail(PA_ERR_UNSUPPORTED, "pa_prefill: %d q heads per kv head not supported (max %d)", group, kRows);
+  if (num_tokens == 0) return PA_OK;
+  if (!q || !out || !cu_seqlens_q || !input_positions || (batch > 0 && (!k_cache || !v_cache || !block_tables)))
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_prefill: null pointer");
+  const uintptr_t align_bits = (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out;
+  if ((align_bits & 15u) || (q_tok_stride | q_head_stride | page_stride | slot_stride | head_stride |
+                             out_tok_stride | out_head_stride) % 8)
+    return fail(PA_ERR_UNSUPPORTED, "pa_prefill: operands must be 16-byte aligned with strides multiple of 8");
+  hipStream_t s = (hipStream_t)stream;
+
+  {
+    prefill_zero_rows_kernel<<<dim3((unsigned)((num_tokens + 3) / 4)), dim3(256), 0, s>>>(
+        cu_seqlens_q, batch, num_tokens, max_seqlen_q, num_heads, out, out_tok_stride, out_head_stride);
+    int rc = launch_status("pa_prefill(zero rows)");
+    if (rc) return rc;
+  }
+  if (batch == 0 || max_seqlen_q == 0) return PA_OK;
+
+  PrefillParams prm;
+  prm.q = q;
+  prm.q_ts = q_tok_stride;
+  prm.q_hs = q_head_stride;
+  prm.k_cache = k_cache;
+  prm.v_cache = v_cache;
+  prm.num_pages = num_pages;
+  prm.page_size = page_size;
+  prm.page_stride = page_stride;
+  prm.slot_stride = slot_stride;
+  prm.head_stride = head_stride;
+  prm.block_tables = block_tables;
+  prm.bt_stride = bt_stride;
+  prm.pages_per_seq = pages_per_seq;
+  prm.cu_q = cu_seqlens_q;
+  prm.cu_k = cu_seqlens_k;
+  prm.positions = input_positions;
+  prm.batch = batch;
+  prm.num_tokens = num_tokens;
+  prm.num_heads = num_heads;
+  prm.num_kv_heads = num_kv_heads;
+  prm.group = group;
+  prm.tile_tokens = kRows / group;
+  prm.n_qtiles = (max_seqlen_q + prm.tile_tokens - 1) / prm.tile_tokens;
+  prm.max_seqlen_q = max_seqlen_q;
+  prm.soft_cap = soft_cap > 0.f ? soft_cap : 0.f;
+  prm.logit_scale = prm.soft_cap > 0.f ? scale : scale * kLog2e;
+  prm.out = out;
+  prm.o_ts = out_tok_stride;
+  prm.o_hs = out_head_stride;
+  const int64_t blocks = (int64_t)prm.n_qtiles * batch * num_kv_heads;
+  if (blocks > 0x7fffffff)
+    return fail(PA_ERR_UNSUPPORTED, "pa_prefill: grid of %lld workgroups too large", (long long)blocks);
+  prefill_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(prm);
+  return launch_status("pa_prefill");
+}
