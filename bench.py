@@ -1,0 +1,281 @@
+"""Benchmark of the gfx950 paged-attention path on one MI355X.
+
+Default run (``python bench.py``): one step = one pass of each headline
+workload, inputs resident in HBM:
+
+* Qwen3-32B long-context ragged prefill (8 sequences, L ~ U[8192, 32768],
+  64 q / 8 kv heads, head_dim 128, 256-token pages, seed 4):
+  KV store of all new tokens + causal GQA paged prefill.
+  ``value`` = algorithmic prefill TFLOP/s (causal-visible pairs only).
+* Qwen3-8B decode (256 sequences, ctx ~ U[512, 8192], 32 q / 8 kv heads,
+  16384-page pool, seed 2): KV store of the new token + split-K decode.
+  Reported under ``"decode"`` in GB/s of algorithmic HBM traffic.
+
+Prints ONE JSON line.  ``roofline`` (prefill, MFMA-bound) and
+``decode.roofline`` (HBM-bound) use the average duration of the attention
+call measured with HIP events on the launch stream.  ``cpu_baseline`` times
+the CPU oracle on a bounded sample of the same workload (rank 0 only).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
+METRIC = "prefill attn TFLOP/s (% bf16 MFMA peak); decode attn GB/s (% HBM peak)"
+
+
+def _load_traffic():
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE,
+    scaled by a copy-kernel calibration), committed under profiles/."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return {}
+    with open(path) as f:
+        return json.load(f)
+
+
+def _events(torch, n):
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+
+
+def run_gpu(args):
+    import torch
+    import __graft_entry__ as ge
+    pkg = ge.load_package()
+    import vllm_jax_amd.workloads as wl
+
+    pkg._lib.load()  # fail loudly if the HIP library is missing
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    # ---------------- prefill: Qwen3-32B long context
+    pb = wl.qwen3_32b_long_prefill(seed=4)
+    pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False)
+    kv_p = pt["kv_cache"]
+    kp_p, vp_p = kv_p[0].permute(2, 0, 1, 3), kv_p[1].permute(2, 0, 1, 3)
+    out_p = torch.empty_like(pt["q"])
+
+    def prefill_step():
+        pkg.update_kv_cache(kv_p, pt["slot_mapping"], pt["k"], pt["v"])
+
+    def prefill_attn():
+        pkg.prefill_paged_attention(pt["q"], kp_p, vp_p, pt["block_tables"], pt["cu_seqlens_q"],
+                                    pt["slot_mapping"], pt["input_positions"],
+                                    max_seqlen_bucket=pb.max_seqlen_bucket, out=out_p)
+
+    # ---------------- decode: Qwen3-8B
+    db = wl.qwen3_8b_decode(seed=2)
+    dt_ = wl.materialize_decode(db, seed=2, device=dev)
+    kv_d = dt_["kv_cache"]
+    kp_d, vp_d = kv_d[0].permute(2, 0, 1, 3), kv_d[1].permute(2, 0, 1, 3)
+    out_d = torch.empty_like(dt_["q"])
+    from vllm_jax_amd.kernels.decode_paged_attention import decode_workspace_bytes
+    ws = torch.empty(decode_workspace_bytes(db.batch, db.num_heads, db.head_dim, db.block_tables.shape[1],
+                                            db.page_size), dtype=torch.uint8, device=dev)
+    dscale = 1.0 / 11.3125  # 1/bf16(sqrt(128)), folded into the kernel
+
+    def decode_step():
+        pkg.update_kv_cache(kv_d, dt_["slot_mapping"], dt_["k"], dt_["v"])
+
+    def decode_attn():
+        pkg.decode_paged_attention(dt_["q"], kp_d, vp_d, dt_["block_tables"], dt_["context_lens"],
+                                   scale=dscale, workspace=ws, out=out_d)
+
+    for _ in range(args.warmup):
+        prefill_step(); prefill_attn(); decode_step(); decode_attn()
+    torch.cuda.synchronize()
+
+    k = args.steps
+    ev = [_events(torch, 6) for _ in range(k)]
+    t_begin, t_end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    t_begin.record()
+    for i in range(k):
+        e = ev[i]
+        e[0].record(); prefill_step(); e[1].record(); prefill_attn(); e[2].record()
+        decode_step(); e[3].record(); decode_attn(); e[4].record()
+    t_end.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+
+    total_ms = t_begin.elapsed_time(t_end)
+    p_store = np.array([e[0].elapsed_time(e[1]) for e in ev])
+    p_attn = np.array([e[1].elapsed_time(e[2]) for e in ev])
+    d_store = np.array([e[2].elapsed_time(e[3]) for e in ev])
+    d_attn = np.array([e[3].elapsed_time(e[4]) for e in ev])
+
+    p_flops = pb.flops()
+    d_bytes = db.hbm_bytes()
+    prefill_step_ms = float((p_store + p_attn).mean())
+    decode_step_ms = float((d_store + d_attn).mean())
+    p_tflops_step = p_flops / (prefill_step_ms * 1e-3) / 1e12
+    p_tflops_kernel = p_flops / (float(p_attn.mean()) * 1e-3) / 1e12
+    d_gbs_step = d_bytes / (decode_step_ms * 1e-3) / 1e9
+    d_gbs_kernel = d_bytes / (float(d_attn.mean()) * 1e-3) / 1e9
+
+    traffic = _load_traffic()
+    res = {
+        "metric": METRIC,
+        "value": round(p_tflops_step, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": k,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_ms / k, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (0.5*N(0,1) bf16 q/k/v, seeded block-table permutations)",
+        "config": {
+            "workload": "qwen3_32b_long_prefill (seed 4) + qwen3_8b_decode (seed 2)",
+            "prefill": {"seqs": int(pb.batch), "q_lens": [int(x) for x in pb.q_lens], "num_heads": 64,
+                        "num_kv_heads": 8, "head_dim": 128, "page_size": 256, "tokens": pb.num_tokens,
+                        "algorithmic_tflop": round(p_flops / 1e12, 4)},
+            "decode": {"seqs": int(db.batch), "num_heads": 32, "num_kv_heads": 8, "head_dim": 128,
+                       "page_size": 256, "pool_pages": db.num_pages,
+                       "context_tokens": int(db.context_lens.sum()),
+                       "algorithmic_gb": round(d_bytes / 1e9, 4)},
+            "parallelism": "single GPU",
+        },
+        "prefill": {
+            "step_ms": round(prefill_step_ms, 4),
+            "kv_store_ms": round(float(p_store.mean()), 4),
+            "attn_ms": round(float(p_attn.mean()), 4),
+            "attn_tflops": round(p_tflops_kernel, 2),
+            "frac_of_mfma_peak": round(p_tflops_kernel / MFMA_BF16_PEAK_TFLOPS, 4),
+        },
+        "roofline": {
+            "kernel": "prefill_kernel",
+            "bound": "mfma",
+            "achieved": round(p_tflops_kernel, 2),
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(p_tflops_kernel / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": traffic.get("prefill_kernel"),
+        },
+        "decode": {
+            "metric": "decode attn GB/s",
+            "value": round(d_gbs_step, 1),
+            "unit": "GB/s",
+            "step_ms": round(decode_step_ms, 4),
+            "kv_store_ms": round(float(d_store.mean()), 4),
+            "attn_ms": round(float(d_attn.mean()), 4),
+            "roofline": {
+                "kernel": "decode_split_kernel + decode_merge_kernel",
+                "bound": "hbm",
+                "achieved": round(d_gbs_kernel, 1),
+                "peak": HBM_PEAK_GBS,
+                "unit": "GB/s",
+                "frac": round(d_gbs_kernel / HBM_PEAK_GBS, 4),
+                "traffic": traffic.get("decode_split_kernel"),
+            },
+        },
+        "wall_s_timed": round(wall, 3),
+    }
+    return res, (pb, pt, db, dt_)
+
+
+def cpu_baseline(pb, pt, db, dt_, budget_s):
+    """Time the CPU oracle on bounded samples of the two workloads (host cores)."""
+    import torch
+    from oracle import paged_attention_oracle as ora
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        threads = 1
+    u16 = lambda x: x.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    # prefill sample: the last R q rows of the shortest sequence, against its whole context
+    b = int(np.argmin(pb.q_lens))
+    q0, q1 = int(pb.cu_seqlens_q[b]), int(pb.cu_seqlens_q[b + 1])
+    n_pages = -(-(q1 - q0) // pb.page_size)
+    blocks = torch.as_tensor(pb.block_tables[b, :n_pages].astype(np.int64), device=pt["q"].device)
+    kv = pt["kv_cache"]
+    kp = u16(kv[0][blocks]).transpose(2, 0, 1, 3)
+    vp = u16(kv[1][blocks]).transpose(2, 0, 1, 3)
+    qh = u16(pt["q"][q0:q1])
+    bt = np.arange(n_pages, dtype=np.int32)[None]
+    cu = np.array([0, q1 - q0], np.int32)
+    pos = pb.input_positions[q0:q1]
+    rows_n, spent, flops = 8, 0.0, 0
+    while True:
+        rows = np.arange(q1 - q0 - rows_n, q1 - q0)
+        t0 = time.perf_counter()
+        ora.prefill_attention(qh, kp, vp, bt, cu, pos, rows=rows)
+        dt = time.perf_counter() - t0
+        if dt * 2.2 > budget_s / 2 or rows_n >= 4096:
+            spent, flops, used_rows = dt, 4 * pb.head_dim * pb.num_heads * int((pos[rows] + 1).sum()), rows_n
+            break
+        rows_n *= 2
+    p_val = flops / spent / 1e12
+
+    # decode sample: the first S sequences
+    s_n, d_spent, d_bytes = 2, 0.0, 0
+    kvd = dt_["kv_cache"]
+    qd = dt_["q"]
+    while True:
+        seqs = np.arange(s_n)
+        used = sorted(set(int(x) for x in db.block_tables[:s_n].ravel() if x >= 0))
+        remap = {blk: i for i, blk in enumerate(used)}
+        bt_s = np.array([[remap.get(int(x), 0) if x >= 0 else -1 for x in row] for row in db.block_tables[:s_n]],
+                        np.int32)
+        idx = torch.as_tensor(used, dtype=torch.long, device=qd.device)
+        kp_s = u16(kvd[0][idx]).transpose(2, 0, 1, 3)
+        vp_s = u16(kvd[1][idx]).transpose(2, 0, 1, 3)
+        qs = u16(qd[:s_n])
+        t0 = time.perf_counter()
+        ora.decode_attention(qs, kp_s, vp_s, bt_s, db.context_lens[:s_n])
+        dt = time.perf_counter() - t0
+        if dt * 2.2 > budget_s / 2 or s_n >= db.batch:
+            d_spent = dt
+            d_bytes = int(db.context_lens[:s_n].sum()) * 2 * db.num_kv_heads * db.head_dim * 2
+            break
+        s_n = min(s_n * 2, db.batch)
+    d_val = d_bytes / d_spent / 1e9
+    ncpu = os.cpu_count()
+    return (
+        {"value": round(p_val, 6), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+         "sample": f"CPU oracle (numpy, {threads} BLAS threads of {ncpu} host CPUs): prefill of the last "
+                   f"{used_rows} q rows of the {q1 - q0}-token sequence against its whole causal context, "
+                   f"{flops / 1e9:.1f} GFLOP in {spent:.1f} s"},
+        {"value": round(d_val, 4), "unit": "GB/s", "cores": int(threads), "kind": "port",
+         "sample": f"CPU oracle decode of the first {s_n} sequences ({d_bytes / 1e9:.3f} GB KV) in {d_spent:.1f} s"},
+    )
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU oracle work (total)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this paged-attention path is built and measured on a single "
+              "MI355X (it would shard over kv heads or sequences with no exchange; see DESIGN.md). "
+              f"--gpus {args.gpus} is not supported.", file=sys.stderr)
+        sys.exit(2)
+    res, ctx = run_gpu(args)
+    if not args.no_cpu_baseline:
+        pcb, dcb = cpu_baseline(*ctx, budget_s=args.cpu_budget)
+        res["cpu_baseline"] = pcb
+        res["decode"]["cpu_baseline"] = dcb
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -83,6 +83,14 @@ __device__ __forceinline__ float sum_xor16(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
+// acc + lo + hi of a packed bf16 pair (v_dot2c_f32_bf16 against (1, 1)).
+__device__ __forceinline__ float dot2_bf16_ones(uint32_t pair, float acc) {
+  const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), ones, acc, false);
+}
+
 // Physical page of logical page `lp` of a sequence: negative ids (padding
 // entries of the block table) read page 0, ids past the pool are clamped so
 // that no access leaves the pool.

@@ -4,18 +4,24 @@
 // a row is a (query token, q head of this kv head) pair: row n of the tile is
 // token n / G, head n % G (G = q heads per kv head).  Packing the G heads into
 // the MFMA dimension makes every K/V tile staged in LDS serve G x tokens rows.
+// Two workgroups share a CU (2 waves per SIMD), so one wave's softmax VALU
+// work overlaps the other's MFMA work.
 //
-// Per 64-token KV tile (double-buffered in LDS, loaded through the block table
-// with 16-byte global loads; tokens past the kv length are zero-filled):
+// Per 64-token KV tile, double-buffered in LDS and filled by direct
+// global->LDS loads (global_load_lds_dwordx4) through the block table:
 //   S^T[t][n] = K[t][:] . Q[n][:]      v_mfma_f32_32x32x16_bf16, K rows read
 //                                       with ds_read_b128, Q^T kept in VGPRs
-//   online softmax per row n            row n = lane % 32, so the row max needs
-//                                       one permlane32 swap and the rescale of
-//                                       O is lane-local
+//   online softmax per row n            row n = lane % 32: the row max needs one
+//                                       permlane32 swap and rescaling O is
+//                                       lane-local; the reference max only
+//                                       moves when a row max grows by more than
+//                                       2^8, so O is rarely rescaled
 //   O^T[d][n] += V^T[d][t] . P^T[t][n]  V^T operand read from the row-major V
-//                                       tile with ds_read_tr16_b64 (gfx950's
-//                                       transposing LDS read), P^T straight
-//                                       from the S^T accumulator registers
+//                                       tile with ds_read_b64_tr_b16 (gfx950's
+//                                       transposing LDS read), P^T straight from
+//                                       the S^T accumulator registers
+// LDS tiles are 64 rows x 256 B with 16-byte chunks XOR-swizzled per row so
+// that both the K reads and the transposing V reads are bank-conflict free.
 // KV tiles entirely above the causal diagonal of the q tile are never loaded;
 // the mask is evaluated only on tiles that straddle it or the kv length.
 // Workgroups are dispatched from the last q tile down so the longest causal
@@ -26,12 +32,10 @@
 namespace pa {
 
 constexpr int kPHeadDim = 128;
-constexpr int kRows = 128;       // rows per workgroup
-constexpr int kTileN = 64;       // kv tokens per tile
-constexpr int kKStride = 136;    // K tile row stride in elements (272 B)
-constexpr int kVStride = 160;    // V tile row stride in elements (320 B)
-constexpr int kKTile = kTileN * kKStride;
-constexpr int kVTile = kTileN * kVStride;
+constexpr int kRows = 128;        // rows per workgroup
+constexpr int kTileN = 64;        // kv tokens per tile
+constexpr int kTileElems = kTileN * kPHeadDim;
+constexpr float kRescaleSlack = 8.f;  // log2 units the running max may lag
 
 struct PrefillParams {
   const uint16_t* q;
@@ -54,6 +58,7 @@ struct PrefillParams {
 };
 
 typedef s16x4 __attribute__((address_space(3))) * lds_s16x4_ptr;
+typedef void __attribute__((address_space(3))) * lds_void_ptr;
 
 // Transposing 8-byte LDS read (ds_read_b64_tr_b16).  `lds` must point into
 // __shared__ memory; the cast is an address-space cast, not a reinterpretation.
@@ -61,10 +66,16 @@ __device__ __forceinline__ s16x4 ds_read_tr16(const uint16_t* lds) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(lds));
 }
 
-__global__ void __launch_bounds__(256)
+// Physical 16-byte chunk of logical chunk c in tile row r.
+__device__ __forceinline__ int swz(int r, int c) {
+  return c ^ (((r & 3) << 2) | ((r >> 2) & 3));
+}
+
+template <bool kSoftCap, bool kAligned>
+__global__ void __launch_bounds__(256, 2)
 prefill_kernel(PrefillParams p) {
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][kKTile];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][kVTile];
+  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2][kTileElems];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2][kTileElems];
   __shared__ int red_max[4], red_min[4];
 
   const int tid = threadIdx.x;
@@ -128,34 +139,52 @@ prefill_kernel(PrefillParams p) {
   const int kv_hi = kv_hi64 < 0 ? 0 : (int)kv_hi64;
   const int n_tiles = (kv_hi + kTileN - 1) / kTileN;
 
-  // ---- cooperative tile loader: thread -> (token tid/16 + 16i, chunk tid%16)
-  const int ld_chunk = tid & 15;
-  const int ld_tok = tid >> 4;
+  // ---- direct global->LDS tile loader.  Wave w fills 1 KiB blocks 4w..4w+3
+  // of each tile (rows 4blk .. 4blk+3); lane l writes LDS bytes 16*l of the
+  // block, i.e. row 4blk + l/16, physical chunk l%16, so it loads the logical
+  // chunk swz(row, l%16) of that token.
   const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
-  const int64_t head_off = (int64_t)kvh * p.head_stride + 8 * ld_chunk;
-  u32x4 kr[4], vr[4];
-  auto load_tile = [&](int j0) {
+  const int ld_r = lane >> 4;            // row within a 1 KiB block
+  const int ld_p = lane & 15;            // physical chunk
+  const int64_t head_off = (int64_t)kvh * p.head_stride;
+  auto issue_tile = [&](int j0, int buf) {
+    // All addresses first, then the loads: a block-table read queued behind
+    // the LDS-DMA loads would make the compiler wait for all of them.
+    int64_t off[4];
+    if constexpr (kAligned) {
+      // page_size % 64 == 0: the whole tile lies in one page (one scalar load)
+      const int lp = j0 / p.page_size;
+      const int32_t page = safe_page(bt_row, lp, p.num_pages);
+      const int64_t pbase = (int64_t)page * p.page_stride + (int64_t)(j0 - lp * p.page_size) * p.slot_stride + head_off;
+      const int last = lk - 1 - j0;  // clamp onto a valid token: masked, never stale
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = j0 + ld_tok + 16 * i;
-      if (j < lk) {
-        const int lp = j / p.page_size;
-        const int32_t page = safe_page(bt_row, lp, p.num_pages);
-        const int64_t off = (int64_t)page * p.page_stride + (int64_t)(j - lp * p.page_size) * p.slot_stride + head_off;
-        kr[i] = ld16(p.k_cache + off);
-        vr[i] = ld16(p.v_cache + off);
-      } else {
-        kr[i] = u32x4{0, 0, 0, 0};
-        vr[i] = u32x4{0, 0, 0, 0};
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * (4 * wave + i) + ld_r;
+        off[i] = pbase + (int64_t)min(r, last) * p.slot_stride + 8 * swz(r, ld_p);
+      }
+    } else {
+      int32_t pages[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * (4 * wave + i) + ld_r;
+        const int j = min(j0 + r, lk - 1);
+        pages[i] = safe_page(bt_row, j / p.page_size, p.num_pages);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 4 * (4 * wave + i) + ld_r;
+        const int j = min(j0 + r, lk - 1);
+        off[i] = (int64_t)pages[i] * p.page_stride + (int64_t)(j % p.page_size) * p.slot_stride + head_off +
+                 8 * swz(r, ld_p);
       }
     }
-  };
-  auto store_tile = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int t = ld_tok + 16 * i;
-      *reinterpret_cast<u32x4*>(&k_lds[buf][t * kKStride + 8 * ld_chunk]) = kr[i];
-      *reinterpret_cast<u32x4*>(&v_lds[buf][t * kVStride + 8 * ld_chunk]) = vr[i];
+      const int blk = 4 * wave + i;
+      __builtin_amdgcn_global_load_lds((const void*)(p.k_cache + off[i]),
+                                       (lds_void_ptr)(&k_lds[buf][blk * 512]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const void*)(p.v_cache + off[i]),
+                                       (lds_void_ptr)(&v_lds[buf][blk * 512]), 16, 0, 0);
     }
   };
 
@@ -164,27 +193,24 @@ prefill_kernel(PrefillParams p) {
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc_o[dt][i] = 0.f;
-  float m_run = -1e30f;
+  float m_ref = -1e30f;  // reference max (log2 units) of the accumulators
   float l_run = 0.f;
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
+  if (n_tiles > 0) issue_tile(0, 0);
+  __syncthreads();  // waits for the loads (vmcnt) before the barrier
 
-  // ds_read_tr16 addressing of the V^T operand (see header comment):
-  // lane = 16*gamma + s; reads row (tokbase + 4h + s/4 [+8]), column
-  // 32dt + 16(gamma%2) + 4(s%4).
+  // ds_read_tr16 addressing of the V^T operand: lane = 16*gamma + s reads
+  // row (tokbase + 4h + s/4 [+8]), logical column 32dt + 16(gamma%2) + 4(s%4).
   const int tr_s = lane & 15;
   const int tr_gamma = lane >> 4;
   const int tr_row = 4 * h + (tr_s >> 2);
   const int tr_col = 16 * (tr_gamma & 1) + 4 * (tr_s & 3);
+  const float c_log2 = p.logit_scale;
 
   for (int it = 0; it < n_tiles; ++it) {
     const int buf = it & 1;
     const int j0 = it * kTileN;
-    if (it + 1 < n_tiles) load_tile(j0 + kTileN);
+    if (it + 1 < n_tiles) issue_tile(j0 + kTileN, buf ^ 1);
 
     const uint16_t* kt = k_lds[buf];
     const uint16_t* vt = v_lds[buf];
@@ -195,38 +221,51 @@ prefill_kernel(PrefillParams p) {
     for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) s_acc[mt][i] = 0.f;
-      const uint16_t* krow = kt + (32 * mt + n) * kKStride + 8 * h;
+      const int r = 32 * mt + n;
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
-        const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(krow + 16 * ks));
+        const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(kt + r * kPHeadDim + 8 * swz(r, 2 * ks + h)));
         s_acc[mt] = mfma32(a, qt_op[ks], s_acc[mt]);
       }
     }
 
-    // ---- logits, mask, online softmax (row n = lane % 32)
+    // ---- logits (log2 units), mask, online softmax for row n = lane % 32.
     // s_acc[mt][i] = S[row n][token j0 + 32mt + 8(i/4) + 4h + i%4]
+    if constexpr (kSoftCap) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          s_acc[mt][i] = p.soft_cap * kLog2e * tanhf(s_acc[mt][i] * p.logit_scale / p.soft_cap);
+    }
+    const float cs = kSoftCap ? 1.f : c_log2;  // multiplier applied inside the exponent
     const bool need_mask = (j0 + kTileN > lk) || (j0 + kTileN - 1 + kv_pos_off > qpos_min);
+    if (need_mask) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int j = j0 + 32 * mt + 8 * (i >> 2) + 4 * h + (i & 3);
+          const bool vis = j < lk && j + kv_pos_off <= qpos;
+          s_acc[mt][i] = vis ? s_acc[mt][i] : -INFINITY;
+        }
+    }
     float mx = -INFINITY;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float v = s_acc[mt][i];
-        if (p.soft_cap > 0.f) v = p.soft_cap * tanhf(v * p.logit_scale / p.soft_cap) * kLog2e;
-        else v = v * p.logit_scale;
-        if (need_mask) {
-          const int j = j0 + 32 * mt + 8 * (i >> 2) + 4 * h + (i & 3);
-          const bool vis = j < lk && j + kv_pos_off <= qpos;
-          v = vis ? v : -INFINITY;
-        }
-        s_acc[mt][i] = v;
-        mx = fmaxf(mx, v);
-      }
-    mx = max_xor32(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float corr = fast_exp2(m_run - m_new);
-    m_run = m_new;
-    float psum = 0.f;
+      for (int i = 0; i < 16; i += 2) mx = fmaxf(mx, fmaxf(s_acc[mt][i], s_acc[mt][i + 1]));
+    mx = max_xor32(mx) * cs;
+    // Move the reference max only when this tile's max exceeds it by more
+    // than the slack (any lane in the wave): exponents stay <= 2^slack.
+    if (__any(mx > m_ref + kRescaleSlack)) {
+      const float m_new = fmaxf(m_ref, mx);
+      const float corr = fast_exp2(m_ref - m_new);
+      m_ref = m_new;
+      l_run *= corr;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) acc_o[dt] = acc_o[dt] * corr;
+    }
     bf16x8 pt[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -235,27 +274,25 @@ prefill_kernel(PrefillParams p) {
       u32x4 w;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float a = fast_exp2(s_acc[mt][base + 2 * e] - m_new);
-        const float c = fast_exp2(s_acc[mt][base + 2 * e + 1] - m_new);
-        psum += a + c;
+        const float a = fast_exp2(__builtin_fmaf(s_acc[mt][base + 2 * e], cs, -m_ref));
+        const float c = fast_exp2(__builtin_fmaf(s_acc[mt][base + 2 * e + 1], cs, -m_ref));
         w[e] = pack_bf16x2(a, c);
       }
       pt[u] = as_bf16x8(w);
-    }
-    l_run = l_run * corr + psum;
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) acc_o[dt] = acc_o[dt] * corr;
+      for (int e = 0; e < 4; ++e) l_run = dot2_bf16_ones(w[e], l_run);
+    }
 
     // ---- O^T += V^T . P^T ; k-step u covers tokens 32(u/2) + 16(u%2) + {4h + r, 8 + 4h + r}
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int tokbase = 32 * (u >> 1) + 16 * (u & 1);
-      const uint16_t* r0 = vt + (tokbase + tr_row) * kVStride + tr_col;
-      const uint16_t* r1 = r0 + 8 * kVStride;
+      const int r0 = 32 * (u >> 1) + 16 * (u & 1) + tr_row;
+      const int r1 = r0 + 8;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const s16x4 lo = ds_read_tr16(r0 + 32 * dt);
-        const s16x4 hi = ds_read_tr16(r1 + 32 * dt);
+        const int col = 32 * dt + tr_col;  // logical column; chunk col/8, half (col%8)/4
+        const s16x4 lo = ds_read_tr16(vt + r0 * kPHeadDim + 8 * swz(r0, col >> 3) + (col & 7));
+        const s16x4 hi = ds_read_tr16(vt + r1 * kPHeadDim + 8 * swz(r1, col >> 3) + (col & 7));
         const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
         const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
         const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
@@ -263,8 +300,7 @@ prefill_kernel(PrefillParams p) {
       }
     }
 
-    if (it + 1 < n_tiles) store_tile(buf ^ 1);
-    __syncthreads();
+    __syncthreads();  // next tile landed (vmcnt) and everyone is done with this one
   }
 
   // ---- epilogue: row n = (token rtok, head rhead); acc_o[dt][i] holds
@@ -399,6 +435,13 @@ extern "C" int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_hea
   const int64_t blocks = (int64_t)prm.n_qtiles * batch * num_kv_heads;
   if (blocks > 0x7fffffff)
     return fail(PA_ERR_UNSUPPORTED, "pa_prefill: grid of %lld workgroups too large", (long long)blocks);
-  prefill_kernel<<<dim3((unsigned)blocks), dim3(256), 0, s>>>(prm);
+  const bool aligned = page_size % kTileN == 0;
+  if (prm.soft_cap > 0.f) {
+    if (aligned) prefill_kernel<true, true><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(prm);
+    else prefill_kernel<true, false><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(prm);
+  } else {
+    if (aligned) prefill_kernel<false, true><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(prm);
+    else prefill_kernel<false, false><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(prm);
+  }
   return launch_status("pa_prefill");
 }
