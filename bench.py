@@ -48,6 +48,28 @@ def _events(torch, n):
     return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
 
 
+def run_copy(args):
+    """A plain 1 GiB device-to-device copy, K times: the calibration kernel for
+    the FETCH_SIZE / WRITE_SIZE counters (1 GiB read + 1 GiB written per launch)."""
+    import torch
+    dev = torch.device("cuda:0")
+    src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    return {"metric": "device copy GB/s (calibration)", "value": round(2 * src.numel() * 2 / ms / 1e6, 1),
+            "unit": "GB/s", "bytes_read_per_launch": src.numel() * 2, "bytes_written_per_launch": src.numel() * 2,
+            "ms_per_step": round(ms, 4), "steps": args.steps}
+
+
 def run_gpu(args):
     import torch
     import __graft_entry__ as ge
@@ -60,7 +82,10 @@ def run_gpu(args):
 
     # ---------------- prefill: Qwen3-32B long context
     pb = wl.qwen3_32b_long_prefill(seed=4)
-    pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False)
+    pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False) if args.only != "decode" else None
+    if pt is None:  # decode-only profiling run: keep the prefill half tiny
+        pb = wl.make_prefill([64], num_heads=64, num_kv_heads=8, rng=np.random.default_rng(0))
+        pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False)
     kv_p = pt["kv_cache"]
     kp_p, vp_p = kv_p[0].permute(2, 0, 1, 3), kv_p[1].permute(2, 0, 1, 3)
     out_p = torch.empty_like(pt["q"])
@@ -74,7 +99,8 @@ def run_gpu(args):
                                     max_seqlen_bucket=pb.max_seqlen_bucket, out=out_p)
 
     # ---------------- decode: Qwen3-8B
-    db = wl.qwen3_8b_decode(seed=2)
+    db = wl.qwen3_8b_decode(seed=2) if args.only != "prefill" else \
+        wl.make_decode([64], num_heads=32, num_kv_heads=8, rng=np.random.default_rng(0))
     dt_ = wl.materialize_decode(db, seed=2, device=dev)
     kv_d = dt_["kv_cache"]
     kp_d, vp_d = kv_d[0].permute(2, 0, 1, 3), kv_d[1].permute(2, 0, 1, 3)
@@ -91,6 +117,13 @@ def run_gpu(args):
         pkg.decode_paged_attention(dt_["q"], kp_d, vp_d, dt_["block_tables"], dt_["context_lens"],
                                    scale=dscale, workspace=ws, out=out_d)
 
+    run_p = args.only in (None, "prefill")
+    run_d = args.only in (None, "decode")
+    nop = lambda: None
+    if not run_p:
+        prefill_step = prefill_attn = nop
+    if not run_d:
+        decode_step = decode_attn = nop
     for _ in range(args.warmup):
         prefill_step(); prefill_attn(); decode_step(); decode_attn()
     torch.cuda.synchronize()
@@ -119,10 +152,11 @@ def run_gpu(args):
     d_bytes = db.hbm_bytes()
     prefill_step_ms = float((p_store + p_attn).mean())
     decode_step_ms = float((d_store + d_attn).mean())
-    p_tflops_step = p_flops / (prefill_step_ms * 1e-3) / 1e12
-    p_tflops_kernel = p_flops / (float(p_attn.mean()) * 1e-3) / 1e12
-    d_gbs_step = d_bytes / (decode_step_ms * 1e-3) / 1e9
-    d_gbs_kernel = d_bytes / (float(d_attn.mean()) * 1e-3) / 1e9
+    rate = lambda work, ms, unit: work / (ms * 1e-3) / unit if ms > 0 else 0.0
+    p_tflops_step = rate(p_flops, prefill_step_ms, 1e12)
+    p_tflops_kernel = rate(p_flops, float(p_attn.mean()), 1e12)
+    d_gbs_step = rate(d_bytes, decode_step_ms, 1e9)
+    d_gbs_kernel = rate(d_bytes, float(d_attn.mean()), 1e9)
 
     traffic = _load_traffic()
     res = {
@@ -263,14 +297,21 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU oracle work (total)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["prefill", "decode", "copy"], default=None,
+                    help="profiling aid: run one kernel family only (the JSON line then covers that part)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this paged-attention path is built and measured on a single "
               "MI355X (it would shard over kv heads or sequences with no exchange; see DESIGN.md). "
               f"--gpus {args.gpus} is not supported.", file=sys.stderr)
         sys.exit(2)
+    if args.only == "copy":
+        print(json.dumps(run_copy(args)), flush=True)
+        return
     res, ctx = run_gpu(args)
-    if not args.no_cpu_baseline:
+    if args.only is not None:
+        res["only"] = args.only
+    if not args.no_cpu_baseline and args.only is None:
         pcb, dcb = cpu_baseline(*ctx, budget_s=args.cpu_budget)
         res["cpu_baseline"] = pcb
         res["decode"]["cpu_baseline"] = dcb

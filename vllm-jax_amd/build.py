@@ -21,8 +21,11 @@ ARCH = "gfx950"
 SOURCES = ["pa_errors.cpp", "kv_store.hip", "decode.hip", "prefill.hip"]
 
 # Packed-FP32 VALU forms are disabled for every device compile: the build
-# relies on scalar/float2 code only.
-DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+# relies on scalar/float2 code only.  Without NaN semantics, fmaxf lowers to a
+# single v_max (no canonicalising v_max x,x before each operand).
+DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                # inputs are finite; -inf is still used (and honoured) for masking
+                "-fno-honor-nans"]
 COMMON_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-result"]
 
 

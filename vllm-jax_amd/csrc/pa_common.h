@@ -55,10 +55,13 @@ __device__ __forceinline__ u32x4 as_u32x4(const bf16x8& v) {
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float f32x2;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
+// Two floats -> one packed bf16 pair (a single v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  __bf16 a = static_cast<__bf16>(lo);
-  __bf16 b = static_cast<__bf16>(hi);
-  return (uint32_t)__builtin_bit_cast(uint16_t, a) | ((uint32_t)__builtin_bit_cast(uint16_t, b) << 16);
+  const f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
 // Value of `x` in lane l^32 / l^16 combined with the own value.  permlane
@@ -83,8 +86,6 @@ __device__ __forceinline__ float sum_xor16(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
-
 // acc + lo + hi of a packed bf16 pair (v_dot2c_f32_bf16 against (1, 1)).
 __device__ __forceinline__ float dot2_bf16_ones(uint32_t pair, float acc) {
   const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};
@@ -96,6 +97,16 @@ __device__ __forceinline__ float dot2_bf16_ones(uint32_t pair, float acc) {
 // that no access leaves the pool.
 __device__ __forceinline__ int32_t safe_page(const int32_t* __restrict__ bt_row, int lp, int num_pages) {
   int32_t p = bt_row[lp];
+  p = p < 0 ? 0 : p;
+  return p >= num_pages ? num_pages - 1 : p;
+}
+
+// safe_page through the scalar cache: for a wave-uniform `lp` this is an
+// s_load (counted by lgkmcnt), so it never waits behind outstanding vector
+// loads.  The block table is read-only for the duration of every kernel.
+__device__ __forceinline__ int32_t safe_page_scalar(const int32_t* __restrict__ bt_row, int lp, int num_pages) {
+  const __attribute__((address_space(4))) int32_t* c = (const __attribute__((address_space(4))) int32_t*)bt_row;
+  int32_t p = c[lp];
   p = p < 0 ? 0 : p;
   return p >= num_pages ? num_pages - 1 : p;
 }

@@ -1,14 +1,14 @@
 // Ragged causal GQA paged prefill for gfx950.
 //
-// Workgroup = (q tile, sequence, kv head); 4 waves x 32 rows = 128 rows, where
+// Workgroup = (q tile, sequence, kv head); 8 waves x 32 rows = 256 rows, where
 // a row is a (query token, q head of this kv head) pair: row n of the tile is
 // token n / G, head n % G (G = q heads per kv head).  Packing the G heads into
 // the MFMA dimension makes every K/V tile staged in LDS serve G x tokens rows.
-// Two workgroups share a CU (2 waves per SIMD), so one wave's softmax VALU
-// work overlaps the other's MFMA work.
+// One workgroup per CU, two waves per SIMD.
 //
-// Per 64-token KV tile, double-buffered in LDS and filled by direct
-// global->LDS loads (global_load_lds_dwordx4) through the block table:
+// KV tiles of 64 tokens go through a 3-stage LDS ring filled by direct
+// global->LDS loads (global_load_lds_dwordx4) through the block table, issued
+// two tiles ahead of use.  Per tile and wave:
 //   S^T[t][n] = K[t][:] . Q[n][:]      v_mfma_f32_32x32x16_bf16, K rows read
 //                                       with ds_read_b128, Q^T kept in VGPRs
 //   online softmax per row n            row n = lane % 32: the row max needs one
@@ -20,20 +20,26 @@
 //                                       tile with ds_read_b64_tr_b16 (gfx950's
 //                                       transposing LDS read), P^T straight from
 //                                       the S^T accumulator registers
-// LDS tiles are 64 rows x 256 B with 16-byte chunks XOR-swizzled per row so
-// that both the K reads and the transposing V reads are bank-conflict free.
-// KV tiles entirely above the causal diagonal of the q tile are never loaded;
-// the mask is evaluated only on tiles that straddle it or the kv length.
-// Workgroups are dispatched from the last q tile down so the longest causal
-// rows start first.
+// The softmax runs per 32-token half so one half's VALU work overlaps the
+// other half's MFMAs.  LDS tiles are 64 rows x 256 B with 16-byte chunks
+// XOR-swizzled per row so that both the K reads and the transposing V reads
+// are bank-conflict free.  KV tiles entirely above the causal diagonal of the
+// q tile are never loaded; the mask is evaluated only on tiles that straddle
+// it or the kv length.  Workgroups are dispatched from the last q tile down so
+// the longest causal rows start first.
+#include <type_traits>
+
 #include "pa_common.h"
 #include "pa_errors.h"
 
 namespace pa {
 
 constexpr int kPHeadDim = 128;
-constexpr int kRows = 128;        // rows per workgroup
+constexpr int kWaves = 8;         // waves per workgroup, 32 rows each
+constexpr int kThreads = 64 * kWaves;
+constexpr int kRows = 32 * kWaves;  // rows per workgroup
 constexpr int kTileN = 64;        // kv tokens per tile
+constexpr int kStages = 3;        // LDS ring depth: loads run two tiles ahead
 constexpr int kTileElems = kTileN * kPHeadDim;
 constexpr float kRescaleSlack = 8.f;  // log2 units the running max may lag
 
@@ -59,11 +65,16 @@ struct PrefillParams {
 
 typedef s16x4 __attribute__((address_space(3))) * lds_s16x4_ptr;
 typedef void __attribute__((address_space(3))) * lds_void_ptr;
+typedef const char __attribute__((address_space(3))) * lds_cbytes;
 
-// Transposing 8-byte LDS read (ds_read_b64_tr_b16).  `lds` must point into
-// __shared__ memory; the cast is an address-space cast, not a reinterpretation.
-__device__ __forceinline__ s16x4 ds_read_tr16(const uint16_t* lds) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(lds));
+// Transposing 8-byte LDS read (ds_read_b64_tr_b16) at LDS byte address `a`.
+__device__ __forceinline__ s16x4 ds_read_tr16(lds_cbytes a) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(a));
+}
+
+// 16-byte LDS read (ds_read_b128) at LDS byte address `a`.
+__device__ __forceinline__ u32x4 ds_read16(lds_cbytes a) {
+  return *reinterpret_cast<const u32x4 __attribute__((address_space(3)))*>(a);
 }
 
 // Physical 16-byte chunk of logical chunk c in tile row r.
@@ -71,21 +82,73 @@ __device__ __forceinline__ int swz(int r, int c) {
   return c ^ (((r & 3) << 2) | ((r >> 2) & 3));
 }
 
+// Work item of workgroup `bid`: (q tile, sequence b, kv head).  Items are
+// ordered from the last q tile down (longest causal rows first).  Within one
+// q-tile level the (b, kv head) pairs are placed so that, with workgroups
+// dealt round-robin to the 8 XCDs, an XCD always serves the same pairs and
+// holds one kv head of every sequence: all q tiles of a (b, head) pair then
+// share that XCD's L2, and every XCD carries the same mix of sequence lengths.
+__device__ __forceinline__ void prefill_item(int bid, int batch, int hkv, int n_qtiles, int& qt, int& b, int& kvh) {
+  const int pairs = batch * hkv;
+  const int level = bid / pairs;
+  const int j = bid - level * pairs;
+  qt = n_qtiles - 1 - level;
+  if (hkv % 8 == 0) {
+    const int xcd = j & 7;
+    const int k = j >> 3;             // 0 .. batch*hkv/8 - 1
+    const int per_b = hkv >> 3;
+    b = k / per_b;
+    kvh = 8 * (k - b * per_b) + ((xcd - b) & 7);
+  } else {
+    b = j / hkv;
+    kvh = j - b * hkv;
+  }
+}
+
+// One 16-byte-per-lane global->LDS load (global_load_lds_dwordx4): lane l's
+// 16 bytes land at LDS byte address lds_block + 16*l.  Issued as inline asm so
+// the compiler does not insert its conservative "wait for every LDS DMA"
+// before unrelated LDS reads; completion is tracked explicitly with
+// wait_vm_lgkm0 + s_barrier before any wave reads the stage.
+__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_block) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_block) : "memory", "m0");
+}
+
+// s_waitcnt with vmcnt = N (N < 16), lgkmcnt = 0, expcnt untouched (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8));
+}
+
 template <bool kSoftCap, bool kAligned>
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(kThreads, 1)
 prefill_kernel(PrefillParams p) {
-  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[2][kTileElems];
-  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[2][kTileElems];
-  __shared__ int red_max[4], red_min[4];
+  // One object per ring stage: the compiler's LDS-DMA wait tracking then sees
+  // that reads of stage s never alias loads in flight into the other stages
+  // (with a single array it waits for every DMA before any LDS read).
+  __shared__ __attribute__((aligned(1024))) uint16_t k_lds0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) uint16_t k_lds1[kTileElems];
+  __shared__ __attribute__((aligned(1024))) uint16_t k_lds2[kTileElems];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds1[kTileElems];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds2[kTileElems];
+  __shared__ int red_max[kWaves], red_min[kWaves];
+  auto k_stage = [&](auto c) -> uint16_t* {
+    constexpr int s = decltype(c)::value;
+    return s == 0 ? k_lds0 : (s == 1 ? k_lds1 : k_lds2);
+  };
+  auto v_stage = [&](auto c) -> uint16_t* {
+    constexpr int s = decltype(c)::value;
+    return s == 0 ? v_lds0 : (s == 1 ? v_lds1 : v_lds2);
+  };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
   const int hkv = p.num_kv_heads;
-  const int kvh = blockIdx.x % hkv;
-  const int rest = blockIdx.x / hkv;
-  const int b = rest % p.batch;
-  const int qt = p.n_qtiles - 1 - rest / p.batch;
+  int qt, b, kvh;
+  prefill_item(blockIdx.x, p.batch, hkv, p.n_qtiles, qt, b, kvh);
 
   const int q0 = p.cu_q[b];
   const int lq = p.cu_q[b + 1] - q0;
@@ -131,62 +194,118 @@ prefill_kernel(PrefillParams p) {
     for (int ks = 0; ks < 8; ++ks)
       qt_op[ks] = as_bf16x8(row_ok ? ld16(qrow + 16 * ks) : u32x4{0, 0, 0, 0});
   }
+  // Retire every compiler-visible vector load here: the tile DMAs below are
+  // invisible to the compiler's wait tracking, so nothing it issued may still
+  // be in flight when they start (else it would drain them at the loop head).
+  wait_vm_lgkm0<0>();
   __syncthreads();
-  const int qpos_max = max(max(red_max[0], red_max[1]), max(red_max[2], red_max[3]));
-  const int qpos_min = min(min(red_min[0], red_min[1]), min(red_min[2], red_min[3]));
+  int qpos_max = red_max[0], qpos_min = red_min[0];
+#pragma unroll
+  for (int w = 1; w < kWaves; ++w) {
+    qpos_max = max(qpos_max, red_max[w]);
+    qpos_min = min(qpos_min, red_min[w]);
+  }
   // kv index j is visible to some row iff j < lk and j + kv_pos_off <= qpos_max
   const int64_t kv_hi64 = min((int64_t)lk, (int64_t)qpos_max - kv_pos_off + 1);
   const int kv_hi = kv_hi64 < 0 ? 0 : (int)kv_hi64;
   const int n_tiles = (kv_hi + kTileN - 1) / kTileN;
+  // tiles [0, n_free) need no mask: every token is < lk and visible to every row
+  const int64_t free_hi = min((int64_t)lk, (int64_t)qpos_min - kv_pos_off + 1);
+  const int n_free = free_hi < 0 ? 0 : (int)(free_hi / kTileN);
 
-  // ---- direct global->LDS tile loader.  Wave w fills 1 KiB blocks 4w..4w+3
-  // of each tile (rows 4blk .. 4blk+3); lane l writes LDS bytes 16*l of the
-  // block, i.e. row 4blk + l/16, physical chunk l%16, so it loads the logical
-  // chunk swz(row, l%16) of that token.
+  // ---- direct global->LDS tile loader.  A tile is 16 blocks of 1 KiB
+  // (4 rows each); wave w fills blocks kBlk*w .. kBlk*w + kBlk-1 of K and V.
+  // Lane l writes LDS bytes 16*l of a block, i.e. row 4blk + l/16, physical
+  // chunk l%16, so it loads the logical chunk swz(row, l%16) of that token.
+  constexpr int kBlk = 16 / kWaves;
   const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
   const int ld_r = lane >> 4;            // row within a 1 KiB block
   const int ld_p = lane & 15;            // physical chunk
   const int64_t head_off = (int64_t)kvh * p.head_stride;
-  auto issue_tile = [&](int j0, int buf) {
+  uint32_t ld_off[kBlk];                 // per-lane element offset of the row within a page
+#pragma unroll
+  for (int i = 0; i < kBlk; ++i) {
+    const int r = 4 * (kBlk * wave + i) + ld_r;
+    ld_off[i] = (uint32_t)(r * (int32_t)p.slot_stride + 8 * swz(r, ld_p));
+  }
+  auto issue_tile = [&](int j0, auto buf_c) {
+    uint16_t* const kdst = k_stage(buf_c);
+    uint16_t* const vdst = v_stage(buf_c);
     // All addresses first, then the loads: a block-table read queued behind
     // the LDS-DMA loads would make the compiler wait for all of them.
-    int64_t off[4];
+    const uint16_t* kb[kBlk];
+    const uint16_t* vb[kBlk];
     if constexpr (kAligned) {
-      // page_size % 64 == 0: the whole tile lies in one page (one scalar load)
+      // page_size % 64 == 0: the whole tile lies in one page (one uniform load)
       const int lp = j0 / p.page_size;
-      const int32_t page = safe_page(bt_row, lp, p.num_pages);
+      const int32_t page = safe_page_scalar(bt_row, lp, p.num_pages);
       const int64_t pbase = (int64_t)page * p.page_stride + (int64_t)(j0 - lp * p.page_size) * p.slot_stride + head_off;
-      const int last = lk - 1 - j0;  // clamp onto a valid token: masked, never stale
+      if (j0 + kTileN <= lk) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * (4 * wave + i) + ld_r;
-        off[i] = pbase + (int64_t)min(r, last) * p.slot_stride + 8 * swz(r, ld_p);
+        for (int i = 0; i < kBlk; ++i) {
+          kb[i] = p.k_cache + pbase + ld_off[i];
+          vb[i] = p.v_cache + pbase + ld_off[i];
+        }
+      } else {
+        const int last = lk - 1 - j0;  // clamp onto a valid token: masked, never stale
+#pragma unroll
+        for (int i = 0; i < kBlk; ++i) {
+          const int r = 4 * (kBlk * wave + i) + ld_r;
+          const int64_t o = pbase + (int64_t)min(r, last) * p.slot_stride + 8 * swz(r, ld_p);
+          kb[i] = p.k_cache + o;
+          vb[i] = p.v_cache + o;
+        }
       }
     } else {
-      int32_t pages[4];
+      int32_t pages[kBlk];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * (4 * wave + i) + ld_r;
+      for (int i = 0; i < kBlk; ++i) {
+        const int r = 4 * (kBlk * wave + i) + ld_r;
         const int j = min(j0 + r, lk - 1);
         pages[i] = safe_page(bt_row, j / p.page_size, p.num_pages);
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 4 * (4 * wave + i) + ld_r;
+      for (int i = 0; i < kBlk; ++i) {
+        const int r = 4 * (kBlk * wave + i) + ld_r;
         const int j = min(j0 + r, lk - 1);
-        off[i] = (int64_t)pages[i] * p.page_stride + (int64_t)(j % p.page_size) * p.slot_stride + head_off +
-                 8 * swz(r, ld_p);
+        const int64_t o = (int64_t)pages[i] * p.page_stride + (int64_t)(j % p.page_size) * p.slot_stride +
+                          head_off + 8 * swz(r, ld_p);
+        kb[i] = p.k_cache + o;
+        vb[i] = p.v_cache + o;
       }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int blk = 4 * wave + i;
-      __builtin_amdgcn_global_load_lds((const void*)(p.k_cache + off[i]),
-                                       (lds_void_ptr)(&k_lds[buf][blk * 512]), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const void*)(p.v_cache + off[i]),
-                                       (lds_void_ptr)(&v_lds[buf][blk * 512]), 16, 0, 0);
+    for (int i = 0; i < kBlk; ++i) {
+      const int blk = kBlk * wave + i;
+      dma16(kb[i], (uint32_t)(uintptr_t)(lds_void_ptr)(kdst + blk * 512));
+      dma16(vb[i], (uint32_t)(uintptr_t)(lds_void_ptr)(vdst + blk * 512));
     }
   };
+  constexpr int kDmaPerTile = 2 * kBlk;  // vm instructions one wave issues per tile
+
+  // ---- per-lane LDS read offsets (bytes), fixed for the whole kernel.
+  // K (A of S^T): row 32mt + n, logical chunk 2ks + h; the swizzle of a row
+  // only depends on its low 4 bits, i.e. on n.
+  const int fn = ((n & 3) << 2) | ((n >> 2) & 3);
+  uint32_t koff[8];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) koff[ks] = n * 256 + 16 * ((2 * ks + h) ^ fn);
+  // V^T (tr16): lane = 16*gamma + s reads row tokbase + 4h + s/4 (+8) and
+  // logical column 32dt + 16(gamma%2) + 4(s%4): chunk 4dt + 2(gamma%2) +
+  // (s%4)/2, byte 8*(s%2) inside it.  tokbase is a multiple of 16, so the
+  // row's swizzle is that of tr_row (or tr_row + 8).
+  const int tr_s = lane & 15;
+  const int tr_gamma = lane >> 4;
+  const int tr_row = 4 * h + (tr_s >> 2);
+  const int f0 = ((tr_row & 3) << 2) | ((tr_row >> 2) & 3);
+  const int f1 = (((tr_row + 8) & 3) << 2) | (((tr_row + 8) >> 2) & 3);
+  uint32_t voff0[4], voff1[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+    const int c = 4 * dt + 2 * (tr_gamma & 1) + ((tr_s & 3) >> 1);
+    voff0[dt] = tr_row * 256 + 16 * (c ^ f0) + 8 * (tr_s & 1);
+    voff1[dt] = (tr_row + 8) * 256 + 16 * (c ^ f1) + 8 * (tr_s & 1);
+  }
 
   f32x16 acc_o[4];
 #pragma unroll
@@ -195,113 +314,110 @@ prefill_kernel(PrefillParams p) {
     for (int i = 0; i < 16; ++i) acc_o[dt][i] = 0.f;
   float m_ref = -1e30f;  // reference max (log2 units) of the accumulators
   float l_run = 0.f;
+  const float cs = kSoftCap ? 1.f : p.logit_scale;  // multiplier applied inside the exponent
 
-  if (n_tiles > 0) issue_tile(0, 0);
-  __syncthreads();  // waits for the loads (vmcnt) before the barrier
-
-  // ds_read_tr16 addressing of the V^T operand: lane = 16*gamma + s reads
-  // row (tokbase + 4h + s/4 [+8]), logical column 32dt + 16(gamma%2) + 4(s%4).
-  const int tr_s = lane & 15;
-  const int tr_gamma = lane >> 4;
-  const int tr_row = 4 * h + (tr_s >> 2);
-  const int tr_col = 16 * (tr_gamma & 1) + 4 * (tr_s & 3);
-  const float c_log2 = p.logit_scale;
-
-  for (int it = 0; it < n_tiles; ++it) {
-    const int buf = it & 1;
+  auto tile = [&](int it, auto buf_c) {
+    constexpr int buf = decltype(buf_c)::value;
     const int j0 = it * kTileN;
-    if (it + 1 < n_tiles) issue_tile(j0 + kTileN, buf ^ 1);
+    if (it + 2 < n_tiles) issue_tile(j0 + 2 * kTileN, std::integral_constant<int, (buf + 2) % kStages>{});
+    const lds_cbytes kt = (lds_cbytes)(k_stage(buf_c));
+    const lds_cbytes vt = (lds_cbytes)(v_stage(buf_c));
 
-    const uint16_t* kt = k_lds[buf];
-    const uint16_t* vt = v_lds[buf];
-
-    // ---- S^T for tokens j0 + 32mt + (0..31)
+    // ---- S^T for both 32-token halves first, so that the softmax of one
+    // half overlaps the MFMAs of the other.
     f32x16 s_acc[2];
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) s_acc[mt][i] = 0.f;
-      const int r = 32 * mt + n;
 #pragma unroll
       for (int ks = 0; ks < 8; ++ks) {
-        const bf16x8 a = as_bf16x8(*reinterpret_cast<const u32x4*>(kt + r * kPHeadDim + 8 * swz(r, 2 * ks + h)));
+        const bf16x8 a = as_bf16x8(ds_read16(kt + koff[ks] + mt * 8192));
         s_acc[mt] = mfma32(a, qt_op[ks], s_acc[mt]);
       }
     }
 
-    // ---- logits (log2 units), mask, online softmax for row n = lane % 32.
-    // s_acc[mt][i] = S[row n][token j0 + 32mt + 8(i/4) + 4h + i%4]
-    if constexpr (kSoftCap) {
 #pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+    for (int mt = 0; mt < 2; ++mt) {
+      // s_acc[mt][i] = S[row n][token j0 + 32mt + 8(i/4) + 4h + i%4]
+      if constexpr (kSoftCap) {
 #pragma unroll
         for (int i = 0; i < 16; ++i)
           s_acc[mt][i] = p.soft_cap * kLog2e * tanhf(s_acc[mt][i] * p.logit_scale / p.soft_cap);
-    }
-    const float cs = kSoftCap ? 1.f : c_log2;  // multiplier applied inside the exponent
-    const bool need_mask = (j0 + kTileN > lk) || (j0 + kTileN - 1 + kv_pos_off > qpos_min);
-    if (need_mask) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
+      }
+      if (it >= n_free) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int j = j0 + 32 * mt + 8 * (i >> 2) + 4 * h + (i & 3);
           const bool vis = j < lk && j + kv_pos_off <= qpos;
           s_acc[mt][i] = vis ? s_acc[mt][i] : -INFINITY;
         }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) mx = fmaxf(mx, fmaxf(s_acc[mt][i], s_acc[mt][i + 1]));
-    mx = max_xor32(mx) * cs;
-    // Move the reference max only when this tile's max exceeds it by more
-    // than the slack (any lane in the wave): exponents stay <= 2^slack.
-    if (__any(mx > m_ref + kRescaleSlack)) {
-      const float m_new = fmaxf(m_ref, mx);
-      const float corr = fast_exp2(m_ref - m_new);
-      m_ref = m_new;
-      l_run *= corr;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) acc_o[dt] = acc_o[dt] * corr;
-    }
-    bf16x8 pt[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int mt = u >> 1;
-      const int base = 8 * (u & 1);
-      u32x4 w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float a = fast_exp2(__builtin_fmaf(s_acc[mt][base + 2 * e], cs, -m_ref));
-        const float c = fast_exp2(__builtin_fmaf(s_acc[mt][base + 2 * e + 1], cs, -m_ref));
-        w[e] = pack_bf16x2(a, c);
       }
-      pt[u] = as_bf16x8(w);
+      float mx = -INFINITY;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) l_run = dot2_bf16_ones(w[e], l_run);
-    }
-
-    // ---- O^T += V^T . P^T ; k-step u covers tokens 32(u/2) + 16(u%2) + {4h + r, 8 + 4h + r}
+      for (int i = 0; i < 16; i += 2) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s_acc[mt][i], s_acc[mt][i + 1]));
+      mx = max_xor32(mx) * cs;
+      // Move the reference max only when this half's max exceeds it by more
+      // than the slack (any lane in the wave): exponents stay <= 2^slack.
+      if (__any(mx > m_ref + kRescaleSlack)) {
+        const float m_new = fmaxf(m_ref, mx);
+        const float corr = fast_exp2(m_ref - m_new);
+        m_ref = m_new;
+        l_run *= corr;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int r0 = 32 * (u >> 1) + 16 * (u & 1) + tr_row;
-      const int r1 = r0 + 8;
+        for (int dt = 0; dt < 4; ++dt) acc_o[dt] = acc_o[dt] * corr;
+      }
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const int col = 32 * dt + tr_col;  // logical column; chunk col/8, half (col%8)/4
-        const s16x4 lo = ds_read_tr16(vt + r0 * kPHeadDim + 8 * swz(r0, col >> 3) + (col & 7));
-        const s16x4 hi = ds_read_tr16(vt + r1 * kPHeadDim + 8 * swz(r1, col >> 3) + (col & 7));
-        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
-        const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
-        const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
-        acc_o[dt] = mfma32(as_bf16x8(a), pt[u], acc_o[dt]);
+      for (int uu = 0; uu < 2; ++uu) {
+        const int u = 2 * mt + uu;  // k-step: tokens 32mt + 16uu + {4h + r, 8 + 4h + r}
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a = fast_exp2(__builtin_fmaf(s_acc[mt][8 * uu + 2 * e], cs, -m_ref));
+          const float c = fast_exp2(__builtin_fmaf(s_acc[mt][8 * uu + 2 * e + 1], cs, -m_ref));
+          w[e] = pack_bf16x2(a, c);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) l_run = dot2_bf16_ones(w[e], l_run);
+        const bf16x8 pt = as_bf16x8(w);
+        const int rb = (32 * mt + 16 * uu) * 256;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const s16x4 lo = ds_read_tr16(vt + rb + voff0[dt]);
+          const s16x4 hi = ds_read_tr16(vt + rb + voff1[dt]);
+          const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
+          const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
+          const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
+          acc_o[dt] = mfma32(as_bf16x8(a), pt, acc_o[dt]);
+        }
       }
     }
 
-    __syncthreads();  // next tile landed (vmcnt) and everyone is done with this one
+    // Next tile landed: this wave's loads for tile it+1 are done once at most
+    // the kDmaPerTile loads of tile it+2 are outstanding.  The barrier then
+    // publishes every wave's part and frees this tile's buffer for reuse.
+    if (it + 2 < n_tiles) wait_vm_lgkm0<kDmaPerTile>();
+    else wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();
+  };
+
+  if (n_tiles > 0) issue_tile(0, std::integral_constant<int, 0>{});
+  if (n_tiles > 1) {
+    issue_tile(kTileN, std::integral_constant<int, 1>{});
+    wait_vm_lgkm0<kDmaPerTile>();
+  } else {
+    wait_vm_lgkm0<0>();
   }
+  __builtin_amdgcn_s_barrier();
+
+  int it = 0;
+  for (; it + 2 < n_tiles; it += 3) {
+    tile(it, std::integral_constant<int, 0>{});
+    tile(it + 1, std::integral_constant<int, 1>{});
+    tile(it + 2, std::integral_constant<int, 2>{});
+  }
+  if (it < n_tiles) tile(it, std::integral_constant<int, 0>{});
+  if (it + 1 < n_tiles) tile(it + 1, std::integral_constant<int, 1>{});
 
   // ---- epilogue: row n = (token rtok, head rhead); acc_o[dt][i] holds
   // d = 32dt + 8(i/4) + 4h + i%4
@@ -437,11 +553,11 @@ extern "C" int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_hea
     return fail(PA_ERR_UNSUPPORTED, "pa_prefill: grid of %lld workgroups too large", (long long)blocks);
   const bool aligned = page_size % kTileN == 0;
   if (prm.soft_cap > 0.f) {
-    if (aligned) prefill_kernel<true, true><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(prm);
-    else prefill_kernel<true, false><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(prm);
+    if (aligned) prefill_kernel<true, true><<<dim3((unsigned)blocks), dim3(kThreads), 0, s>>>(prm);
+    else prefill_kernel<true, false><<<dim3((unsigned)blocks), dim3(kThreads), 0, s>>>(prm);
   } else {
-    if (aligned) prefill_kernel<false, true><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(prm);
-    else prefill_kernel<false, false><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(prm);
+    if (aligned) prefill_kernel<false, true><<<dim3((unsigned)blocks), dim3(kThreads), 0, s>>>(prm);
+    else prefill_kernel<false, false><<<dim3((unsigned)blocks), dim3(kThreads), 0, s>>>(prm);
   }
   return launch_status("pa_prefill");
 }
