@@ -39,9 +39,13 @@ constexpr int kWaves = 8;         // waves per workgroup, 32 rows each
 constexpr int kThreads = 64 * kWaves;
 constexpr int kRows = 32 * kWaves;  // rows per workgroup
 constexpr int kTileN = 64;        // kv tokens per tile
-constexpr int kStages = 3;        // LDS ring depth: loads run two tiles ahead
+constexpr int kStages = 4;        // LDS ring depth: loads run two tiles ahead
 constexpr int kTileElems = kTileN * kPHeadDim;
 constexpr float kRescaleSlack = 8.f;  // log2 units the running max may lag
+// instruction classes of __builtin_amdgcn_sched_group_barrier
+constexpr int kSchedMfma = 0x008;
+constexpr int kSchedDsRead = 0x100;
+constexpr int kReadsAhead = 8;  // LDS reads kept in flight ahead of the MFMAs
 
 struct PrefillParams {
   const uint16_t* q;
@@ -127,21 +131,11 @@ prefill_kernel(PrefillParams p) {
   // One object per ring stage: the compiler's LDS-DMA wait tracking then sees
   // that reads of stage s never alias loads in flight into the other stages
   // (with a single array it waits for every DMA before any LDS read).
-  __shared__ __attribute__((aligned(1024))) uint16_t k_lds0[kTileElems];
-  __shared__ __attribute__((aligned(1024))) uint16_t k_lds1[kTileElems];
-  __shared__ __attribute__((aligned(1024))) uint16_t k_lds2[kTileElems];
-  __shared__ __attribute__((aligned(1024))) uint16_t v_lds0[kTileElems];
-  __shared__ __attribute__((aligned(1024))) uint16_t v_lds1[kTileElems];
-  __shared__ __attribute__((aligned(1024))) uint16_t v_lds2[kTileElems];
+  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[kStages][kTileElems];
+  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[kStages][kTileElems];
   __shared__ int red_max[kWaves], red_min[kWaves];
-  auto k_stage = [&](auto c) -> uint16_t* {
-    constexpr int s = decltype(c)::value;
-    return s == 0 ? k_lds0 : (s == 1 ? k_lds1 : k_lds2);
-  };
-  auto v_stage = [&](auto c) -> uint16_t* {
-    constexpr int s = decltype(c)::value;
-    return s == 0 ? v_lds0 : (s == 1 ? v_lds1 : v_lds2);
-  };
+  auto k_stage = [&](auto c) __attribute__((always_inline)) -> uint16_t* { return k_lds[decltype(c)::value]; };
+  auto v_stage = [&](auto c) __attribute__((always_inline)) -> uint16_t* { return v_lds[decltype(c)::value]; };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -228,7 +222,7 @@ prefill_kernel(PrefillParams p) {
     const int r = 4 * (kBlk * wave + i) + ld_r;
     ld_off[i] = (uint32_t)(r * (int32_t)p.slot_stride + 8 * swz(r, ld_p));
   }
-  auto issue_tile = [&](int j0, auto buf_c) {
+  auto issue_tile = [&](int j0, auto buf_c) __attribute__((always_inline)) {
     uint16_t* const kdst = k_stage(buf_c);
     uint16_t* const vdst = v_stage(buf_c);
     // All addresses first, then the loads: a block-table read queued behind
@@ -315,90 +309,149 @@ prefill_kernel(PrefillParams p) {
   float m_ref = -1e30f;  // reference max (log2 units) of the accumulators
   float l_run = 0.f;
   const float cs = kSoftCap ? 1.f : p.logit_scale;  // multiplier applied inside the exponent
+  f32x16 s_acc[2];  // S^T of the tile between its QK and its softmax
+  bf16x8 pt[4];     // P^T of the tile between its softmax and its PV
 
-  auto tile = [&](int it, auto buf_c) {
-    constexpr int buf = decltype(buf_c)::value;
-    const int j0 = it * kTileN;
-    if (it + 2 < n_tiles) issue_tile(j0 + 2 * kTileN, std::integral_constant<int, (buf + 2) % kStages>{});
-    const lds_cbytes kt = (lds_cbytes)(k_stage(buf_c));
-    const lds_cbytes vt = (lds_cbytes)(v_stage(buf_c));
-
-    // ---- S^T for both 32-token halves first, so that the softmax of one
-    // half overlaps the MFMAs of the other.
-    f32x16 s_acc[2];
+  // ---- work pieces.  M(t) = PV(t-1) + QK(t) is MFMA work, SM(t) = softmax of
+  // tile t is VALU work.  Waves 0-3 (group A) and 4-7 (group B) share the
+  // SIMDs pairwise and run the same sequence half a step apart:
+  //   segment 2t:   A: M(t)    B: SM(t-1)
+  //   segment 2t+1: A: SM(t)   B: M(t)
+  // with a workgroup barrier after every segment, so on every SIMD one wave
+  // feeds the matrix core while the other one does its softmax (ping-pong).
+  auto qk = [&](auto kst) __attribute__((always_inline)) {
+    const lds_cbytes kt = (lds_cbytes)(k_stage(kst));
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; ++i) s_acc[mt][i] = 0.f;
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
+    for (int ks = 0; ks < 8; ++ks) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
         const bf16x8 a = as_bf16x8(ds_read16(kt + koff[ks] + mt * 8192));
         s_acc[mt] = mfma32(a, qt_op[ks], s_acc[mt]);
       }
     }
-
+  };
+  auto pv = [&](auto vst) __attribute__((always_inline)) {
+    const lds_cbytes vt = (lds_cbytes)(v_stage(vst));
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      // s_acc[mt][i] = S[row n][token j0 + 32mt + 8(i/4) + 4h + i%4]
-      if constexpr (kSoftCap) {
+    for (int u = 0; u < 4; ++u) {
+      // k-step u: tokens 32(u/2) + 16(u%2) + {4h + r, 8 + 4h + r}
+      const int rb = (32 * (u >> 1) + 16 * (u & 1)) * 256;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const s16x4 lo = ds_read_tr16(vt + rb + voff0[dt]);
+        const s16x4 hi = ds_read_tr16(vt + rb + voff1[dt]);
+        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
+        const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
+        const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
+        acc_o[dt] = mfma32(as_bf16x8(a), pt[u], acc_o[dt]);
+      }
+    }
+  };
+  auto softmax = [&](int t) __attribute__((always_inline)) {
+    const int j0 = t * kTileN;
+    if constexpr (kSoftCap) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
           s_acc[mt][i] = p.soft_cap * kLog2e * tanhf(s_acc[mt][i] * p.logit_scale / p.soft_cap);
-      }
-      if (it >= n_free) {
+    }
+    // s_acc[mt][i] = S[row n][token j0 + 32mt + 8(i/4) + 4h + i%4]
+    if (t >= n_free) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int j = j0 + 32 * mt + 8 * (i >> 2) + 4 * h + (i & 3);
           const bool vis = j < lk && j + kv_pos_off <= qpos;
           s_acc[mt][i] = vis ? s_acc[mt][i] : -INFINITY;
         }
-      }
-      float mx = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int i = 0; i < 16; i += 2) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s_acc[mt][i], s_acc[mt][i + 1]));
-      mx = max_xor32(mx) * cs;
-      // Move the reference max only when this half's max exceeds it by more
-      // than the slack (any lane in the wave): exponents stay <= 2^slack.
-      if (__any(mx > m_ref + kRescaleSlack)) {
-        const float m_new = fmaxf(m_ref, mx);
-        const float corr = fast_exp2(m_ref - m_new);
-        m_ref = m_new;
-        l_run *= corr;
+    mx = max_xor32(mx) * cs;
+    // Move the reference max only when this tile's max exceeds it by more
+    // than the slack (any lane in the wave): exponents stay <= 2^slack.
+    if (__any(mx > m_ref + kRescaleSlack)) {
+      const float m_new = fmaxf(m_ref, mx);
+      const float corr = fast_exp2(m_ref - m_new);
+      m_ref = m_new;
+      l_run *= corr;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) acc_o[dt] = acc_o[dt] * corr;
-      }
-#pragma unroll
-      for (int uu = 0; uu < 2; ++uu) {
-        const int u = 2 * mt + uu;  // k-step: tokens 32mt + 16uu + {4h + r, 8 + 4h + r}
-        u32x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float a = fast_exp2(__builtin_fmaf(s_acc[mt][8 * uu + 2 * e], cs, -m_ref));
-          const float c = fast_exp2(__builtin_fmaf(s_acc[mt][8 * uu + 2 * e + 1], cs, -m_ref));
-          w[e] = pack_bf16x2(a, c);
-        }
-#pragma unroll
-        for (int e = 0; e < 4; ++e) l_run = dot2_bf16_ones(w[e], l_run);
-        const bf16x8 pt = as_bf16x8(w);
-        const int rb = (32 * mt + 16 * uu) * 256;
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          const s16x4 lo = ds_read_tr16(vt + rb + voff0[dt]);
-          const s16x4 hi = ds_read_tr16(vt + rb + voff1[dt]);
-          const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
-          const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
-          const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
-          acc_o[dt] = mfma32(as_bf16x8(a), pt, acc_o[dt]);
-        }
-      }
+      for (int dt = 0; dt < 4; ++dt) acc_o[dt] = acc_o[dt] * corr;
     }
-
-    // Next tile landed: this wave's loads for tile it+1 are done once at most
-    // the kDmaPerTile loads of tile it+2 are outstanding.  The barrier then
-    // publishes every wave's part and frees this tile's buffer for reuse.
-    if (it + 2 < n_tiles) wait_vm_lgkm0<kDmaPerTile>();
-    else wait_vm_lgkm0<0>();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int mt = u >> 1;
+      const int base = 8 * (u & 1);
+      u32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float a = fast_exp2(__builtin_fmaf(s_acc[mt][base + 2 * e], cs, -m_ref));
+        const float c = fast_exp2(__builtin_fmaf(s_acc[mt][base + 2 * e + 1], cs, -m_ref));
+        w[e] = pack_bf16x2(a, c);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) l_run = dot2_bf16_ones(w[e], l_run);
+      // Materialise P here: otherwise the compiler sinks the exp work past
+      // the barrier into the next MFMA segment, undoing the ping-pong.
+      asm volatile("" : "+v"(w));
+      pt[u] = as_bf16x8(w);
+    }
+    asm volatile("" : "+v"(l_run));
+  };
+  auto barrier = [&]() __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Every wave runs the same sequence  M(0) SM(0) M(1) SM(1) ... M(n)  with a
+  // barrier after each piece; group B starts with one idle barrier (and group
+  // A ends with one), which shifts B half a step behind A.
+  //
+  // Tile T sits in stage T % 4.  A wave issues its share of tile T's DMA when
+  // it starts iteration T-2 and waits for it before the barrier that ends its
+  // M(T-1); both groups have thus waited by the end of global segment 2T-1,
+  // before A's QK(T) in segment 2T.  The previous occupant, tile T-4, was last
+  // read by B's M(T-3) in segment 2T-5.
+  const bool grp_b = wave >= kWaves / 2;
+  auto iteration = [&](int t, auto st) __attribute__((always_inline)) {
+    constexpr int s = decltype(st)::value;
+    using KS = std::integral_constant<int, s>;
+    using VS = std::integral_constant<int, (s + kStages - 1) % kStages>;
+    if (t + 2 < n_tiles) issue_tile((t + 2) * kTileN, std::integral_constant<int, (s + 2) % kStages>{});
+    if (t > 0) pv(VS{});
+    if (t < n_tiles) qk(KS{});
+    // One schedule for the whole MFMA segment: keep kReadsAhead LDS reads in
+    // flight ahead of the MFMAs (PV needs 2 reads per MFMA, QK 1).
+    if (t > 0 && t < n_tiles) {
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kReadsAhead, 0);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 16 - kReadsAhead; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, kReadsAhead, 0);
+    }
+    // tile t+1 complete: at most the DMAs of tile t+2 (issued above) remain
+    if (t + 2 < n_tiles) wait_vm_lgkm0<kDmaPerTile>();
+    else wait_vm_lgkm0<0>();
+    barrier();
+    if (t < n_tiles) softmax(t);
+    barrier();
   };
 
   if (n_tiles > 0) issue_tile(0, std::integral_constant<int, 0>{});
@@ -409,15 +462,20 @@ prefill_kernel(PrefillParams p) {
     wait_vm_lgkm0<0>();
   }
   __builtin_amdgcn_s_barrier();
+  if (grp_b) barrier();
 
-  int it = 0;
-  for (; it + 2 < n_tiles; it += 3) {
-    tile(it, std::integral_constant<int, 0>{});
-    tile(it + 1, std::integral_constant<int, 1>{});
-    tile(it + 2, std::integral_constant<int, 2>{});
+  // iterations t = 0 .. n_tiles (the last one only finishes PV(n_tiles-1))
+  int t = 0;
+  for (; t + 3 <= n_tiles; t += 4) {
+    iteration(t, std::integral_constant<int, 0>{});
+    iteration(t + 1, std::integral_constant<int, 1>{});
+    iteration(t + 2, std::integral_constant<int, 2>{});
+    iteration(t + 3, std::integral_constant<int, 3>{});
   }
-  if (it < n_tiles) tile(it, std::integral_constant<int, 0>{});
-  if (it + 1 < n_tiles) tile(it + 1, std::integral_constant<int, 1>{});
+  if (t <= n_tiles) iteration(t, std::integral_constant<int, 0>{});
+  if (t + 1 <= n_tiles) iteration(t + 1, std::integral_constant<int, 1>{});
+  if (t + 2 <= n_tiles) iteration(t + 2, std::integral_constant<int, 2>{});
+  if (!grp_b) barrier();
 
   // ---- epilogue: row n = (token rtok, head rhead); acc_o[dt][i] holds
   // d = 32dt + 8(i/4) + 4h + i%4
