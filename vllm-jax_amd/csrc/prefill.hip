@@ -415,54 +415,56 @@ prefill_kernel(PrefillParams p) {
 
   // Every wave runs the same sequence  M(0) SM(0) M(1) SM(1) ... M(n)  with a
   // barrier after each piece; group B starts with one idle barrier (and group
-  // A ends with one), which shifts B half a step behind A.
+  // A ends with one), which shifts B half a step behind A: A's M(t) runs in
+  // global segment 2t, B's in 2t+1.
   //
-  // Tile T sits in stage T % 4.  A wave issues its share of tile T's DMA when
-  // it starts iteration T-2 and waits for it before the barrier that ends its
-  // M(T-1); both groups have thus waited by the end of global segment 2T-1,
-  // before A's QK(T) in segment 2T.  The previous occupant, tile T-4, was last
-  // read by B's M(T-3) in segment 2T-5.
+  // Tile T sits in stage T % 4.  Tile DMAs are issued from the softmax
+  // segment (VALU-bound, so the memory instructions cost nothing there),
+  // never from the MFMA segment.  Group A issues its share of tile T during
+  // SM(T-2) (segment 2T-3) and waits for it at the end of iteration T-1
+  // (segment 2T-1); group B, half a step later, issues during SM(T-3)
+  // (segment 2T-4) and waits at the end of iteration T-2 (segment 2T-2).  So
+  // every share of tile T has landed before A's QK(T) in segment 2T, and the
+  // stage's previous tile T-4 was last read by B's M(T-3) in segment 2T-5.
   const bool grp_b = wave >= kWaves / 2;
+  const int ahead = grp_b ? 3 : 2;  // tile issued during SM(t) is t + ahead
   auto iteration = [&](int t, auto st) __attribute__((always_inline)) {
     constexpr int s = decltype(st)::value;
     using KS = std::integral_constant<int, s>;
     using VS = std::integral_constant<int, (s + kStages - 1) % kStages>;
-    if (t + 2 < n_tiles) issue_tile((t + 2) * kTileN, std::integral_constant<int, (s + 2) % kStages>{});
     if (t > 0) pv(VS{});
     if (t < n_tiles) qk(KS{});
-    // One schedule for the whole MFMA segment: keep kReadsAhead LDS reads in
-    // flight ahead of the MFMAs (PV needs 2 reads per MFMA, QK 1).
-    if (t > 0 && t < n_tiles) {
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, kReadsAhead, 0);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 16 - kReadsAhead; ++i) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, kReadsAhead, 0);
-    }
-    // tile t+1 complete: at most the DMAs of tile t+2 (issued above) remain
-    if (t + 2 < n_tiles) wait_vm_lgkm0<kDmaPerTile>();
-    else wait_vm_lgkm0<0>();
+    wait_vm_lgkm0<15>();  // LDS reads of this segment retired (vmcnt untouched)
     barrier();
+    const int ti = t + ahead;
+    if (ti < n_tiles) {
+      if (grp_b) issue_tile(ti * kTileN, std::integral_constant<int, (s + 3) % kStages>{});
+      else issue_tile(ti * kTileN, std::integral_constant<int, (s + 2) % kStages>{});
+    }
     if (t < n_tiles) softmax(t);
+    // this wave's share of tile t + ahead - 1 has landed: at most the loads of
+    // tile t + ahead (issued above) may still be outstanding
+    if (ti < n_tiles) wait_vm_lgkm0<kDmaPerTile>();
+    else wait_vm_lgkm0<0>();
     barrier();
   };
 
+  // Prologue: A issues tiles 0 and 1, B tiles 0, 1 and 2.  Everyone waits for
+  // tile 0 before the first barrier; B also waits for tile 1 before its idle
+  // barrier (which ends segment 0, i.e. before A's M(1) in segment 2).
   if (n_tiles > 0) issue_tile(0, std::integral_constant<int, 0>{});
-  if (n_tiles > 1) {
-    issue_tile(kTileN, std::integral_constant<int, 1>{});
-    wait_vm_lgkm0<kDmaPerTile>();
-  } else {
-    wait_vm_lgkm0<0>();
-  }
+  if (n_tiles > 1) issue_tile(kTileN, std::integral_constant<int, 1>{});
+  if (grp_b && n_tiles > 2) issue_tile(2 * kTileN, std::integral_constant<int, 2>{});
+  const int issued = min(n_tiles, grp_b ? 3 : 2);
+  if (issued == 3) wait_vm_lgkm0<2 * kDmaPerTile>();
+  else if (issued == 2) wait_vm_lgkm0<kDmaPerTile>();
+  else wait_vm_lgkm0<0>();
   __builtin_amdgcn_s_barrier();
-  if (grp_b) barrier();
+  if (grp_b) {
+    if (issued == 3) wait_vm_lgkm0<kDmaPerTile>();
+    else wait_vm_lgkm0<0>();
+    barrier();
+  }
 
   // iterations t = 0 .. n_tiles (the last one only finishes PV(n_tiles-1))
   int t = 0;
