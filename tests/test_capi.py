@@ -1,0 +1,111 @@
+"""The C-ABI library: it loads, exports every entry point the header declares,
+and rejects bad arguments with error codes before touching a device."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from conftest import PKG, ROOT
+
+HEADER = os.path.join(ROOT, "include", "paged_attention.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(pa_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib_path = PKG._lib.lib_path()
+    assert os.path.exists(lib_path), "build the library first (__graft_entry__.build())"
+    out = subprocess.run(["nm", "-D", "--defined-only", lib_path], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (pa_\w+)$", out, re.M))
+    declared = _declared()
+    assert declared, "no declarations parsed"
+    missing = [s for s in declared if s not in exported]
+    assert not missing, missing
+    # and the ctypes table covers them all
+    assert set(declared) <= set(PKG._lib.SIGNATURES)
+
+
+def test_error_codes_match_header():
+    text = open(HEADER).read()
+    codes = dict(re.findall(r"#define (PA_\w+) \(?(-?\d+)\)?", text))
+    assert codes == {"PA_OK": "0", "PA_ERR_INVALID_ARGUMENT": "-1", "PA_ERR_UNSUPPORTED": "-2",
+                     "PA_ERR_WORKSPACE": "-3", "PA_ERR_LAUNCH": "-4"}
+
+
+def test_abi_version():
+    assert PKG._lib.load().pa_abi_version() == 1
+
+
+def _decode_args(**over):
+    a = dict(q=None, q_bs=128 * 32, q_hs=128, k=None, v=None, num_pages=16, page_size=256,
+             ps=256 * 8 * 128, ss=8 * 128, hs=128, bt=None, bt_stride=4, pps=4, lens=None, batch=2,
+             heads=32, kv_heads=8, head_dim=128, scale=1.0, cap=0.0, out=None, o_bs=128 * 32, o_hs=128,
+             ws=None, ws_bytes=0, stream=None)
+    a.update(over)
+    return list(a.values())
+
+
+def test_decode_rejects_bad_arguments_without_a_device():
+    lib = PKG._lib.load()
+    rc = lib.pa_decode(*_decode_args(heads=30))
+    assert rc == -1
+    assert "divisible" in lib.pa_last_error().decode()
+    assert lib.pa_decode(*_decode_args(head_dim=64)) == -2
+    assert "head_dim" in lib.pa_last_error().decode()
+    assert lib.pa_decode(*_decode_args(heads=64, kv_heads=2)) == -2   # 32 q heads per kv head
+    assert lib.pa_decode(*_decode_args(batch=0)) == 0                  # nothing to do
+    assert lib.pa_decode(*_decode_args(page_size=0)) == -1
+
+
+def test_prefill_rejects_bad_arguments_without_a_device():
+    lib = PKG._lib.load()
+    args = [None, 2048, 128, None, None, 16, 256, 262144, 1024, 128, None, 4, 4, None, None, None,
+            2, 100, 64, 16, 8, 128, 0.088, 0.0, None, 2048, 128, None]
+    bad_div = list(args)
+    bad_div[19] = 15
+    assert lib.pa_prefill(*bad_div) == -1
+    bad_dim = list(args)
+    bad_dim[21] = 96
+    assert lib.pa_prefill(*bad_dim) == -2
+    empty = list(args)
+    empty[17] = 0   # num_tokens == 0: nothing to write
+    assert lib.pa_prefill(*empty) == 0
+    nulls = list(args)  # valid sizes but null pointers
+    assert lib.pa_prefill(*nulls) == -1
+    assert "null" in lib.pa_last_error().decode()
+
+
+def test_kv_store_edge_arguments_without_a_device():
+    lib = PKG._lib.load()
+    base = [None, 1024, 128, None, 1024, 128, None, 0, 8, 128, None, None, 16, 256, 262144, 1024, 128, None]
+    assert lib.pa_kv_store(*base) == 0                 # zero tokens
+    neg = list(base)
+    neg[7] = -1
+    assert lib.pa_kv_store(*neg) == -1
+    nulls = list(base)
+    nulls[7] = 5
+    assert lib.pa_kv_store(*nulls) == -1
+
+
+def test_decode_workspace_size():
+    lib = PKG._lib.load()
+    # 512-token work items: ceil(32 pages * 256 / 512) = 16 chunks per sequence
+    assert lib.pa_decode_workspace_size(256, 32, 128, 32, 256) == 256 * 32 * 16 * (128 + 2) * 4
+    assert lib.pa_decode_workspace_size(0, 32, 128, 32, 256) == 0
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """No silent fallback: a missing .so is an error, not a CPU path."""
+    import importlib
+    lib_mod = importlib.import_module("vllm_jax_amd._lib")
+    monkeypatch.setattr(lib_mod, "_LIB", None)
+    monkeypatch.setattr(lib_mod, "lib_path", lambda: str(tmp_path / "missing.so"))
+    with pytest.raises(RuntimeError, match="missing"):
+        lib_mod.load()

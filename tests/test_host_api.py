@@ -1,0 +1,105 @@
+"""Host-side behaviour of the reference-compatible entry points: argument
+checks raise the reference's ValueError messages (prefill_paged_attention.py:
+189-207,430-431; decode_paged_attention.py:346-372) before any device work,
+and CPU tensors are refused rather than computed on the host."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import PKG
+
+
+def _prefill_args(t=10, h=16, hkv=8, d=128, nb=4, bs=16, b=2):
+    q = torch.zeros(t, h, d, dtype=torch.bfloat16)
+    kp = torch.zeros(hkv, nb, bs, d, dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    bt = torch.zeros(b, 2, dtype=torch.int32)
+    cu = torch.tensor([0, 4, t][:b + 1], dtype=torch.int32)
+    sm = torch.zeros(t, dtype=torch.int32)
+    pos = torch.zeros(t, dtype=torch.int32)
+    return [q, kp, vp, bt, cu, sm, pos]
+
+
+def test_prefill_shape_errors_match_reference():
+    a = _prefill_args()
+    with pytest.raises(ValueError, match="k_pages and v_pages must have the same shape"):
+        PKG.prefill_paged_attention(a[0], a[1], a[2][:, :2], *a[3:], max_seqlen_bucket=8)
+    with pytest.raises(ValueError, match="Number of Q heads must be divisible by number of KV heads"):
+        b = _prefill_args(h=12, hkv=8)
+        PKG.prefill_paged_attention(*b, max_seqlen_bucket=8)
+    with pytest.raises(ValueError, match="head_dim of Q must be the same as that of K/V"):
+        b = _prefill_args()
+        PKG.prefill_paged_attention(b[0][..., :64], *b[1:], max_seqlen_bucket=8)
+    with pytest.raises(ValueError, match=r"cu_seqlens must have shape \[batch \+ 1\]"):
+        b = _prefill_args()
+        PKG.prefill_paged_attention(*b[:4], b[4][:2], *b[5:], max_seqlen_bucket=8)
+    with pytest.raises(ValueError, match="block_tables must be int32"):
+        b = _prefill_args()
+        PKG.prefill_paged_attention(*b[:3], b[3].long(), *b[4:], max_seqlen_bucket=8)
+    with pytest.raises(ValueError, match="block_h must divisible by 16"):
+        PKG.prefill_paged_attention(*_prefill_args(), max_seqlen_bucket=8, block_h=8)
+    with pytest.raises(NotImplementedError):
+        PKG.prefill_paged_attention(*_prefill_args(), max_seqlen_bucket=8, k_scales_pages=torch.zeros(1))
+
+
+def test_prefill_refuses_host_tensors():
+    with pytest.raises(ValueError, match="HIP device"):
+        PKG.prefill_paged_attention(*_prefill_args(), max_seqlen_bucket=8)
+
+
+def _decode_args(b=3, h=32, hkv=8, d=128, nb=8, bs=16, p=4):
+    q = torch.zeros(b, h, d, dtype=torch.bfloat16)
+    kp = torch.zeros(hkv, nb, bs, d, dtype=torch.bfloat16)
+    bt = torch.zeros(b, p, dtype=torch.int32)
+    lens = torch.ones(b, dtype=torch.int32)
+    return [q, kp, kp.clone(), bt, lens]
+
+
+def test_decode_shape_errors_match_reference():
+    a = _decode_args()
+    with pytest.raises(ValueError, match="k_pages and v_pages must have the same shape"):
+        PKG.decode_paged_attention(a[0], a[1], a[2][:, :3], a[3], a[4])
+    with pytest.raises(ValueError, match="Number of Q heads must be divisible"):
+        PKG.decode_paged_attention(*_decode_args(h=30))
+    with pytest.raises(ValueError, match="head_dim of Q must be the same"):
+        PKG.decode_paged_attention(a[0][..., :64], *a[1:])
+    with pytest.raises(ValueError, match="`block_tables` and `q` must have the same batch size"):
+        PKG.decode_paged_attention(a[0], a[1], a[2], a[3][:2], a[4])
+    with pytest.raises(ValueError, match="`lengths` and `q` must have the same batch size"):
+        PKG.decode_paged_attention(*a[:4], a[4][:2])
+    with pytest.raises(ValueError, match="The dtype of `lengths` must be int32"):
+        PKG.decode_paged_attention(*a[:4], a[4].long())
+    with pytest.raises(ValueError, match="block_h must divisible by 16"):
+        PKG.decode_paged_attention(*a, block_h=24)
+    with pytest.raises(NotImplementedError):
+        PKG.decode_paged_attention(*a, k_scales_pages=torch.zeros(1))
+
+
+def test_decode_refuses_host_tensors():
+    with pytest.raises(ValueError, match="HIP device"):
+        PKG.decode_paged_attention(*_decode_args())
+
+
+def test_kv_store_validates_shapes_and_device():
+    cache = torch.zeros(2, 4, 16, 8, 128, dtype=torch.bfloat16)
+    k = torch.zeros(5, 8, 128, dtype=torch.bfloat16)
+    sm = torch.zeros(5, dtype=torch.int32)
+    with pytest.raises(ValueError, match="HIP device"):
+        PKG.update_kv_cache(cache, sm, k, k)
+
+
+def test_attention_metadata_types_mirror_reference():
+    import dataclasses
+    d = [f.name for f in dataclasses.fields(PKG.DecodeAttentionMetadata)]
+    assert d == ["input_positions", "slot_mapping", "block_tables", "context_lens"]      # qwen3.py:17-22
+    p = [f.name for f in dataclasses.fields(PKG.PrefillAttentionMetadata)]
+    assert p == ["input_positions", "slot_mapping", "block_tables", "cu_seqlens_q", "cu_seqlens_k",
+                 "max_seqlen_q", "max_seqlen_k", "max_seqlen_bucket"]                        # qwen3.py:25-34
+
+
+def test_bf16_scale_constants():
+    from vllm_jax_amd.kernels._common import inv_sqrt_head_dim_bf16, bf16_round
+    assert inv_sqrt_head_dim_bf16(128) == 0.08837890625        # bf16(1/sqrt(128))
+    assert bf16_round(128 ** 0.5) == 11.3125                    # bf16(sqrt(128)), qwen3.py:207

@@ -1,0 +1,329 @@
+"""Pins of the CPU oracle (oracle/paged_attention_oracle.py).
+
+The reference (JAX/Pallas) cannot run here, so every oracle function is
+checked against something independent of its own formula:
+
+* bf16 conversion    -- torch's float32 -> bfloat16 cast (round to nearest even);
+* kv_store / gather  -- their closed forms, element by element;
+* prefill / decode   -- float64 brute force on tiny inputs, special cases that
+                        reduce to textbook results (one key -> v_0, equal keys
+                        -> mean(v), empty -> 0), and invariants (block
+                        relabelling, split count, prefix truncation,
+                        prefill-last-row == decode);
+* mutation checks    -- a planted mistake (wrong kv head, missing scale,
+                        swapped K/V, wrong block) must fail the same checks.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged_attention_oracle as ora
+
+TOL = 2e-2   # bf16 output tolerance of the path
+BRUTE_TOL = 1.2e-2  # oracle (bf16 P and partials, reference algebra) vs float64
+
+
+def _bf16(rng, shape, scale=0.5):
+    return ora.f32_to_bf16(rng.standard_normal(shape).astype(np.float32) * scale)
+
+
+def _pool(rng, nb, bs, hkv, d=128):
+    return _bf16(rng, (nb, bs, hkv, d)), _bf16(rng, (nb, bs, hkv, d))
+
+
+def _tables(rng, lens, bs, nb):
+    p = max(1, max(-(-int(n) // bs) for n in lens))
+    perm = rng.permutation(nb)
+    bt = np.full((len(lens), p), -1, np.int32)
+    c = 0
+    for b, n in enumerate(lens):
+        k = -(-int(n) // bs)
+        bt[b, :k] = perm[c:c + k]
+        c += k
+    return bt
+
+
+# ---------------------------------------------------------------------------
+# bf16
+# ---------------------------------------------------------------------------
+def test_bf16_matches_torch_round_to_nearest_even():
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-30, 30, 20000),
+        np.array([0.0, -0.0, 1.0, 1.00390625, 1.01171875, 65504.0, 3.3895314e38, 1e-40, -1e-40,
+                  np.inf, -np.inf], np.float32),
+        # exact ties between two bf16 values: must round to even
+        (np.arange(1, 2000, dtype=np.uint32) << 16 | 0x8000).view(np.float32),
+    ])
+    ours = ora.f32_to_bf16(x)
+    theirs = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(ours, theirs)
+    assert np.array_equal(ora.bf16_to_f32(ours), torch.from_numpy(x).to(torch.bfloat16).float().numpy())
+
+
+def test_bf16_nan_stays_nan():
+    x = np.array([np.nan, -np.nan], np.float32)
+    assert np.isnan(ora.bf16_to_f32(ora.f32_to_bf16(x))).all()
+
+
+# ---------------------------------------------------------------------------
+# KV store and gather: closed forms
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("nb,bs,hkv,t", [(8, 16, 2, 50), (4, 256, 8, 300), (3, 5, 1, 15)])
+def test_kv_store_closed_form(nb, bs, hkv, t):
+    rng = np.random.default_rng(t)
+    kc, vc = _pool(rng, nb, bs, hkv)
+    k = _bf16(rng, (t, hkv, 128))
+    v = _bf16(rng, (t, hkv, 128))
+    slots = rng.permutation(nb * bs)[:t].astype(np.int32)
+    slots[::5] = -1                    # padding tokens
+    slots[1] = nb * bs + 3             # past the pool: dropped
+    k2, v2 = ora.kv_store(kc, vc, k, v, slots)
+    written = np.zeros(nb * bs, bool)
+    for i, s in enumerate(slots):
+        if 0 <= s < nb * bs:
+            assert np.array_equal(k2[s // bs, s % bs], k[i])
+            assert np.array_equal(v2[s // bs, s % bs], v[i])
+            written[s] = True
+    keep = ~written.reshape(nb, bs)
+    assert np.array_equal(k2[keep], kc[keep]) and np.array_equal(v2[keep], vc[keep])
+    # inputs untouched
+    assert not np.shares_memory(k2, kc)
+
+
+def test_gather_closed_form():
+    rng = np.random.default_rng(1)
+    nb, bs, hkv = 16, 16, 2
+    cache, _ = _pool(rng, nb, bs, hkv)
+    lens = np.array([0, 1, 16, 17, 45], np.int32)
+    bt = _tables(rng, lens, bs, nb)
+    bt[0, 0] = -1
+    ctx = ora.gather_kv(cache, bt, lens)
+    for b, n in enumerate(lens):
+        for j in range(bt.shape[1] * bs):
+            want = cache[max(bt[b, j // bs], 0), j % bs] if j < n else np.zeros((hkv, 128), np.uint16)
+            assert np.array_equal(ctx[b, j], want)
+
+
+# ---------------------------------------------------------------------------
+# prefill / decode vs float64 brute force
+# ---------------------------------------------------------------------------
+def _prefill_case(rng, lens, h, hkv, bs, prefix=None):
+    lens = np.asarray(lens)
+    prefix = np.zeros_like(lens) if prefix is None else np.asarray(prefix)
+    kv_lens = lens + prefix
+    nb = int(sum(-(-int(n) // bs) for n in kv_lens)) + 2
+    kc, vc = _pool(rng, nb, bs, hkv)
+    bt = _tables(rng, kv_lens, bs, nb)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cuk = np.concatenate([[0], np.cumsum(kv_lens)]).astype(np.int32)
+    pos = np.concatenate([np.arange(p, p + n) for p, n in zip(prefix, lens)]).astype(np.int32)
+    q = _bf16(rng, (int(cu[-1]), h, 128))
+    return q, kc, vc, bt, cu, cuk, pos, kv_lens
+
+
+@pytest.mark.parametrize("lens,h,hkv,bs", [
+    ([5, 1, 33], 4, 2, 16), ([40], 8, 8, 32), ([17, 30], 16, 2, 8), ([64, 3], 4, 1, 64)])
+def test_prefill_vs_brute_force(lens, h, hkv, bs):
+    rng = np.random.default_rng(sum(lens) + h)
+    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, lens, h, hkv, bs)
+    got = ora.bf16_to_f32(ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3),
+                                                bt, cu, pos))
+    kctx, vctx = ora.gather_kv(kc, bt, kvl), ora.gather_kv(vc, bt, kvl)
+    # the reference scales q in bf16 by bf16(1/sqrt(d)) (prefill...:60)
+    sc = float(ora.round_bf16(np.float32(1 / math.sqrt(128))).reshape(-1)[0])
+    qs = ora.f32_to_bf16(ora.round_bf16(ora.bf16_to_f32(q) * np.float32(sc)))
+    want = ora.dense_prefill_f64(qs, kctx, vctx, cu, pos, scale=1.0)
+    assert np.abs(got - want).max() <= BRUTE_TOL
+
+
+def test_prefill_prefix_vs_brute_force():
+    rng = np.random.default_rng(7)
+    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, [12, 30, 1], 8, 2, 16, prefix=[0, 20, 47])
+    got = ora.bf16_to_f32(ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3),
+                                                bt, cu, pos, cu_seqlens_k=cuk))
+    kctx, vctx = ora.gather_kv(kc, bt, kvl), ora.gather_kv(vc, bt, kvl)
+    sc = float(ora.round_bf16(np.float32(1 / math.sqrt(128))).reshape(-1)[0])
+    qs = ora.f32_to_bf16(ora.round_bf16(ora.bf16_to_f32(q) * np.float32(sc)))
+    want = ora.dense_prefill_f64(qs, kctx, vctx, cu, pos, cu_seqlens_k=cuk, scale=1.0)
+    assert np.abs(got - want).max() <= BRUTE_TOL
+
+
+@pytest.mark.parametrize("lens,h,hkv,bs", [([1, 15, 16, 17, 60, 0], 8, 2, 16), ([300, 40], 32, 8, 256)])
+def test_decode_vs_brute_force(lens, h, hkv, bs):
+    rng = np.random.default_rng(len(lens) + h)
+    nb = int(sum(-(-int(n) // bs) for n in lens)) + 1
+    kc, vc = _pool(rng, nb, bs, hkv)
+    bt = _tables(rng, lens, bs, nb)
+    q = _bf16(rng, (len(lens), h, 128))
+    got = ora.bf16_to_f32(ora.decode_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, lens))
+    want = ora.dense_decode_f64(q, ora.gather_kv(kc, bt, lens), ora.gather_kv(vc, bt, lens), lens)
+    assert np.abs(got - want).max() <= BRUTE_TOL
+    assert not got[np.asarray(lens) == 0].any()
+
+
+def test_decode_soft_cap_vs_brute_force():
+    rng = np.random.default_rng(3)
+    lens = [100, 7]
+    kc, vc = _pool(rng, 8, 16, 2)
+    bt = _tables(rng, lens, 16, 8)
+    q = _bf16(rng, (2, 4, 128), scale=2.0)
+    got = ora.bf16_to_f32(ora.decode_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, lens,
+                                               soft_cap=3.0))
+    want = ora.dense_decode_f64(q, ora.gather_kv(kc, bt, lens), ora.gather_kv(vc, bt, lens), lens, soft_cap=3.0)
+    assert np.abs(got - want).max() <= BRUTE_TOL
+
+
+# ---------------------------------------------------------------------------
+# special cases
+# ---------------------------------------------------------------------------
+def test_decode_single_key_returns_v0_exactly():
+    rng = np.random.default_rng(4)
+    kc, vc = _pool(rng, 4, 16, 2)
+    bt = np.array([[2], [0]], np.int32)
+    q = _bf16(rng, (2, 4, 128), scale=3.0)
+    got = ora.decode_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, [1, 1])
+    for b in range(2):
+        for hh in range(4):
+            assert np.array_equal(got[b, hh], vc[bt[b, 0], 0, hh // 2])
+
+
+def test_prefill_first_row_returns_v0_exactly():
+    rng = np.random.default_rng(5)
+    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, [9, 4], 4, 2, 16)
+    got = ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, pos)
+    for b in range(2):
+        row = cu[b]
+        for hh in range(4):
+            assert np.array_equal(got[row, hh], vc[bt[b, 0], 0, hh // 2])
+
+
+def test_equal_keys_give_mean_of_values():
+    rng = np.random.default_rng(6)
+    kc, vc = _pool(rng, 2, 64, 1)
+    kc[:] = kc[0, 0]                     # every key identical
+    q = _bf16(rng, (1, 2, 128))
+    bt = np.array([[1, 0]], np.int32)
+    n = 100
+    got = ora.bf16_to_f32(ora.decode_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, [n]))
+    ctx = ora.bf16_to_f32(ora.gather_kv(vc, bt, [n]))[0, :n, 0]
+    assert np.abs(got[0] - ctx.mean(0)[None]).max() <= 1e-2
+
+
+def test_rows_outside_sequences_are_zero():
+    rng = np.random.default_rng(8)
+    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, [5, 6], 4, 2, 16)
+    qpad = np.concatenate([q, _bf16(rng, (5, 4, 128))])
+    pos = np.concatenate([pos, np.zeros(5, np.int32)])
+    got = ora.prefill_attention(qpad, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, pos)
+    assert not got[11:].any() and got[:11].any()
+
+
+# ---------------------------------------------------------------------------
+# invariants
+# ---------------------------------------------------------------------------
+def test_block_relabelling_is_bit_identical():
+    rng = np.random.default_rng(9)
+    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, [50, 70], 8, 2, 16)
+    a = ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, pos)
+    perm = rng.permutation(kc.shape[0])
+    kc2, vc2 = np.empty_like(kc), np.empty_like(vc)
+    kc2[perm], vc2[perm] = kc, vc
+    bt2 = np.where(bt >= 0, perm[np.maximum(bt, 0)], -1).astype(np.int32)
+    b = ora.prefill_attention(q, kc2.transpose(2, 0, 1, 3), vc2.transpose(2, 0, 1, 3), bt2, cu, pos)
+    assert np.array_equal(a, b)
+
+
+def test_split_count_changes_only_rounding():
+    rng = np.random.default_rng(10)
+    lens = [700, 300]
+    kc, vc = _pool(rng, 12, 128, 2)
+    bt = _tables(rng, lens, 128, 12)
+    bt = np.concatenate([bt, np.full((2, 8 - bt.shape[1]), -1, np.int32)], 1)
+    q = _bf16(rng, (2, 4, 128))
+    outs = [ora.bf16_to_f32(ora.decode_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, lens,
+                                                 k_splits=ks)) for ks in (1, 2, 4, 8)]
+    for o in outs[1:]:
+        assert np.abs(o - outs[0]).max() <= TOL
+
+
+def test_prefix_truncation_does_not_change_earlier_rows():
+    rng = np.random.default_rng(11)
+    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, [40], 4, 2, 16)
+    a = ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, pos)
+    kc2, vc2 = kc.copy(), vc.copy()
+    # scramble every kv token at index >= 25 (rows < 25 must not see them)
+    for j in range(25, 40):
+        kc2[bt[0, j // 16], j % 16] = _bf16(rng, (2, 128))
+        vc2[bt[0, j // 16], j % 16] = _bf16(rng, (2, 128))
+    b = ora.prefill_attention(q, kc2.transpose(2, 0, 1, 3), vc2.transpose(2, 0, 1, 3), bt, cu, pos)
+    assert np.array_equal(a[:25], b[:25]) and not np.array_equal(a[25:], b[25:])
+
+
+def test_prefill_last_row_matches_decode():
+    rng = np.random.default_rng(12)
+    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, [200], 8, 2, 16)
+    bt = np.concatenate([bt, np.full((1, 16 - bt.shape[1]), -1, np.int32)], 1)  # decode splits need 16 | width
+    pre = ora.bf16_to_f32(ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, pos))
+    sc = float(ora.round_bf16(np.float32(1 / math.sqrt(128))).reshape(-1)[0])
+    qs = ora.f32_to_bf16(ora.round_bf16(ora.bf16_to_f32(q[-1:]) * np.float32(sc)))
+    dec = ora.bf16_to_f32(ora.decode_attention(qs, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, [200]))
+    assert np.abs(pre[-1] - dec[0]).max() <= TOL
+
+
+def test_gqa_mapping_matches_repeat():
+    """q head h reads kv head h // G, i.e. the same as jnp.repeat of K/V over heads (qwen3.py:81-86)."""
+    rng = np.random.default_rng(13)
+    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, [30], 8, 2, 16)
+    a = ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, pos)
+    kr, vr = np.repeat(kc, 4, axis=2), np.repeat(vc, 4, axis=2)
+    b = ora.prefill_attention(q, kr.transpose(2, 0, 1, 3), vr.transpose(2, 0, 1, 3), bt, cu, pos)
+    assert np.array_equal(a, b)
+
+
+# ---------------------------------------------------------------------------
+# mutation checks: a planted mistake must fail the pins above
+# ---------------------------------------------------------------------------
+def test_planted_mistakes_are_caught():
+    rng = np.random.default_rng(14)
+    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, [40, 20], 8, 2, 16)
+    kctx, vctx = ora.gather_kv(kc, bt, kvl), ora.gather_kv(vc, bt, kvl)
+    sc = float(ora.round_bf16(np.float32(1 / math.sqrt(128))).reshape(-1)[0])
+    qs = ora.f32_to_bf16(ora.round_bf16(ora.bf16_to_f32(q) * np.float32(sc)))
+    want = ora.dense_prefill_f64(qs, kctx, vctx, cu, pos, scale=1.0)
+
+    def err(out):
+        return np.abs(ora.bf16_to_f32(out) - want).max()
+
+    good = ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, pos)
+    assert err(good) <= BRUTE_TOL
+    # swapped K and V
+    assert err(ora.prefill_attention(q, vc.transpose(2, 0, 1, 3), kc.transpose(2, 0, 1, 3), bt, cu, pos)) > 0.1
+    # wrong GQA mapping (kv heads swapped)
+    assert err(ora.prefill_attention(q, kc[:, :, ::-1].transpose(2, 0, 1, 3), vc[:, :, ::-1].transpose(2, 0, 1, 3),
+                                     bt, cu, pos)) > 0.1
+    # wrong block (tables shifted by one entry)
+    bt_bad = np.roll(bt, 1, axis=1)
+    assert err(ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt_bad, cu, pos)) > 0.1
+    # missing 1/sqrt(d) scale (q pre-multiplied by sqrt(d))
+    q_big = ora.f32_to_bf16(ora.bf16_to_f32(q) * np.float32(math.sqrt(128)))
+    assert err(ora.prefill_attention(q_big, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, pos)) > 0.1
+    # off-by-one causal mask: every row but a sequence's first sees one key fewer
+    pos_bad = pos.copy()
+    first = np.zeros(len(pos), bool)
+    first[cu[:-1]] = True
+    pos_bad[~first] -= 1
+    assert err(ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, pos_bad)) > 0.05
+    # a uniform shift of all positions is NOT a mistake: the mask is relative
+    assert err(ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, pos + 5)) <= BRUTE_TOL
+
+
+def test_visible_pairs_closed_form():
+    cu = np.array([0, 17, 145, 445, 956])
+    assert ora.prefill_visible_pairs(cu) == sum(n * (n + 1) // 2 for n in (17, 128, 300, 511)) == 184375
+    cuk = np.array([0, 27, 155, 455, 966])  # first sequence: prefix 10
+    assert ora.prefill_visible_pairs(cu, cuk) == 184375 + 17 * 10
