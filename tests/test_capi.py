@@ -96,8 +96,8 @@ def test_kv_store_edge_arguments_without_a_device():
 
 def test_decode_workspace_size():
     lib = PKG._lib.load()
-    # 512-token work items: ceil(32 pages * 256 / 512) = 16 chunks per sequence
-    assert lib.pa_decode_workspace_size(256, 32, 128, 32, 256) == 256 * 32 * 16 * (128 + 2) * 4
+    # 1024-token work items: ceil(32 pages * 256 / 1024) = 8 chunks per sequence
+    assert lib.pa_decode_workspace_size(256, 32, 128, 32, 256) == 256 * 32 * 8 * (128 + 2) * 4
     assert lib.pa_decode_workspace_size(0, 32, 128, 32, 256) == 0
 
 

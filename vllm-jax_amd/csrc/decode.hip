@@ -1,6 +1,6 @@
 // Split-K paged GQA decode for gfx950.
 //
-// Work item = (sequence b, kv head, chunk of kDecodeChunk context tokens),
+// Work item = (sequence b, kv head, chunk of kDecodeChunk = 1024 context tokens),
 // one wavefront per item, four independent items per 256-thread workgroup.
 // Each wave streams its chunk 32 tokens at a time straight from HBM into
 // registers (no LDS):
@@ -27,7 +27,7 @@
 namespace pa {
 
 constexpr int kHeadDim = 128;
-constexpr int kDecodeChunk = 512;  // tokens per work item
+constexpr int kDecodeChunk = 1024;  // tokens per work item
 constexpr int kDecodeStep = 32;    // tokens per inner iteration
 constexpr int kDecodeWaves = 4;    // items per workgroup
 
@@ -49,6 +49,13 @@ struct DecodeParams {
   float* ws_o;        // [batch, Hkv, n_chunks, group, d]
   float* ws_ml;       // [batch, Hkv, n_chunks, group, 2] (max log2, sum)
 };
+
+// V rows are read exactly once and in whole 256-byte rows: stream them past
+// the caches.  K rows are read 64 bytes per row per instruction, so their
+// 128-byte lines are kept cacheable for the instruction that reads the rest.
+__device__ __forceinline__ u32x4 ld16_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
 
 // Offset of token `t` of a sequence in the pool (without the head offset).
 __device__ __forceinline__ int64_t token_offset(const DecodeParams& p, const int32_t* bt_row, int t) {
@@ -130,7 +137,7 @@ decode_split_kernel(DecodeParams p) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int t = min(t0 + vtok(i), len - 1);
-        vreg[i] = ld16(p.v_cache + pbase + (int64_t)(t - pstart) * p.slot_stride + 8 * n);
+        vreg[i] = ld16_stream(p.v_cache + pbase + (int64_t)(t - pstart) * p.slot_stride + 8 * n);
       }
     } else {
 #pragma unroll
@@ -143,7 +150,7 @@ decode_split_kernel(DecodeParams p) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int t = min(t0 + vtok(i), len - 1);
-        vreg[i] = ld16(p.v_cache + token_offset(p, bt_row, t) + head_off + 8 * n);
+        vreg[i] = ld16_stream(p.v_cache + token_offset(p, bt_row, t) + head_off + 8 * n);
       }
     }
   };
