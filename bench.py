@@ -213,7 +213,8 @@ def run_gpu(args):
                 "peak": HBM_PEAK_GBS,
                 "unit": "GB/s",
                 "frac": round(d_gbs_kernel / HBM_PEAK_GBS, 4),
-                "traffic": traffic.get("decode_split_kernel"),
+                "traffic": (traffic["decode_split_kernel"] + traffic["decode_merge_kernel"]
+                            if "decode_split_kernel" in traffic and "decode_merge_kernel" in traffic else None),
             },
         },
         "wall_s_timed": round(wall, 3),

@@ -26,7 +26,7 @@
  * are skipped by the KV store.
  *
  * Supported shapes: head_dim == 128, num_heads % num_kv_heads == 0,
- * num_heads / num_kv_heads <= 16 for decode and <= 128 for prefill.
+ * num_heads / num_kv_heads <= 16 for decode and <= 256 for prefill.
  */
 #ifndef VLLM_JAX_AMD_PAGED_ATTENTION_H_
 #define VLLM_JAX_AMD_PAGED_ATTENTION_H_
