@@ -41,9 +41,15 @@ def _run_and_check(pkg, dev, db, seed, *, seqs=None, soft_cap=None):
     ([300, 4000, 17], 16, 8, 256),                          # Qwen3-0.6B heads
     ([70, 500], 16, 16, 32),                                # MHA (G = 1)
     ([129, 1024], 16, 1, 64),                               # G = 16
+    ([1100, 2049, 64, 1024], 8, 2, 16),                     # 16-token pages: 64 page ids per chunk
+    ([5, 40, 1500, 2100], 8, 2, 24),                        # page size not a multiple of 16
+    ([2048, 2049, 4097, 6000], 32, 8, 256),                 # chunk boundaries
 ])
 def test_decode_small(pkg, dev, lens, h, hkv, bs):
-    db = wl.make_decode(lens, num_heads=h, num_kv_heads=hkv, page_size=bs, rng=np.random.default_rng(len(lens)))
+    # power-of-two table width: the oracle keeps the reference's split divisibility rules
+    width = 1 << (max(-(-n // bs) for n in lens) - 1).bit_length()
+    db = wl.make_decode(lens, num_heads=h, num_kv_heads=hkv, page_size=bs, rng=np.random.default_rng(len(lens)),
+                        table_width=width)
     _run_and_check(pkg, dev, db, seed=3)
 
 

@@ -1,35 +1,52 @@
 // Split-K paged GQA decode for gfx950.
 //
-// Work item = (sequence b, kv head, chunk of kDecodeChunk = 1024 context tokens),
-// one wavefront per item, four independent items per 256-thread workgroup.
-// Each wave streams its chunk 32 tokens at a time straight from HBM into
-// registers (no LDS):
+// Workgroup = (sequence b, kv head, chunk of 2048 context tokens; 1024 when
+// pages hold 16 tokens), four wavefronts.  The chunk is cut into 16-token steps dealt round-robin to
+// the waves (wave w takes steps w, w+4, ...), so the four waves stream
+// adjacent token rows and finish together.  Each wave keeps kDecodeBufs steps
+// of K and V in flight in VGPRs: the loads of step i+kDecodeBufs are issued as
+// soon as step i has been consumed, so HBM always sees several 8 KiB requests
+// per wave.  Per step:
 //
-//   S^T[t][q] = K[t][:] . Q[q][:]          two v_mfma_f32_16x16x32_bf16 tiles
+//   S^T[t][q] = K[t][:] . Q[q][:]          4 x v_mfma_f32_16x16x32_bf16
 //                                           (16 tokens x 16 q columns, K = d)
-//   online softmax per q column (lane-local after two permlane swaps)
-//   O^T[d][q] += V^T[d][t] . P^T[t][q]      eight 16x16x32 MFMAs (d = 128)
+//   online softmax per q column (lane-local after two permlane swaps; the
+//   accumulator is rescaled only when the running max grows by more than
+//   2^kDecodeSlack)
+//   O^T[d][q] += V^T[d][t] . P^T[t][q]      8 x v_mfma_f32_16x16x16_bf16
 //
-// Keeping the q heads of one kv head in the N dimension makes the softmax row
-// of a lane equal to its accumulator column, so rescaling O needs no lane
-// exchange.  V is loaded as 16-byte row pieces (each 16-lane group reads one
-// whole 256-byte token row per instruction) and transposed in registers with
-// v_perm_b32 into the MFMA A layout.  The M (d) dimension of the PV MFMA is
-// permuted so that M-tile j row m holds d = 8m + j: a lane then owns the 8
-// contiguous d values of its 16-byte load.
+// The q heads of one kv head sit in the N dimension, so the softmax row of a
+// lane is its accumulator column.  K is read as 64-byte row pieces in the MFMA
+// A layout; V as 16-byte pieces where each 16-lane group reads one whole
+// 256-byte token row, transposed in registers with v_perm_b32.  The M (d)
+// dimension of the PV MFMA is permuted so that M-tile j row m holds
+// d = 8m + j: a lane then owns the 8 contiguous d values of its V load.
 //
-// Partials (unnormalised o, running max in log2 units, running sum) go to a
-// caller-owned f32 workspace; decode_merge_kernel combines the chunks of a
-// sequence with the log-sum-exp rule of decode_paged_attention.py:274-282.
+// Workgroups are dealt round-robin to the 8 XCDs; the grid is renumbered so
+// that each XCD runs a contiguous range of (sequence, chunk, kv head) items.
+// The kv heads of one token row (adjacent in the pool) are then read by one
+// XCD at nearly the same time, which keeps HBM accesses close together:
+// measured 6.07 TB/s against 5.36 TB/s with the heads spread over all XCDs.
+//
+// The four waves combine (m, l, o) through LDS.  A sequence covered by one
+// chunk is finished right there; longer sequences leave one f32 partial per
+// chunk in the caller's workspace and decode_merge_kernel combines them with
+// the log-sum-exp rule of decode_paged_attention.py:274-282.
 #include "pa_common.h"
 #include "pa_errors.h"
 
 namespace pa {
 
 constexpr int kHeadDim = 128;
-constexpr int kDecodeChunk = 1024;  // tokens per work item
-constexpr int kDecodeStep = 32;    // tokens per inner iteration
-constexpr int kDecodeWaves = 4;    // items per workgroup
+constexpr int kDecodeStep = 16;     // tokens per wave step
+constexpr int kDecodeWaves = 4;     // waves per workgroup
+#ifndef PA_DECODE_BUFS
+#define PA_DECODE_BUFS 4
+#endif
+constexpr int kDecodeBufs = PA_DECODE_BUFS;  // steps in flight per wave
+constexpr float kDecodeSlack = 8.f;          // lazy-rescale threshold (log2 units)
+
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4v;
 
 struct DecodeParams {
   const uint16_t* q;
@@ -43,59 +60,83 @@ struct DecodeParams {
   int32_t pages_per_seq;
   const int32_t* lengths;
   int32_t batch, num_heads, num_kv_heads, group;
-  int32_t n_chunks;
+  int32_t chunk;     // tokens per workgroup
+  int32_t n_chunks;  // chunks of the widest block-table row
   float logit_scale;  // scale * log2(e) when soft_cap is off, else scale
   float soft_cap;     // <= 0: off
   float* ws_o;        // [batch, Hkv, n_chunks, group, d]
   float* ws_ml;       // [batch, Hkv, n_chunks, group, 2] (max log2, sum)
+  uint16_t* out;
+  int64_t out_bs, out_hs;
 };
 
-// V rows are read exactly once and in whole 256-byte rows: stream them past
+// V rows are read exactly once and as whole 256-byte rows: stream them past
 // the caches.  K rows are read 64 bytes per row per instruction, so their
-// 128-byte lines are kept cacheable for the instruction that reads the rest.
+// 128-byte lines stay cacheable for the instruction that reads the other half.
 __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
-// Offset of token `t` of a sequence in the pool (without the head offset).
-__device__ __forceinline__ int64_t token_offset(const DecodeParams& p, const int32_t* bt_row, int t) {
-  const int lp = t / p.page_size;
-  const int32_t page = safe_page(bt_row, lp, p.num_pages);
-  return (int64_t)page * p.page_stride + (int64_t)(t - lp * p.page_size) * p.slot_stride;
+__device__ __forceinline__ f32x4 mfma16k16(const bf16x4v& a, const bf16x4v& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ uint32_t perm_lo(uint32_t a, uint32_t b) {
-  // (a.lo16) | (b.lo16 << 16)
-  return __builtin_amdgcn_perm(b, a, 0x05040100u);
-}
-__device__ __forceinline__ uint32_t perm_hi(uint32_t a, uint32_t b) {
-  // (a.hi16) | (b.hi16 << 16)
-  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+// The bf16 halves selected by `hi` of a and b, packed as (a_half, b_half).
+__device__ __forceinline__ uint32_t pick2(uint32_t a, uint32_t b, bool hi) {
+  return hi ? __builtin_amdgcn_perm(b, a, 0x07060302u) : __builtin_amdgcn_perm(b, a, 0x05040100u);
 }
 
-template <bool kAligned>
-__global__ void __launch_bounds__(256)
+struct alignas(16) DecodeLds {
+  float o[kDecodeWaves][16][kHeadDim];
+  float m[kDecodeWaves][16];
+  float l[kDecodeWaves][16];
+};
+
+// Tokens per workgroup: the aligned path keeps the chunk's page ids in one
+// VGPR (one per lane), so a chunk spans at most 64 pages.
+__host__ __device__ inline int decode_chunk_tokens(int page_size) { return page_size >= 32 ? 2048 : 1024; }
+
+// kAligned: page_size % 16 == 0, so a 16-token step never crosses a page and
+// the chunk's page ids (at most 64) are read once, one per lane.
+template <bool kAligned, bool kSoftCap>
+__global__ void __launch_bounds__(256, 2)
 decode_split_kernel(DecodeParams p) {
+  __shared__ DecodeLds red;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int64_t item = (int64_t)blockIdx.x * kDecodeWaves + wave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hkv = p.num_kv_heads;
-  const int64_t n_items = (int64_t)p.batch * p.n_chunks * hkv;
-  if (item >= n_items) return;
-  const int kvh = (int)(item % hkv);
-  const int64_t rest = item / hkv;
-  const int chunk = (int)(rest % p.n_chunks);
-  const int b = (int)(rest / p.n_chunks);
+  // XCD x = blockIdx % 8 serves items [x*q8 + min(x, r8), ...) in order
+  int item;
+  {
+    const int nb = gridDim.x, x = blockIdx.x & 7, k = blockIdx.x >> 3;
+    const int q8 = nb >> 3, r8 = nb & 7;
+    item = x * q8 + min(x, r8) + k;  // a bijection of [0, nb)
+  }
+  const int kvh = item % hkv;
+  const int rest = item / hkv;
+  const int chunk = rest % p.n_chunks;
+  const int b = rest / p.n_chunks;
   // lengths past the block table's span are clamped to it (no read beyond the table row)
   const int len = min(p.lengths[b], p.pages_per_seq * p.page_size);
-  const int t_begin = chunk * kDecodeChunk;
-  if (t_begin >= len) return;
-  const int t_end = min(t_begin + kDecodeChunk, len);
+  const int t_begin = chunk * p.chunk;
+  if (t_begin >= len) return;  // uniform over the workgroup
+  const int t_end = min(t_begin + p.chunk, len);
+  const int n_steps = (t_end - t_begin + kDecodeStep - 1) / kDecodeStep;
+  const int my_steps = n_steps > wave ? (n_steps - wave + kDecodeWaves - 1) / kDecodeWaves : 0;
+  const int n_chunks_b = (len + p.chunk - 1) / p.chunk;
 
-  const int n = lane & 15;   // q column of S/O; also the d-chunk of V loads
-  const int g = lane >> 4;   // k group
+  const int n = lane & 15;  // q column of S/O; the d chunk of V loads; the token of K loads
+  const int g = lane >> 4;  // 16-lane group
   const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
   const int64_t head_off = (int64_t)kvh * p.head_stride;
+
+  // Page ids of the chunk, one per lane (aligned path).
+  const int lp_first = t_begin / p.page_size;
+  int32_t my_page = 0;
+  if constexpr (kAligned) {
+    const int lp = lp_first + lane;
+    if (lp < p.pages_per_seq) my_page = safe_page(bt_row, lp, p.num_pages);
+  }
 
   // Q^T operand: k-step s uses d chunk (4s + g) for both Q and K.
   bf16x8 qt[4];
@@ -115,141 +156,171 @@ decode_split_kernel(DecodeParams p) {
   float m_run = -1e30f;  // finite so that exp2(x - m) never sees inf - inf
   float l_run = 0.f;
 
-  // Token of V k-slot i of this lane's group within a 32-token step.
-  auto vtok = [&](int i) { return (i < 4 ? 4 * g + i : 16 + 4 * g + (i - 4)); };
+  u32x4 kb[kDecodeBufs][4], vb[kDecodeBufs][4];
 
-  u32x4 kreg[2][4], vreg[8];
-  auto load_step = [&](int t0) {
+  // Loads of wave step `ks` (tokens t0 .. t0+15) into one buffer.  Tokens past
+  // the sequence end are clamped onto its last token (same page in the aligned
+  // case), so no stale or NaN data reaches the accumulator.  A step past the
+  // wave's last one still issues its 8 loads, all of the first 256 bytes of q
+  // (cache hits): every buffer then sees the same number of loads issued
+  // after it, and the compiler waits for exactly the buffer being consumed.
+  auto issue = [&](u32x4 (&kd)[4], u32x4 (&vd)[4], int ks) __attribute__((always_inline)) {
+    const bool valid = ks < my_steps;  // uniform
+    const int t0 = t_begin + kDecodeStep * (kDecodeWaves * ks + wave);
+    const int lim = len - 1 - t0;  // >= 0 when valid
     if constexpr (kAligned) {
-      // A 32-token step never crosses a page; clamp tokens past the end onto
-      // the last valid one (same page) so no stale or NaN data is read.
-      const int lp = t0 / p.page_size;
-      const int32_t page = safe_page(bt_row, lp, p.num_pages);
-      const int64_t pbase = (int64_t)page * p.page_stride + head_off;
-      const int pstart = lp * p.page_size;
-#pragma unroll
-      for (int tile = 0; tile < 2; ++tile) {
-        const int t = min(t0 + 16 * tile + n, len - 1);
-        const uint16_t* row = p.k_cache + pbase + (int64_t)(t - pstart) * p.slot_stride;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) kreg[tile][s] = ld16(row + 8 * (4 * s + g));
+      const uint16_t* kbase = p.q;
+      const uint16_t* vbase = p.q;
+      int64_t rs = 0;
+      if (valid) {
+        const int lp = t0 / p.page_size;
+        const int32_t page = __builtin_amdgcn_readlane(my_page, lp - lp_first);
+        const int64_t base = (int64_t)page * p.page_stride +
+                             (int64_t)(t0 - lp * p.page_size) * p.slot_stride + head_off;
+        kbase = p.k_cache + base;
+        vbase = p.v_cache + base;
+        rs = p.slot_stride;
       }
+      const int64_t krow = (int64_t)min(n, lim) * rs;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int t = min(t0 + vtok(i), len - 1);
-        vreg[i] = ld16_stream(p.v_cache + pbase + (int64_t)(t - pstart) * p.slot_stride + 8 * n);
-      }
+      for (int s = 0; s < 4; ++s) kd[s] = ld16(kbase + krow + 8 * (4 * s + g));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vd[i] = ld16_stream(vbase + (int64_t)min(4 * g + i, lim) * rs + 8 * n);
     } else {
+      if (!valid) {
 #pragma unroll
-      for (int tile = 0; tile < 2; ++tile) {
-        const int t = min(t0 + 16 * tile + n, len - 1);
-        const uint16_t* row = p.k_cache + token_offset(p, bt_row, t) + head_off;
+        for (int s = 0; s < 4; ++s) kd[s] = ld16(p.q + 8 * (4 * s + g));
 #pragma unroll
-        for (int s = 0; s < 4; ++s) kreg[tile][s] = ld16(row + 8 * (4 * s + g));
+        for (int i = 0; i < 4; ++i) vd[i] = ld16_stream(p.q + 8 * n);
+        return;
       }
+      auto tok_off = [&](int t) {
+        const int lp = t / p.page_size;
+        const int32_t page = safe_page(bt_row, lp, p.num_pages);
+        return (int64_t)page * p.page_stride + (int64_t)(t - lp * p.page_size) * p.slot_stride + head_off;
+      };
+      const uint16_t* krow = p.k_cache + tok_off(t0 + min(n, lim));
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int t = min(t0 + vtok(i), len - 1);
-        vreg[i] = ld16_stream(p.v_cache + token_offset(p, bt_row, t) + head_off + 8 * n);
-      }
+      for (int s = 0; s < 4; ++s) kd[s] = ld16(krow + 8 * (4 * s + g));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vd[i] = ld16_stream(p.v_cache + tok_off(t0 + min(4 * g + i, lim)) + 8 * n);
     }
   };
 
-  load_step(t_begin);
-  for (int t0 = t_begin; t0 < t_end; t0 += kDecodeStep) {
-    u32x4 kc[2][4], vc[8];
+  auto consume = [&](const u32x4 (&kd)[4], const u32x4 (&vd)[4], int ks) __attribute__((always_inline)) {
+    const int t0 = t_begin + kDecodeStep * (kDecodeWaves * ks + wave);
+    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int tile = 0; tile < 2; ++tile)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) kc[tile][s] = kreg[tile][s];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) vc[i] = vreg[i];
-    if (t0 + kDecodeStep < t_end) load_step(t0 + kDecodeStep);
-
-    // ---- S^T = K . Q^T for tokens t0..t0+15 (sa) and t0+16..t0+31 (sb)
-    f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sb = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      sa = mfma16(as_bf16x8(kc[0][s]), qt[s], sa);
-      sb = mfma16(as_bf16x8(kc[1][s]), qt[s], sb);
-    }
-    // lane holds S[q = n][token t0 + 4g + i] (sa) and [t0 + 16 + 4g + i] (sb)
-    float x[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      x[i] = sa[i];
-      x[4 + i] = sb[i];
-    }
+    for (int s = 0; s < 4; ++s) sc = mfma16(as_bf16x8(kd[s]), qt[s], sc);
+    // lane holds S[q = n][token t0 + 4g + r]
+    float x[4];
     float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = x[i];
-      if (p.soft_cap > 0.f) v = p.soft_cap * tanhf(v * p.logit_scale / p.soft_cap) * kLog2e;
+    for (int r = 0; r < 4; ++r) {
+      float v = sc[r];
+      if constexpr (kSoftCap) v = p.soft_cap * tanhf(v * p.logit_scale / p.soft_cap) * kLog2e;
       else v = v * p.logit_scale;
-      const int t = t0 + vtok(i);
-      v = t < len ? v : -INFINITY;
-      x[i] = v;
+      v = t0 + 4 * g + r < len ? v : -INFINITY;
+      x[r] = v;
       mx = fmaxf(mx, v);
     }
     mx = max_xor16(mx);
     mx = max_xor32(mx);
-    const float m_new = fmaxf(m_run, mx);
-    const float corr = fast_exp2(m_run - m_new);
-    m_run = m_new;
-    float psum = 0.f;
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + kDecodeSlack)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float corr = fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= corr;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      x[i] = fast_exp2(x[i] - m_new);
-      psum += x[i];
+      for (int j = 0; j < 8; ++j) acc[j] = acc[j] * corr;
     }
-    l_run = l_run * corr + psum;
-    u32x4 pw;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      x[r] = fast_exp2(x[r] - m_run);
+      l_run += x[r];
+    }
+    u32x2 pw;
     pw[0] = pack_bf16x2(x[0], x[1]);
     pw[1] = pack_bf16x2(x[2], x[3]);
-    pw[2] = pack_bf16x2(x[4], x[5]);
-    pw[3] = pack_bf16x2(x[6], x[7]);
-    const bf16x8 pt = as_bf16x8(pw);
+    const bf16x4v pt = __builtin_bit_cast(bf16x4v, pw);
+    // V^T tile j: lane (n, g) supplies d = 8n + j of tokens 4g .. 4g+3
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      u32x2 a;
+      a[0] = pick2(vd[0][j >> 1], vd[1][j >> 1], j & 1);
+      a[1] = pick2(vd[2][j >> 1], vd[3][j >> 1], j & 1);
+      acc[j] = mfma16k16(__builtin_bit_cast(bf16x4v, a), pt, acc[j]);
+    }
+  };
 
-    // ---- transpose V pieces into the A layout of the 8 d-tiles
 #pragma unroll
-    for (int q2 = 0; q2 < 4; ++q2) {
-      u32x4 lo, hi;
+  for (int j = 0; j < kDecodeBufs; ++j) issue(kb[j], vb[j], j);
+  for (int k0 = 0; k0 < my_steps; k0 += kDecodeBufs) {
 #pragma unroll
-      for (int pp = 0; pp < 4; ++pp) {
-        lo[pp] = perm_lo(vc[2 * pp][q2], vc[2 * pp + 1][q2]);
-        hi[pp] = perm_hi(vc[2 * pp][q2], vc[2 * pp + 1][q2]);
-      }
-      acc[2 * q2] = acc[2 * q2] * corr;
-      acc[2 * q2 + 1] = acc[2 * q2 + 1] * corr;
-      acc[2 * q2] = mfma16(as_bf16x8(lo), pt, acc[2 * q2]);
-      acc[2 * q2 + 1] = mfma16(as_bf16x8(hi), pt, acc[2 * q2 + 1]);
+    for (int j = 0; j < kDecodeBufs; ++j) {
+      const int ks = k0 + j;
+      if (ks < my_steps) consume(kb[j], vb[j], ks);
+      issue(kb[j], vb[j], ks + kDecodeBufs);
     }
   }
 
+  // ---- combine the four waves through LDS
   l_run = sum_xor16(l_run);
   l_run = sum_xor32(l_run);
-
-  if (n < p.group) {
-    const int64_t part = (((int64_t)b * hkv + kvh) * p.n_chunks + chunk) * p.group + n;
-    float* dst = p.ws_o + part * kHeadDim + 32 * g;
-    // acc[j][r] = O^T[d = 32g + 8r + j][q = n]
+  // acc[j][r] = O^T[d = 8 * (4g + r) + j][q = n]
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      f32x4 lo = {acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
-      f32x4 hi = {acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
-      *reinterpret_cast<f32x4*>(dst + 8 * r) = lo;
-      *reinterpret_cast<f32x4*>(dst + 8 * r + 4) = hi;
+  for (int r = 0; r < 4; ++r) {
+    float* dst = &red.o[wave][n][32 * g + 8 * r];
+    *reinterpret_cast<f32x4*>(dst) = f32x4{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{acc[4][r], acc[5][r], acc[6][r], acc[7][r]};
+  }
+  if (g == 0) {
+    red.m[wave][n] = m_run;
+    red.l[wave][n] = l_run;
+  }
+  __syncthreads();
+  // wave w finishes d = 32w + 8g .. +7 of column n
+  float mm = red.m[0][n];
+#pragma unroll
+  for (int w = 1; w < kDecodeWaves; ++w) mm = fmaxf(mm, red.m[w][n]);
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float ll = 0.f;
+  const int d0 = 32 * wave + 8 * g;
+#pragma unroll
+  for (int w = 0; w < kDecodeWaves; ++w) {
+    const float sw = fast_exp2(red.m[w][n] - mm);
+    ll += sw * red.l[w][n];
+    const f32x4 a = *reinterpret_cast<const f32x4*>(&red.o[w][n][d0]);
+    const f32x4 c = *reinterpret_cast<const f32x4*>(&red.o[w][n][d0 + 4]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      o[i] += sw * a[i];
+      o[4 + i] += sw * c[i];
     }
-    if (g == 0) {
-      p.ws_ml[2 * part] = m_run;
-      p.ws_ml[2 * part + 1] = l_run;
+  }
+  if (n >= p.group) return;
+  if (n_chunks_b == 1) {
+    const float inv = 1.f / ll;  // ll >= 1: the chunk holds a visible token
+    u32x4 w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = pack_bf16x2(o[2 * i] * inv, o[2 * i + 1] * inv);
+    st16(p.out + (int64_t)b * p.out_bs + (int64_t)(kvh * p.group + n) * p.out_hs + d0, w);
+  } else {
+    const int64_t part = (((int64_t)b * hkv + kvh) * p.n_chunks + chunk) * p.group + n;
+    float* dst = p.ws_o + part * kHeadDim + d0;
+    *reinterpret_cast<f32x4*>(dst) = f32x4{o[0], o[1], o[2], o[3]};
+    *reinterpret_cast<f32x4*>(dst + 4) = f32x4{o[4], o[5], o[6], o[7]};
+    if (wave == 0 && g == 0) {
+      p.ws_ml[2 * part] = mm;
+      p.ws_ml[2 * part + 1] = ll;
     }
   }
 }
 
 // One wave per (sequence, q head): out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M).
+// Sequences of one chunk were finished by the split kernel; length 0 gives zeros.
 __global__ void __launch_bounds__(256)
-decode_merge_kernel(DecodeParams p, uint16_t* __restrict__ out, int64_t out_bs, int64_t out_hs) {
+decode_merge_kernel(DecodeParams p) {
   const int lane = threadIdx.x & 63;
   const int64_t pair = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (pair >= (int64_t)p.batch * p.num_heads) return;
@@ -258,7 +329,8 @@ decode_merge_kernel(DecodeParams p, uint16_t* __restrict__ out, int64_t out_bs, 
   const int kvh = h / p.group;
   const int qi = h - kvh * p.group;
   const int len = min(p.lengths[b], p.pages_per_seq * p.page_size);
-  const int nc = len > 0 ? min((len + kDecodeChunk - 1) / kDecodeChunk, p.n_chunks) : 0;
+  const int nc = len > 0 ? min((len + p.chunk - 1) / p.chunk, p.n_chunks) : 0;
+  if (nc == 1) return;
   const int64_t base = ((int64_t)b * p.num_kv_heads + kvh) * p.n_chunks;
   float mmax = -INFINITY;
   for (int c = 0; c < nc; ++c) mmax = fmaxf(mmax, p.ws_ml[2 * ((base + c) * p.group + qi)]);
@@ -272,13 +344,14 @@ decode_merge_kernel(DecodeParams p, uint16_t* __restrict__ out, int64_t out_bs, 
     o1 += o.y * w;
   }
   const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-  uint32_t* dst = reinterpret_cast<uint32_t*>(out + (int64_t)b * out_bs + (int64_t)h * out_hs) + lane;
+  uint32_t* dst = reinterpret_cast<uint32_t*>(p.out + (int64_t)b * p.out_bs + (int64_t)h * p.out_hs) + lane;
   *dst = pack_bf16x2(o0 * inv, o1 * inv);
 }
 
 static int decode_chunks(int32_t pages_per_seq, int32_t page_size) {
   const int64_t max_tokens = (int64_t)pages_per_seq * page_size;
-  return (int)((max_tokens + kDecodeChunk - 1) / kDecodeChunk);
+  const int chunk = decode_chunk_tokens(page_size);
+  return (int)((max_tokens + chunk - 1) / chunk);
 }
 
 }  // namespace pa
@@ -322,8 +395,10 @@ extern "C" int pa_decode(const uint16_t* q, int64_t q_batch_stride, int64_t q_he
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_decode: null pointer");
   const uintptr_t align_bits = (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out;
   if ((align_bits & 15u) || (q_batch_stride | q_head_stride | page_stride | slot_stride | head_stride) % 8 ||
-      (out_batch_stride | out_head_stride) % 2)
+      (out_batch_stride | out_head_stride) % 8)
     return fail(PA_ERR_UNSUPPORTED, "pa_decode: operands must be 16-byte aligned with strides multiple of 8");
+  if ((int64_t)pages_per_seq * page_size > 0x7fffffffLL)
+    return fail(PA_ERR_UNSUPPORTED, "pa_decode: block table spans more than 2^31 tokens");
   const size_t need = pa_decode_workspace_size(batch, num_heads, head_dim, pages_per_seq, page_size);
   if (pages_per_seq > 0 && (!workspace || workspace_bytes < need))
     return fail(PA_ERR_WORKSPACE, "pa_decode: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
@@ -347,28 +422,32 @@ extern "C" int pa_decode(const uint16_t* q, int64_t q_batch_stride, int64_t q_he
   prm.num_heads = num_heads;
   prm.num_kv_heads = num_kv_heads;
   prm.group = group;
+  prm.chunk = decode_chunk_tokens(page_size);
   prm.n_chunks = pages_per_seq > 0 ? decode_chunks(pages_per_seq, page_size) : 0;
   prm.soft_cap = soft_cap > 0.f ? soft_cap : 0.f;
   prm.logit_scale = prm.soft_cap > 0.f ? scale : scale * kLog2e;
   const size_t parts = (size_t)batch * num_heads * prm.n_chunks;
   prm.ws_o = reinterpret_cast<float*>(workspace);
   prm.ws_ml = prm.ws_o + parts * head_dim;
+  prm.out = out;
+  prm.out_bs = out_batch_stride;
+  prm.out_hs = out_head_stride;
 
   hipStream_t s = (hipStream_t)stream;
-  const int64_t items = (int64_t)batch * prm.n_chunks * num_kv_heads;
-  const int64_t blocks = (items + kDecodeWaves - 1) / kDecodeWaves;
+  const int64_t blocks = (int64_t)batch * prm.n_chunks * num_kv_heads;
   if (blocks > 0x7fffffff)
     return fail(PA_ERR_UNSUPPORTED, "pa_decode: grid of %lld workgroups too large", (long long)blocks);
   if (blocks > 0) {  // no table pages: every row is zero, only the merge pass runs
-    if (page_size % kDecodeStep == 0)
-      decode_split_kernel<true><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(prm);
-    else
-      decode_split_kernel<false><<<dim3((unsigned)blocks), dim3(256), 0, s>>>(prm);
+    const bool aligned = page_size % kDecodeStep == 0;
+    const dim3 grid((unsigned)blocks), block(64 * kDecodeWaves);
+    if (aligned && prm.soft_cap == 0.f) decode_split_kernel<true, false><<<grid, block, 0, s>>>(prm);
+    else if (aligned) decode_split_kernel<true, true><<<grid, block, 0, s>>>(prm);
+    else if (prm.soft_cap == 0.f) decode_split_kernel<false, false><<<grid, block, 0, s>>>(prm);
+    else decode_split_kernel<false, true><<<grid, block, 0, s>>>(prm);
     int rc = launch_status("pa_decode(split)");
     if (rc) return rc;
   }
   const int64_t pairs = (int64_t)batch * num_heads;
-  decode_merge_kernel<<<dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s>>>(prm, out, out_batch_stride,
-                                                                           out_head_stride);
+  decode_merge_kernel<<<dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s>>>(prm);
   return launch_status("pa_decode(merge)");
 }
