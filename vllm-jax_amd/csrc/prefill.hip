@@ -45,7 +45,10 @@ constexpr float kRescaleSlack = 8.f;  // log2 units the running max may lag
 // instruction classes of __builtin_amdgcn_sched_group_barrier
 constexpr int kSchedMfma = 0x008;
 constexpr int kSchedDsRead = 0x100;
-constexpr int kReadsAhead = 8;  // LDS reads kept in flight ahead of the MFMAs
+#ifndef PA_AHEAD_MFMA
+#define PA_AHEAD_MFMA 4
+#endif
+constexpr int kAheadMfma = PA_AHEAD_MFMA;  // MFMAs between an LDS read and the MFMA it feeds
 
 struct PrefillParams {
   const uint16_t* q;
@@ -428,12 +431,32 @@ prefill_kernel(PrefillParams p) {
   // stage's previous tile T-4 was last read by B's M(T-3) in segment 2T-5.
   const bool grp_b = wave >= kWaves / 2;
   const int ahead = grp_b ? 3 : 2;  // tile issued during SM(t) is t + ahead
-  auto iteration = [&](int t, auto st) __attribute__((always_inline)) {
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  // One M segment + one SM segment.  kPv / kQk say whether PV(t-1) / QK(t)
+  // exist (every iteration but the first and the last has both), so that the
+  // steady-state M segment is a single block the scheduler can interleave.
+  auto iteration = [&](int t, auto st, auto has_pv, auto has_qk) __attribute__((always_inline)) {
     constexpr int s = decltype(st)::value;
+    constexpr bool kPv = decltype(has_pv)::value;
+    constexpr bool kQk = decltype(has_qk)::value;
     using KS = std::integral_constant<int, s>;
     using VS = std::integral_constant<int, (s + kStages - 1) % kStages>;
-    if (t > 0) pv(VS{});
-    if (t < n_tiles) qk(KS{});
+    if constexpr (kPv) pv(VS{});
+    if constexpr (kQk) qk(KS{});
+    if constexpr (kPv && kQk) {
+      // 16 PV MFMAs (2 transposing V reads each) then 16 QK MFMAs (1 K read
+      // each): every read is issued kAheadMfma MFMAs before the MFMA it feeds.
+      constexpr int A = kAheadMfma;
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * A, 0);
+#pragma unroll
+      for (int i = 1; i <= 32; ++i) {
+        const int next = i + A;  // MFMA whose operands are read now
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        if (next <= 16) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+        else if (next <= 32) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+    }
     wait_vm_lgkm0<15>();  // LDS reads of this segment retired (vmcnt untouched)
     barrier();
     const int ti = t + ahead;
@@ -441,20 +464,24 @@ prefill_kernel(PrefillParams p) {
       if (grp_b) issue_tile(ti * kTileN, std::integral_constant<int, (s + 3) % kStages>{});
       else issue_tile(ti * kTileN, std::integral_constant<int, (s + 2) % kStages>{});
     }
-    if (t < n_tiles) softmax(t);
+    if constexpr (kQk) softmax(t);
     // this wave's share of tile t + ahead - 1 has landed: at most the loads of
     // tile t + ahead (issued above) may still be outstanding
     if (ti < n_tiles) wait_vm_lgkm0<kDmaPerTile>();
     else wait_vm_lgkm0<0>();
     barrier();
   };
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  using S2 = std::integral_constant<int, 2>;
+  using S3 = std::integral_constant<int, 3>;
 
   // Prologue: A issues tiles 0 and 1, B tiles 0, 1 and 2.  Everyone waits for
   // tile 0 before the first barrier; B also waits for tile 1 before its idle
   // barrier (which ends segment 0, i.e. before A's M(1) in segment 2).
-  if (n_tiles > 0) issue_tile(0, std::integral_constant<int, 0>{});
-  if (n_tiles > 1) issue_tile(kTileN, std::integral_constant<int, 1>{});
-  if (grp_b && n_tiles > 2) issue_tile(2 * kTileN, std::integral_constant<int, 2>{});
+  if (n_tiles > 0) issue_tile(0, S0{});
+  if (n_tiles > 1) issue_tile(kTileN, S1{});
+  if (grp_b && n_tiles > 2) issue_tile(2 * kTileN, S2{});
   const int issued = min(n_tiles, grp_b ? 3 : 2);
   if (issued == 3) wait_vm_lgkm0<2 * kDmaPerTile>();
   else if (issued == 2) wait_vm_lgkm0<kDmaPerTile>();
@@ -466,17 +493,29 @@ prefill_kernel(PrefillParams p) {
     barrier();
   }
 
-  // iterations t = 0 .. n_tiles (the last one only finishes PV(n_tiles-1))
-  int t = 0;
-  for (; t + 3 <= n_tiles; t += 4) {
-    iteration(t, std::integral_constant<int, 0>{});
-    iteration(t + 1, std::integral_constant<int, 1>{});
-    iteration(t + 2, std::integral_constant<int, 2>{});
-    iteration(t + 3, std::integral_constant<int, 3>{});
+  // iterations t = 0 .. n_tiles: QK(0) alone, then PV(t-1) + QK(t), then
+  // PV(n_tiles-1) alone.  Tile t sits in stage t % 4.
+  if (n_tiles == 0) {
+    iteration(0, S0{}, F_{}, F_{});
+  } else {
+    iteration(0, S0{}, F_{}, T_{});
+    int t = 1;
+    for (; t + 4 <= n_tiles; t += 4) {
+      iteration(t, S1{}, T_{}, T_{});
+      iteration(t + 1, S2{}, T_{}, T_{});
+      iteration(t + 2, S3{}, T_{}, T_{});
+      iteration(t + 3, S0{}, T_{}, T_{});
+    }
+    if (t < n_tiles) iteration(t, S1{}, T_{}, T_{});
+    if (t + 1 < n_tiles) iteration(t + 1, S2{}, T_{}, T_{});
+    if (t + 2 < n_tiles) iteration(t + 2, S3{}, T_{}, T_{});
+    switch (n_tiles & 3) {
+      case 0: iteration(n_tiles, S0{}, T_{}, F_{}); break;
+      case 1: iteration(n_tiles, S1{}, T_{}, F_{}); break;
+      case 2: iteration(n_tiles, S2{}, T_{}, F_{}); break;
+      default: iteration(n_tiles, S3{}, T_{}, F_{}); break;
+    }
   }
-  if (t <= n_tiles) iteration(t, std::integral_constant<int, 0>{});
-  if (t + 1 <= n_tiles) iteration(t + 1, std::integral_constant<int, 1>{});
-  if (t + 2 <= n_tiles) iteration(t + 2, std::integral_constant<int, 2>{});
   if (!grp_b) barrier();
 
   // ---- epilogue: row n = (token rtok, head rhead); acc_o[dt][i] holds
