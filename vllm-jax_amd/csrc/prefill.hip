@@ -104,8 +104,13 @@ __device__ __forceinline__ void prefill_item(int bid, int batch, int hkv, int n_
     const int xcd = j & 7;
     const int k = j >> 3;             // 0 .. batch*hkv/8 - 1
     const int per_b = hkv >> 3;
-    b = k / per_b;
-    kvh = 8 * (k - b * per_b) + ((xcd - b) & 7);
+    // An XCD deals its workgroups round-robin to its shader engines, so its
+    // k-th workgroup of a level lands on the same engine at every level;
+    // rotating the sequences by level gives every engine every sequence.
+    const int bk = k / per_b;
+    b = bk + level % batch;
+    b = b >= batch ? b - batch : b;
+    kvh = 8 * (k - bk * per_b) + ((xcd - b) & 7);
   } else {
     b = j / hkv;
     kvh = j - b * hkv;
@@ -225,23 +230,30 @@ prefill_kernel(PrefillParams p) {
     const int r = 4 * (kBlk * wave + i) + ld_r;
     ld_off[i] = (uint32_t)(r * (int32_t)p.slot_stride + 8 * swz(r, ld_p));
   }
-  auto issue_tile = [&](int j0, auto buf_c) __attribute__((always_inline)) {
-    uint16_t* const kdst = k_stage(buf_c);
-    uint16_t* const vdst = v_stage(buf_c);
-    // All addresses first, then the loads: a block-table read queued behind
-    // the LDS-DMA loads would make the compiler wait for all of them.
-    const uint16_t* kb[kBlk];
-    const uint16_t* vb[kBlk];
+  // Tile DMA in two steps: tile_addrs() computes this wave's 2*kBlk global
+  // addresses (K block 0, V block 0, K block 1, ...), dma_issue() issues one
+  // of them, so the loads can be spread through other work.  In the aligned
+  // case the tile's page id comes in raw (read ahead of time by the caller).
+  struct TileAddrs {
+    const uint16_t* g[2 * kBlk];
+  };
+  auto page_raw = [&](int j0) __attribute__((always_inline)) {
+    const int lp = min(j0 / p.page_size, p.pages_per_seq - 1);  // stays inside the table row
+    const __attribute__((address_space(4))) int32_t* c = (const __attribute__((address_space(4))) int32_t*)bt_row;
+    return c[lp];
+  };
+  auto tile_addrs = [&](int j0, int32_t raw) __attribute__((always_inline)) {
+    TileAddrs a;
     if constexpr (kAligned) {
-      // page_size % 64 == 0: the whole tile lies in one page (one uniform load)
+      // page_size % 64 == 0: the whole tile lies in one page
       const int lp = j0 / p.page_size;
-      const int32_t page = safe_page_scalar(bt_row, lp, p.num_pages);
+      const int32_t page = raw < 0 ? 0 : (raw >= p.num_pages ? p.num_pages - 1 : raw);
       const int64_t pbase = (int64_t)page * p.page_stride + (int64_t)(j0 - lp * p.page_size) * p.slot_stride + head_off;
       if (j0 + kTileN <= lk) {
 #pragma unroll
         for (int i = 0; i < kBlk; ++i) {
-          kb[i] = p.k_cache + pbase + ld_off[i];
-          vb[i] = p.v_cache + pbase + ld_off[i];
+          a.g[2 * i] = p.k_cache + pbase + ld_off[i];
+          a.g[2 * i + 1] = p.v_cache + pbase + ld_off[i];
         }
       } else {
         const int last = lk - 1 - j0;  // clamp onto a valid token: masked, never stale
@@ -249,8 +261,8 @@ prefill_kernel(PrefillParams p) {
         for (int i = 0; i < kBlk; ++i) {
           const int r = 4 * (kBlk * wave + i) + ld_r;
           const int64_t o = pbase + (int64_t)min(r, last) * p.slot_stride + 8 * swz(r, ld_p);
-          kb[i] = p.k_cache + o;
-          vb[i] = p.v_cache + o;
+          a.g[2 * i] = p.k_cache + o;
+          a.g[2 * i + 1] = p.v_cache + o;
         }
       }
     } else {
@@ -267,16 +279,22 @@ prefill_kernel(PrefillParams p) {
         const int j = min(j0 + r, lk - 1);
         const int64_t o = (int64_t)pages[i] * p.page_stride + (int64_t)(j % p.page_size) * p.slot_stride +
                           head_off + 8 * swz(r, ld_p);
-        kb[i] = p.k_cache + o;
-        vb[i] = p.v_cache + o;
+        a.g[2 * i] = p.k_cache + o;
+        a.g[2 * i + 1] = p.v_cache + o;
       }
     }
+    return a;
+  };
+  const uint32_t k_lds0 = (uint32_t)(uintptr_t)(lds_void_ptr)(&k_lds[0][0]);
+  const uint32_t v_lds0 = (uint32_t)(uintptr_t)(lds_void_ptr)(&v_lds[0][0]);
+  auto dma_issue = [&](const TileAddrs& a, int i, int stage) __attribute__((always_inline)) {
+    const uint32_t base = (i & 1) ? v_lds0 : k_lds0;
+    dma16(a.g[i], base + (uint32_t)(stage * kTileElems * 2 + (kBlk * wave + (i >> 1)) * 1024));
+  };
+  auto issue_tile = [&](int j0, int stage) __attribute__((always_inline)) {
+    const TileAddrs a = tile_addrs(j0, kAligned ? page_raw(j0) : 0);
 #pragma unroll
-    for (int i = 0; i < kBlk; ++i) {
-      const int blk = kBlk * wave + i;
-      dma16(kb[i], (uint32_t)(uintptr_t)(lds_void_ptr)(kdst + blk * 512));
-      dma16(vb[i], (uint32_t)(uintptr_t)(lds_void_ptr)(vdst + blk * 512));
-    }
+    for (int i = 0; i < 2 * kBlk; ++i) dma_issue(a, i, stage);
   };
   constexpr int kDmaPerTile = 2 * kBlk;  // vm instructions one wave issues per tile
 
@@ -354,7 +372,7 @@ prefill_kernel(PrefillParams p) {
       }
     }
   };
-  auto softmax = [&](int t) __attribute__((always_inline)) {
+  auto softmax = [&](int t, auto&& between) __attribute__((always_inline)) {
     const int j0 = t * kTileN;
     if constexpr (kSoftCap) {
 #pragma unroll
@@ -374,11 +392,14 @@ prefill_kernel(PrefillParams p) {
           s_acc[mt][i] = vis ? s_acc[mt][i] : -INFINITY;
         }
     }
-    float mx = -INFINITY;
+    // two independent max3 chains (one per 32-token half)
+    float mx0 = s_acc[0][0], mx1 = s_acc[1][0];
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; i += 2) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s_acc[mt][i], s_acc[mt][i + 1]));
+    for (int i = 1; i < 15; i += 2) {
+      mx0 = __builtin_fmaxf(__builtin_fmaxf(mx0, s_acc[0][i]), s_acc[0][i + 1]);
+      mx1 = __builtin_fmaxf(__builtin_fmaxf(mx1, s_acc[1][i]), s_acc[1][i + 1]);
+    }
+    float mx = __builtin_fmaxf(__builtin_fmaxf(mx0, s_acc[0][15]), __builtin_fmaxf(mx1, s_acc[1][15]));
     mx = max_xor32(mx) * cs;
     // Move the reference max only when this tile's max exceeds it by more
     // than the slack (any lane in the wave): exponents stay <= 2^slack.
@@ -392,6 +413,7 @@ prefill_kernel(PrefillParams p) {
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
+      between(u);
       const int mt = u >> 1;
       const int base = 8 * (u & 1);
       u32x4 w;
@@ -436,6 +458,7 @@ prefill_kernel(PrefillParams p) {
   // One M segment + one SM segment.  kPv / kQk say whether PV(t-1) / QK(t)
   // exist (every iteration but the first and the last has both), so that the
   // steady-state M segment is a single block the scheduler can interleave.
+  int32_t page_next = 0;  // raw block-table entry of the next tile to load (aligned path)
   auto iteration = [&](int t, auto st, auto has_pv, auto has_qk) __attribute__((always_inline)) {
     constexpr int s = decltype(st)::value;
     constexpr bool kPv = decltype(has_pv)::value;
@@ -460,11 +483,22 @@ prefill_kernel(PrefillParams p) {
     wait_vm_lgkm0<15>();  // LDS reads of this segment retired (vmcnt untouched)
     barrier();
     const int ti = t + ahead;
-    if (ti < n_tiles) {
-      if (grp_b) issue_tile(ti * kTileN, std::integral_constant<int, (s + 3) % kStages>{});
-      else issue_tile(ti * kTileN, std::integral_constant<int, (s + 2) % kStages>{});
+    const bool dma = ti < n_tiles;
+    const int dstage = grp_b ? (s + 3) % kStages : (s + 2) % kStages;
+    TileAddrs ta;
+    if (dma) ta = tile_addrs(ti * kTileN, page_next);
+    if constexpr (kAligned) page_next = page_raw((ti + 1) * kTileN);  // for the next iteration
+    // one DMA before each quarter of the softmax: a burst of them would
+    // stall on the address queue
+    auto between = [&](int u) __attribute__((always_inline)) {
+      if (dma) dma_issue(ta, u, dstage);
+    };
+    if constexpr (kQk) {
+      softmax(t, between);
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) between(u);
     }
-    if constexpr (kQk) softmax(t);
     // this wave's share of tile t + ahead - 1 has landed: at most the loads of
     // tile t + ahead (issued above) may still be outstanding
     if (ti < n_tiles) wait_vm_lgkm0<kDmaPerTile>();
@@ -479,9 +513,11 @@ prefill_kernel(PrefillParams p) {
   // Prologue: A issues tiles 0 and 1, B tiles 0, 1 and 2.  Everyone waits for
   // tile 0 before the first barrier; B also waits for tile 1 before its idle
   // barrier (which ends segment 0, i.e. before A's M(1) in segment 2).
-  if (n_tiles > 0) issue_tile(0, S0{});
-  if (n_tiles > 1) issue_tile(kTileN, S1{});
-  if (grp_b && n_tiles > 2) issue_tile(2 * kTileN, S2{});
+  if (n_tiles > 0) issue_tile(0, 0);
+  if (n_tiles > 1) issue_tile(kTileN, 1);
+  if (grp_b && n_tiles > 2) issue_tile(2 * kTileN, 2);
+  // raw page id of the first tile the loop loads (tile `ahead`)
+  if (kAligned && n_tiles > 0) page_next = page_raw(ahead * kTileN);
   const int issued = min(n_tiles, grp_b ? 3 : 2);
   if (issued == 3) wait_vm_lgkm0<2 * kDmaPerTile>();
   else if (issued == 2) wait_vm_lgkm0<kDmaPerTile>();
