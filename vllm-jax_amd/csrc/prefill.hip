@@ -328,7 +328,9 @@ prefill_kernel(PrefillParams p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc_o[dt][i] = 0.f;
   float m_ref = -1e30f;  // reference max (log2 units) of the accumulators
-  float l_run = 0.f;
+  // running row sums, one per quarter of a tile: four short dot2c chains
+  // instead of one long one
+  float l_part[4] = {0.f, 0.f, 0.f, 0.f};
   const float cs = kSoftCap ? 1.f : p.logit_scale;  // multiplier applied inside the exponent
   f32x16 s_acc[2];  // S^T of the tile between its QK and its softmax
   bf16x8 pt[4];     // P^T of the tile between its softmax and its PV
@@ -392,14 +394,17 @@ prefill_kernel(PrefillParams p) {
           s_acc[mt][i] = vis ? s_acc[mt][i] : -INFINITY;
         }
     }
-    // two independent max3 chains (one per 32-token half)
-    float mx0 = s_acc[0][0], mx1 = s_acc[1][0];
+    // four independent max3 chains (one per 16-token quarter)
+    float mq[4];
 #pragma unroll
-    for (int i = 1; i < 15; i += 2) {
-      mx0 = __builtin_fmaxf(__builtin_fmaxf(mx0, s_acc[0][i]), s_acc[0][i + 1]);
-      mx1 = __builtin_fmaxf(__builtin_fmaxf(mx1, s_acc[1][i]), s_acc[1][i + 1]);
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int mt = q4 >> 1, b0 = 8 * (q4 & 1);
+      float m = __builtin_fmaxf(__builtin_fmaxf(s_acc[mt][b0], s_acc[mt][b0 + 1]), s_acc[mt][b0 + 2]);
+      m = __builtin_fmaxf(__builtin_fmaxf(m, s_acc[mt][b0 + 3]), s_acc[mt][b0 + 4]);
+      m = __builtin_fmaxf(__builtin_fmaxf(m, s_acc[mt][b0 + 5]), s_acc[mt][b0 + 6]);
+      mq[q4] = __builtin_fmaxf(m, s_acc[mt][b0 + 7]);
     }
-    float mx = __builtin_fmaxf(__builtin_fmaxf(mx0, s_acc[0][15]), __builtin_fmaxf(mx1, s_acc[1][15]));
+    float mx = __builtin_fmaxf(__builtin_fmaxf(mq[0], mq[1]), __builtin_fmaxf(mq[2], mq[3]));
     mx = max_xor32(mx) * cs;
     // Move the reference max only when this tile's max exceeds it by more
     // than the slack (any lane in the wave): exponents stay <= 2^slack.
@@ -407,7 +412,8 @@ prefill_kernel(PrefillParams p) {
       const float m_new = fmaxf(m_ref, mx);
       const float corr = fast_exp2(m_ref - m_new);
       m_ref = m_new;
-      l_run *= corr;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) l_part[u] *= corr;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) acc_o[dt] = acc_o[dt] * corr;
     }
@@ -424,13 +430,13 @@ prefill_kernel(PrefillParams p) {
         w[e] = pack_bf16x2(a, c);
       }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) l_run = dot2_bf16_ones(w[e], l_run);
+      for (int e = 0; e < 4; ++e) l_part[u] = dot2_bf16_ones(w[e], l_part[u]);
       // Materialise P here: otherwise the compiler sinks the exp work past
       // the barrier into the next MFMA segment, undoing the ping-pong.
       asm volatile("" : "+v"(w));
       pt[u] = as_bf16x8(w);
     }
-    asm volatile("" : "+v"(l_run));
+    asm volatile("" : "+v"(l_part[0]), "+v"(l_part[1]), "+v"(l_part[2]), "+v"(l_part[3]));
   };
   auto barrier = [&]() __attribute__((always_inline)) {
     __builtin_amdgcn_sched_barrier(0);
@@ -556,7 +562,7 @@ prefill_kernel(PrefillParams p) {
 
   // ---- epilogue: row n = (token rtok, head rhead); acc_o[dt][i] holds
   // d = 32dt + 8(i/4) + 4h + i%4
-  l_run = sum_xor32(l_run);
+  const float l_run = sum_xor32((l_part[0] + l_part[1]) + (l_part[2] + l_part[3]));
   if (row_ok) {
     const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
     uint16_t* orow = p.out + (int64_t)(q0 + rtok) * p.o_ts + (int64_t)(kvh * p.group + rhead) * p.o_hs + 4 * h;
