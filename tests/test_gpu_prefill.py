@@ -124,3 +124,13 @@ def test_prefill_qwen3_32b_long(pkg, dev):
     diff = float(np.abs(ora.bf16_to_f32(u16(dec)) - got[cu[1:] - 1]).max())
     print(f"prefill last rows vs decode max-abs diff {diff:.3e}")
     assert diff <= TOL
+
+
+def test_prefill_many_sequences(pkg, dev):
+    """A batch of 70 short ragged sequences (most q tiles of the launch grid
+    fall outside their sequence)."""
+    rng = np.random.default_rng(22)
+    lens = rng.integers(1, 200, 70).tolist()
+    pb = wl.make_prefill(lens, num_heads=16, num_kv_heads=8, page_size=64, rng=rng)
+    rows = np.unique(np.concatenate([pb.cu_seqlens_q[1:] - 1, rng.integers(0, pb.num_tokens, 64)]))
+    _prefill(pkg, dev, pb, seed=22, rows=rows)
