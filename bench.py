@@ -10,6 +10,9 @@ workload, inputs resident in HBM:
 * Qwen3-8B decode (256 sequences, ctx ~ U[512, 8192], 32 q / 8 kv heads,
   16384-page pool, seed 2): KV store of the new token + split-K decode.
   Reported under ``"decode"`` in GB/s of algorithmic HBM traffic.
+* The fused q/k RMSNorm + RoPE + KV store over the prefill workload's tokens
+  (timed in its own loop after the step): reported under ``"qk_norm_rope"``
+  in GB/s of algorithmic HBM traffic, (2 H + 4 Hkv) * 256 + 8 bytes a token.
 
 Prints ONE JSON line.  ``roofline`` (prefill, MFMA-bound) and
 ``decode.roofline`` (HBM-bound) use the average duration of the attention
@@ -99,7 +102,7 @@ def run_gpu(args):
                                     max_seqlen_bucket=pb.max_seqlen_bucket, out=out_p)
 
     # ---------------- decode: Qwen3-8B
-    db = wl.qwen3_8b_decode(seed=2) if args.only != "prefill" else \
+    db = wl.qwen3_8b_decode(seed=2) if args.only not in ("prefill", "rope") else \
         wl.make_decode([64], num_heads=32, num_kv_heads=8, rng=np.random.default_rng(0))
     dt_ = wl.materialize_decode(db, seed=2, device=dev)
     kv_d = dt_["kv_cache"]
@@ -119,6 +122,7 @@ def run_gpu(args):
 
     run_p = args.only in (None, "prefill")
     run_d = args.only in (None, "decode")
+    run_r = args.only in (None, "rope")
     nop = lambda: None
     if not run_p:
         prefill_step = prefill_attn = nop
@@ -157,6 +161,8 @@ def run_gpu(args):
     p_tflops_kernel = rate(p_flops, float(p_attn.mean()), 1e12)
     d_gbs_step = rate(d_bytes, decode_step_ms, 1e9)
     d_gbs_kernel = rate(d_bytes, float(d_attn.mean()), 1e9)
+
+    rope = run_rope(args, torch, pkg, pb, pt, kv_p) if run_r else None
 
     traffic = _load_traffic()
     res = {
@@ -219,7 +225,46 @@ def run_gpu(args):
         },
         "wall_s_timed": round(wall, 3),
     }
+    if rope is not None:
+        rope["roofline"]["traffic"] = traffic.get("qk_norm_rope_store_kernel")
+        res["qk_norm_rope"] = rope
     return res, (pb, pt, db, dt_)
+
+
+def run_rope(args, torch, pkg, pb, pt, kv):
+    """Time the fused q/k RMSNorm + RoPE + KV store on the prefill tokens."""
+    g = torch.Generator(device=kv.device)
+    g.manual_seed(7)
+    d = pb.head_dim
+    qw = (1.0 + 0.1 * torch.randn(d, generator=g, device=kv.device)).to(torch.bfloat16)
+    kw = (1.0 + 0.1 * torch.randn(d, generator=g, device=kv.device)).to(torch.bfloat16)
+    q_out = torch.empty_like(pt["q"])
+
+    def call():
+        pkg.qk_norm_rope_store(pt["q"], pt["k"], pt["v"], qw, kw, pt["input_positions"], pt["slot_mapping"], kv,
+                               eps=1e-6, rope_theta=1e6, out=q_out)
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(args.steps):
+        call()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    t = pb.num_tokens
+    nbytes = t * ((2 * pb.num_heads + 4 * pb.num_kv_heads) * d * 2 + 8)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "fused qk rmsnorm + rope + kv store GB/s",
+        "tokens": int(t), "num_heads": int(pb.num_heads), "num_kv_heads": int(pb.num_kv_heads),
+        "algorithmic_gb": round(nbytes / 1e9, 4),
+        "ms": round(ms, 4),
+        "roofline": {"kernel": "qk_norm_rope_store_kernel", "bound": "hbm", "achieved": round(gbs, 1),
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
 
 
 def cpu_baseline(pb, pt, db, dt_, budget_s):
@@ -298,7 +343,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU oracle work (total)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "copy"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "rope", "copy"], default=None,
                     help="profiling aid: run one kernel family only (the JSON line then covers that part)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

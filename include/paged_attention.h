@@ -136,6 +136,34 @@ int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
                uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
                void* stream);
 
+/*
+ * The layer step between the q/k/v projections and attention, fused:
+ *   q_out[t, h]        = rope(rmsnorm(q[t, h]) * q_norm_weight, pos[t])
+ *   k_cache[slot[t], h] = rope(rmsnorm(k[t, h]) * k_norm_weight, pos[t])
+ *   v_cache[slot[t], h] = v[t, h]
+ * rmsnorm(x) = x * rsqrt(mean(x^2) + eps); rope rotates interleaved pairs
+ * (x[2i], x[2i+1]) by pos * inv_freq[i], inv_freq = 1 / theta^(2i/d), with
+ * positions divided by rope_scaling_factor (1 = no scaling), all evaluated
+ * with bf16 operands as the reference does.  Tokens whose slot lies outside
+ * [0, num_pages*page_size) store nothing (q_out is still written).
+ * Replaces q_norm/k_norm + apply_rope (vllm/model/qwen3.py:286-296,
+ * 59-78) and the K/V scatter of _update_kv_cache (qwen3.py:105-111).
+ * q/k/v/q_out: [num_tokens, heads, d] with (tok, head) strides; the norm
+ * weights are [d].  q_out may alias q (same strides).
+ */
+int pa_qk_norm_rope_store(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                          const uint16_t* k, int64_t k_tok_stride, int64_t k_head_stride,
+                          const uint16_t* v, int64_t v_tok_stride, int64_t v_head_stride,
+                          const uint16_t* q_norm_weight, const uint16_t* k_norm_weight,
+                          float eps, float rope_theta, float rope_scaling_factor,
+                          const int32_t* positions, const int32_t* slot_mapping,
+                          int32_t num_tokens, int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                          uint16_t* q_out, int64_t q_out_tok_stride, int64_t q_out_head_stride,
+                          uint16_t* k_cache, uint16_t* v_cache,
+                          int32_t num_pages, int32_t page_size,
+                          int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

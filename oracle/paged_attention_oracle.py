@@ -453,3 +453,77 @@ def prefill_visible_pairs(cu_seqlens, cu_seqlens_k=None) -> int:
     n = np.diff(cu)
     pfx = np.diff(cuk) - n
     return int((n * pfx + n * (n + 1) // 2).sum())
+
+
+# ----------------------------------------------------------------------------
+# f1: QK RMSNorm + RoPE + KV store, the layer step before attention
+#     (qwen3.py:286-299 with apply_rope qwen3.py:59-78)
+# ----------------------------------------------------------------------------
+def rope_inv_freq(head_dim: int, rope_theta: float) -> np.ndarray:
+    """``1 / rope_theta ** (arange(0, d, 2, bf16) / d)`` as the reference
+    evaluates it (qwen3.py:62-63): every operand and result is bf16, so the
+    weakly typed ``rope_theta`` is rounded to bf16 first (1e6 -> 999424) and
+    each of arange/d, the power and the reciprocal is rounded to bf16.
+    Returns float32 values (all representable in bf16), shape [d/2]."""
+    e = round_bf16(np.arange(0, head_dim, 2, dtype=np.float32) / np.float32(head_dim))
+    theta = round_bf16(np.float32(rope_theta)).reshape(-1)[0]
+    p = round_bf16(np.power(theta, e, dtype=np.float32))
+    return round_bf16(np.float32(1.0) / p)
+
+
+def rope_positions(positions, rope_scaling=None) -> np.ndarray:
+    """``_maybe_scale_positions`` then ``.astype(bf16)`` (qwen3.py:48-56,61):
+    linear/dynamic scaling divides by the factor in float32, then positions
+    are rounded to bf16 (exact only up to 256)."""
+    pos = np.asarray(positions).astype(np.float32)
+    if rope_scaling is not None and rope_scaling.get("type") in {"linear", "dynamic"}:
+        pos = pos / np.float32(rope_scaling.get("factor", 1.0))
+    return round_bf16(pos)
+
+
+def rope_cos_sin(positions, head_dim: int, rope_theta: float, rope_scaling=None):
+    """cos/sin tables [T, d/2] (qwen3.py:64-66): freqs = bf16(pos x inv_freq),
+    cos/sin evaluated in float32 and rounded to bf16."""
+    pos = rope_positions(positions, rope_scaling)
+    inv = rope_inv_freq(head_dim, rope_theta)
+    freqs = round_bf16(pos[:, None] * inv[None, :])
+    return round_bf16(np.cos(freqs)), round_bf16(np.sin(freqs))
+
+
+def apply_rope(x, cos, sin) -> np.ndarray:
+    """Rotate interleaved pairs (x[2i], x[2i+1]) (qwen3.py:68-73):
+    (x1 cos - x2 sin, x1 sin + x2 cos), written back interleaved.  x: bf16
+    bits [T, heads, d]; cos/sin: [T, d/2].  The rotation is evaluated in
+    float32 and rounded once to bf16."""
+    xf = _as_f32(x)
+    x1, x2 = xf[..., 0::2], xf[..., 1::2]
+    c, s = cos[:, None, :], sin[:, None, :]
+    out = np.empty_like(xf)
+    out[..., 0::2] = x1 * c - x2 * s
+    out[..., 1::2] = x1 * s + x2 * c
+    return f32_to_bf16(out)
+
+
+def rms_norm(x, weight, eps: float) -> np.ndarray:
+    """flax ``nnx.RMSNorm`` over the last axis as the reference layer uses it
+    (qwen3.py:235-241,287,293): mean of squares in float32,
+    ``y = x * (rsqrt(mean + eps) * weight)`` in float32, rounded to bf16."""
+    xf = _as_f32(x)
+    w = _as_f32(weight)
+    ms = np.mean(xf * xf, axis=-1, keepdims=True, dtype=np.float32)
+    mul = (np.float32(1.0) / np.sqrt(ms + np.float32(eps))).astype(np.float32) * w
+    return f32_to_bf16(xf * mul)
+
+
+def qk_norm_rope_store(q, k, v, q_norm_w, k_norm_w, positions, slot_mapping, k_cache, v_cache, *,
+                       eps: float, rope_theta: float, rope_scaling=None):
+    """The layer step before attention (qwen3.py:286-299): q and k get RMSNorm
+    then RoPE; k and v are stored into the pool through the slot mapping
+    (``_update_kv_cache``, qwen3.py:105-111).  Returns (q_out, k_cache,
+    v_cache); bf16 bit patterns throughout."""
+    d = np.asarray(q).shape[-1]
+    cos, sin = rope_cos_sin(positions, d, rope_theta, rope_scaling)
+    q_out = apply_rope(rms_norm(q, q_norm_w, eps), cos, sin)
+    k_out = apply_rope(rms_norm(k, k_norm_w, eps), cos, sin)
+    kc, vc = kv_store(k_cache, v_cache, k_out, v, slot_mapping)
+    return q_out, kc, vc

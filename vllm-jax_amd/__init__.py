@@ -6,7 +6,9 @@ Public surface (mirrors simpissa/vllm-jax):
   / ``DecodeAttentionMetadata`` -- the layer seam of vllm/model/qwen3.py;
 * ``prefill_paged_attention`` / ``decode_paged_attention`` -- the kernel
   entries of vllm/kernels/;
-* ``update_kv_cache`` -- the KV store.
+* ``update_kv_cache`` -- the KV store;
+* ``qk_norm_rope_store`` / ``qwen3_attention_core`` -- the q/k RMSNorm +
+  RoPE + KV store step before attention, fused into one kernel.
 
 All device work runs in ``libpaged_attention.so`` (hand-written HIP for
 gfx950, built by ``build.py``) through a C ABI; there is no CPU fallback.
@@ -18,6 +20,7 @@ module name ``vllm_jax_amd``::
         submodule_search_locations=["<repo>/vllm-jax_amd"])
 """
 from .attention import (DecodeAttentionMetadata, PrefillAttentionMetadata, attention,  # noqa: F401
-                        gather_kv, update_kv_cache)
+                        attention_stored, gather_kv, qk_norm_rope_store, qwen3_attention_core,
+                        update_kv_cache)
 from .kernels.decode_paged_attention import decode_paged_attention  # noqa: F401
 from .kernels.prefill_paged_attention import prefill_paged_attention  # noqa: F401

@@ -60,6 +60,19 @@ SIGNATURES = {
         c_vp, c_i64, c_i64,            # out
         c_vp,                          # stream
     ]),
+    "pa_qk_norm_rope_store": (ctypes.c_int, [
+        c_vp, c_i64, c_i64,            # q
+        c_vp, c_i64, c_i64,            # k
+        c_vp, c_i64, c_i64,            # v
+        c_vp, c_vp,                    # q_norm_weight, k_norm_weight
+        c_f32, c_f32, c_f32,           # eps, rope_theta, rope_scaling_factor
+        c_vp, c_vp,                    # positions, slot_mapping
+        c_i32, c_i32, c_i32, c_i32,    # num_tokens, num_heads, num_kv_heads, head_dim
+        c_vp, c_i64, c_i64,            # q_out
+        c_vp, c_vp, c_i32, c_i32,      # caches, num_pages, page_size
+        c_i64, c_i64, c_i64,           # page/slot/head strides
+        c_vp,                          # stream
+    ]),
 }
 
 

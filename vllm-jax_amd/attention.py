@@ -19,7 +19,7 @@ prefill or decode kernel.  Differences from the reference, all deliberate:
 from __future__ import annotations
 
 from dataclasses import dataclass, field
-from typing import Tuple, Union
+from typing import Optional, Tuple, Union
 
 import torch
 
@@ -94,12 +94,85 @@ def update_kv_cache(kv_cache: torch.Tensor, slot_mapping: torch.Tensor, k: torch
 _update_kv_cache = update_kv_cache
 
 
+def qk_norm_rope_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_weight: torch.Tensor,
+                       k_norm_weight: torch.Tensor, positions: torch.Tensor, slot_mapping: torch.Tensor,
+                       kv_cache: torch.Tensor, *, eps: float, rope_theta: float,
+                       rope_scaling: Optional[dict] = None,
+                       out: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The layer step between the projections and attention, in one kernel:
+    ``q = rope(q_norm(q))``, ``k = rope(k_norm(k))`` (qwen3.py:286-296 with
+    apply_rope qwen3.py:59-78) and the K/V store of ``_update_kv_cache``
+    (qwen3.py:105-111), in place.  Returns ``(q_out, kv_cache)``; ``out``
+    may be ``q`` itself.  ``rope_scaling`` of type linear/dynamic divides the
+    positions by its factor (qwen3.py:48-56); other types leave them as is.
+    """
+    for name, t in (("q", q), ("k", k), ("v", v), ("q_norm_weight", q_norm_weight),
+                    ("k_norm_weight", k_norm_weight), ("positions", positions),
+                    ("slot_mapping", slot_mapping), ("kv_cache", kv_cache)):
+        require_device(name, t)
+    for name, t in (("q", q), ("k", k), ("v", v), ("q_norm_weight", q_norm_weight),
+                    ("k_norm_weight", k_norm_weight), ("kv_cache", kv_cache)):
+        require_bf16(name, t)
+    if kv_cache.dim() != 5 or kv_cache.shape[0] != 2:
+        raise ValueError(f"kv_cache must be [2, NB, BS, Hkv, d], got {tuple(kv_cache.shape)}")
+    _, nb, bs, hkv, d = kv_cache.shape
+    if q.dim() != 3 or q.shape[-1] != d:
+        raise ValueError(f"q must be [T, H, {d}], got {tuple(q.shape)}")
+    t_count, h = q.shape[0], q.shape[1]
+    if tuple(k.shape) != (t_count, hkv, d) or tuple(v.shape) != (t_count, hkv, d):
+        raise ValueError(f"k/v must be [{t_count}, {hkv}, {d}], got {tuple(k.shape)} and {tuple(v.shape)}")
+    if tuple(q_norm_weight.shape) != (d,) or tuple(k_norm_weight.shape) != (d,):
+        raise ValueError("norm weights must be [head_dim]")
+    for name, t in (("positions", positions), ("slot_mapping", slot_mapping)):
+        if t.dtype != torch.int32 or tuple(t.shape) != (t_count,):
+            raise ValueError(f"{name} must be int32 of shape [T]")
+    factor = 1.0
+    if rope_scaling is not None and rope_scaling.get("type") in {"linear", "dynamic"}:
+        factor = float(rope_scaling.get("factor", 1.0))
+    if out is None:
+        out = torch.empty_like(q)
+    kc, vc = kv_cache[0], kv_cache[1]
+    pos = positions.contiguous()
+    sm = slot_mapping.contiguous()
+    qw, kw = q_norm_weight.contiguous(), k_norm_weight.contiguous()
+    _lib.call(
+        "pa_qk_norm_rope_store",
+        q.data_ptr(), q.stride(0), q.stride(1),
+        k.data_ptr(), k.stride(0), k.stride(1),
+        v.data_ptr(), v.stride(0), v.stride(1),
+        qw.data_ptr(), kw.data_ptr(), float(eps), float(rope_theta), factor,
+        pos.data_ptr(), sm.data_ptr(), t_count, h, hkv, d,
+        out.data_ptr(), out.stride(0), out.stride(1),
+        kc.data_ptr(), vc.data_ptr(), nb, bs, kc.stride(0), kc.stride(1), kc.stride(2),
+        stream_handle(q))
+    return out, kv_cache
+
+
 def attention(kv_cache: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
               metadata: AttentionMetadata) -> Tuple[torch.Tensor, torch.Tensor]:
     """qwen3.py:172-218 on gfx950 kernels; returns ``(kv_cache, out)``."""
+    kv_cache = update_kv_cache(kv_cache, metadata.slot_mapping, k, v)
+    return kv_cache, attention_stored(kv_cache, q, metadata)
+
+
+def qwen3_attention_core(kv_cache: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                         q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor,
+                         metadata: AttentionMetadata, *, eps: float, rope_theta: float,
+                         rope_scaling: Optional[dict] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Everything of ``Qwen3Attention.__call__`` between the q/k/v
+    projections and o_proj (qwen3.py:287-299): q/k RMSNorm + RoPE and the KV
+    store in one fused kernel, then paged attention.  Returns
+    ``(kv_cache, out)``."""
+    q_rot, kv_cache = qk_norm_rope_store(q, k, v, q_norm_weight, k_norm_weight, metadata.input_positions,
+                                         metadata.slot_mapping, kv_cache, eps=eps, rope_theta=rope_theta,
+                                         rope_scaling=rope_scaling)
+    return kv_cache, attention_stored(kv_cache, q_rot, metadata)
+
+
+def attention_stored(kv_cache: torch.Tensor, q: torch.Tensor, metadata: AttentionMetadata) -> torch.Tensor:
+    """The attention part of qwen3.py:175-218 for K/V already in the pool."""
     if not (USE_PREFILL_PAGED_ATTENTION_KERNEL and USE_DECODE_PAGED_ATTENTION_KERNEL):
         raise NotImplementedError("the dense fallbacks of qwen3.py:120-169 are not part of this library")
-    kv_cache = update_kv_cache(kv_cache, metadata.slot_mapping, k, v)
     k_pages = kv_cache[0].permute(2, 0, 1, 3)   # [Hkv, NB, BS, d] view
     v_pages = kv_cache[1].permute(2, 0, 1, 3)
     if isinstance(metadata, PrefillAttentionMetadata):
@@ -113,7 +186,7 @@ def attention(kv_cache: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch
         outputs = decode_paged_attention(
             q, k_pages, v_pages, metadata.block_tables, metadata.context_lens,
             scale=1.0 / bf16_round(float(head_dim) ** 0.5))
-    return kv_cache, outputs
+    return outputs
 
 
 def gather_kv(cache: torch.Tensor, block_tables: torch.Tensor, lengths: torch.Tensor) -> torch.Tensor:
