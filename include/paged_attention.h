@@ -164,6 +164,42 @@ int pa_qk_norm_rope_store(const uint16_t* q, int64_t q_tok_stride, int64_t q_hea
                           int64_t page_stride, int64_t slot_stride, int64_t head_stride,
                           void* stream);
 
+/*
+ * Workspace bytes pa_mixed needs (0 when every decode sequence fits one
+ * 4096-token chunk, i.e. pages_per_seq * page_size <= the chunk).
+ */
+size_t pa_mixed_workspace_size(int32_t num_decodes, int32_t num_heads, int32_t head_dim,
+                               int32_t pages_per_seq, int32_t page_size);
+
+/*
+ * One launch for a scheduler step that mixes decode and prefill sequences,
+ * unpadded.  Sequence b owns q rows [cu_seqlens_q[b], cu_seqlens_q[b+1]) and
+ * kv indices [0, kv_lens[b]) through block_tables[b].
+ *   - b < num_decodes (decode): its single q row attends to every kv index,
+ *     scale decode_scale (the reference pre-scales q, qwen3.py:207: pass 1
+ *     for such q); kv_lens[b] == 0 gives a zero row; a decode sequence
+ *     without a q row writes nothing.
+ *   - b >= num_decodes (prefill): as pa_prefill with Lk_b = kv_lens[b],
+ *     scale prefill_scale, rows at offset >= max_seqlen_q left zero.
+ * Rows outside every sequence, and rows past the first of a decode
+ * sequence, are written as zeros.
+ * Replaces the reference step's two jitted calls, decode then prefill, each
+ * padded to a power-of-two bucket (vllm/src/model_runner.py:310-333, padding
+ * 243-255, 286-292), at the attention seam (vllm/model/qwen3.py:172-218).
+ * q/out: [num_tokens, H, d] with (tok, head) strides.
+ */
+int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+             const uint16_t* k_cache, const uint16_t* v_cache,
+             int32_t num_pages, int32_t page_size,
+             int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+             const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+             const int32_t* cu_seqlens_q, const int32_t* kv_lens, const int32_t* input_positions,
+             int32_t batch, int32_t num_decodes, int32_t num_tokens, int32_t max_seqlen_q,
+             int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+             float prefill_scale, float decode_scale, float soft_cap,
+             uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
+             void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

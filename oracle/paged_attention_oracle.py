@@ -527,3 +527,54 @@ def qk_norm_rope_store(q, k, v, q_norm_w, k_norm_w, positions, slot_mapping, k_c
     k_out = apply_rope(rms_norm(k, k_norm_w, eps), cos, sin)
     kc, vc = kv_store(k_cache, v_cache, k_out, v, slot_mapping)
     return q_out, kc, vc
+
+
+# ----------------------------------------------------------------------------
+# f2: one scheduler step with decode and prefill sequences
+#     (model_runner.py:310-333 runs them as two calls: decode, then prefill)
+# ----------------------------------------------------------------------------
+def mixed_attention(q, k_pages, v_pages, block_tables, cu_seqlens_q, kv_lens, input_positions,
+                    num_decodes: int, *, soft_cap=None, prefill_rows=None, decode_seqs=None):
+    """The reference step's two attention calls over one unpadded batch.
+
+    Sequences ``b < num_decodes`` are decode sequences: their q row
+    ``cu_seqlens_q[b]`` is scaled as the decode caller does it,
+    ``bf16(q / bf16(sqrt(d)))`` (qwen3.py:207), and attends to kv indices
+    ``j < kv_lens[b]`` (decode_attention above).  The others are prefill
+    sequences with kv length ``kv_lens[b]`` (prefill_attention above with
+    ``cu_seqlens_k`` built from kv_lens).  Rows no sequence computes are 0.
+    ``prefill_rows`` (rows of q, optional) and ``decode_seqs`` (optional)
+    restrict the work for sampling.  Returns bf16 bit patterns ``[T, H, d]``.
+    """
+    qf = _as_f32(q)
+    t_total, h, d = qf.shape
+    bt = np.asarray(block_tables)
+    cu = np.asarray(cu_seqlens_q, dtype=np.int64)
+    kl = np.asarray(kv_lens, dtype=np.int64)
+    pos = np.asarray(input_positions)
+    nd = int(num_decodes)
+    out = np.zeros((t_total, h, d), np.uint16)
+    if nd > 0:
+        root = float(round_bf16(np.float32(math.sqrt(d))).reshape(-1)[0])
+        dec_rows = cu[:nd]
+        has_row = (cu[1:nd + 1] > cu[:nd]) & (cu[:nd] < t_total)
+        seqs = np.nonzero(has_row)[0]
+        if decode_seqs is not None:
+            seqs = np.intersect1d(seqs, np.asarray(decode_seqs))
+        qd = np.zeros((nd, h, d), np.float32)
+        qd[seqs] = qf[dec_rows[seqs]]
+        qd = round_bf16(qd / np.float32(root))
+        od = decode_attention(qd, k_pages, v_pages, bt[:nd], kl[:nd], soft_cap=soft_cap, seqs=seqs)
+        out[dec_rows[seqs]] = od[seqs]
+    if nd < len(kl):
+        base = int(cu[nd])
+        cu_p = cu[nd:] - base
+        cuk = np.concatenate([[0], np.cumsum(kl[nd:])])
+        rows = None
+        if prefill_rows is not None:
+            rows = np.asarray(prefill_rows, dtype=np.int64) - base
+        tail = prefill_attention(qf[base:], k_pages, v_pages, bt[nd:], cu_p, pos[base:], cu_seqlens_k=cuk,
+                                 soft_cap=soft_cap, rows=rows)
+        sel = slice(base, base + int(cu_p[-1]))
+        out[sel] = tail[:int(cu_p[-1])]
+    return out

@@ -327,3 +327,61 @@ def test_visible_pairs_closed_form():
     assert ora.prefill_visible_pairs(cu) == sum(n * (n + 1) // 2 for n in (17, 128, 300, 511)) == 184375
     cuk = np.array([0, 27, 155, 455, 966])  # first sequence: prefix 10
     assert ora.prefill_visible_pairs(cu, cuk) == 184375 + 17 * 10
+
+
+# ---------------------------------------------------------------------------
+# mixed step (decode sequences first, then prefill sequences)
+# ---------------------------------------------------------------------------
+def _mixed_case(rng, dec_lens, pre_q, pre_prefix, h, hkv, bs, pad_rows=0):
+    kv = list(dec_lens) + [p + n for p, n in zip(pre_prefix, pre_q)]
+    nb = int(sum(-(-int(n) // bs) for n in kv)) + 2
+    kc, vc = _pool(rng, nb, bs, hkv)
+    bt = _tables(rng, kv, bs, nb)
+    q_lens = [1] * len(dec_lens) + list(pre_q)
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    pos = np.concatenate([[max(n - 1, 0)] for n in dec_lens] +
+                         [np.arange(p, p + n) for p, n in zip(pre_prefix, pre_q)]).astype(np.int32)
+    pos = np.concatenate([pos, np.zeros(pad_rows, np.int32)])
+    q = _bf16(rng, (int(cu[-1]) + pad_rows, h, 128))
+    return q, kc, vc, bt, cu, np.asarray(kv, np.int32), pos
+
+
+def test_mixed_vs_brute_force():
+    rng = np.random.default_rng(11)
+    dec, pre_q, pre_p = [1, 40, 0, 70], [5, 33, 1], [0, 12, 50]
+    q, kc, vc, bt, cu, kv, pos = _mixed_case(rng, dec, pre_q, pre_p, 8, 2, 16, pad_rows=3)
+    nd = len(dec)
+    got = ora.bf16_to_f32(ora.mixed_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, kv,
+                                              pos, nd))
+    kctx, vctx = ora.gather_kv(kc, bt, kv), ora.gather_kv(vc, bt, kv)
+    # decode rows: q pre-scaled in bf16 by 1/bf16(sqrt(d)) (qwen3.py:207)
+    qd = ora.f32_to_bf16(ora.round_bf16(ora.bf16_to_f32(q[cu[:nd]]) / np.float32(11.3125)))
+    want_d = ora.dense_decode_f64(qd, kctx[:nd], vctx[:nd], kv[:nd])
+    assert np.abs(got[cu[:nd]] - want_d).max() <= BRUTE_TOL
+    assert not got[cu[2]].any()                       # kv length 0
+    # prefill rows: q scaled by bf16(1/sqrt(d)) in bf16 (prefill...:60)
+    sc = float(ora.round_bf16(np.float32(1 / math.sqrt(128))).reshape(-1)[0])
+    base = int(cu[nd])
+    qp = ora.f32_to_bf16(ora.round_bf16(ora.bf16_to_f32(q[base:cu[-1]]) * np.float32(sc)))
+    cup = cu[nd:] - base
+    cuk = np.concatenate([[0], np.cumsum(kv[nd:])])
+    want_p = ora.dense_prefill_f64(qp, kctx[nd:], vctx[nd:], cup, pos[base:cu[-1]], cu_seqlens_k=cuk, scale=1.0)
+    assert np.abs(got[base:cu[-1]] - want_p).max() <= BRUTE_TOL
+    assert not got[cu[-1]:].any()                     # rows outside every sequence
+    # mutation: treating the first prefill sequence as a decode sequence drops
+    # its causal mask on row 0 and its later rows
+    wrong = ora.bf16_to_f32(ora.mixed_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, kv,
+                                                pos, nd + 1))
+    assert np.abs(wrong[base:cu[-1]] - want_p).max() > BRUTE_TOL
+
+
+def test_mixed_decode_row_equals_prefill_last_row():
+    """A decode sequence and a one-row prefill sequence over the same context
+    differ only in how q is scaled; with the scales made equal they agree."""
+    rng = np.random.default_rng(12)
+    q, kc, vc, bt, cu, kv, pos = _mixed_case(rng, [90], [1], [89], 4, 2, 16)
+    bt[1] = bt[0]                                     # same context pages
+    q[1] = q[0]                                       # same query
+    kp, vp = kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3)
+    both = ora.bf16_to_f32(ora.mixed_attention(q, kp, vp, bt, cu, kv, pos, 1))
+    assert np.abs(both[0] - both[1]).max() <= 2e-2 * max(1.0, np.abs(both).max())

@@ -8,7 +8,9 @@ Public surface (mirrors simpissa/vllm-jax):
   entries of vllm/kernels/;
 * ``update_kv_cache`` -- the KV store;
 * ``qk_norm_rope_store`` / ``qwen3_attention_core`` -- the q/k RMSNorm +
-  RoPE + KV store step before attention, fused into one kernel.
+  RoPE + KV store step before attention, fused into one kernel;
+* ``MixedAttentionMetadata`` / ``mixed_paged_attention`` -- a step's decode
+  and prefill sequences in one unpadded launch.
 
 All device work runs in ``libpaged_attention.so`` (hand-written HIP for
 gfx950, built by ``build.py``) through a C ABI; there is no CPU fallback.
@@ -19,8 +21,10 @@ module name ``vllm_jax_amd``::
         "vllm_jax_amd", "<repo>/vllm-jax_amd/__init__.py",
         submodule_search_locations=["<repo>/vllm-jax_amd"])
 """
-from .attention import (DecodeAttentionMetadata, PrefillAttentionMetadata, attention,  # noqa: F401
+from .attention import (DecodeAttentionMetadata, MixedAttentionMetadata, PrefillAttentionMetadata,  # noqa: F401
+                        attention,
                         attention_stored, gather_kv, qk_norm_rope_store, qwen3_attention_core,
                         update_kv_cache)
 from .kernels.decode_paged_attention import decode_paged_attention  # noqa: F401
+from .kernels.mixed_paged_attention import mixed_paged_attention  # noqa: F401
 from .kernels.prefill_paged_attention import prefill_paged_attention  # noqa: F401

@@ -73,6 +73,19 @@ SIGNATURES = {
         c_i64, c_i64, c_i64,           # page/slot/head strides
         c_vp,                          # stream
     ]),
+    "pa_mixed_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "pa_mixed": (ctypes.c_int, [
+        c_vp, c_i64, c_i64,            # q
+        c_vp, c_vp, c_i32, c_i32,      # caches, num_pages, page_size
+        c_i64, c_i64, c_i64,           # strides
+        c_vp, c_i64, c_i32,            # block_tables, bt_stride, pages_per_seq
+        c_vp, c_vp, c_vp,              # cu_seqlens_q, kv_lens, input_positions
+        c_i32, c_i32, c_i32, c_i32,    # batch, num_decodes, num_tokens, max_seqlen_q
+        c_i32, c_i32, c_i32,           # heads, kv heads, head_dim
+        c_f32, c_f32, c_f32,           # prefill_scale, decode_scale, soft_cap
+        c_vp, c_i64, c_i64,            # out
+        c_vp, c_sz, c_vp,              # workspace, bytes, stream
+    ]),
 }
 
 

@@ -14,7 +14,10 @@ prefill or decode kernel.  Differences from the reference, all deliberate:
   in bf16 (qwen3.py:207);
 * prefill passes ``cu_seqlens_k`` so a cached prefix can precede the new
   tokens (with ``cu_seqlens_k == cu_seqlens_q``, the engine's case, the
-  semantics are the reference's).
+  semantics are the reference's);
+* a third metadata type, ``MixedAttentionMetadata``, runs a step's decode
+  and prefill sequences together in one unpadded launch (the reference runs
+  them as two padded jitted calls, model_runner.py:310-333).
 """
 from __future__ import annotations
 
@@ -26,6 +29,7 @@ import torch
 from . import _lib
 from .kernels._common import bf16_round, require_bf16, require_device, stream_handle
 from .kernels.decode_paged_attention import decode_paged_attention
+from .kernels.mixed_paged_attention import mixed_paged_attention
 from .kernels.prefill_paged_attention import prefill_paged_attention
 
 USE_DECODE_PAGED_ATTENTION_KERNEL = True
@@ -54,7 +58,24 @@ class PrefillAttentionMetadata:
     max_seqlen_bucket: int = field(default=0)
 
 
-AttentionMetadata = Union[DecodeAttentionMetadata, PrefillAttentionMetadata]
+@dataclass
+class MixedAttentionMetadata:
+    """One scheduler step, unpadded: sequences ``0 .. num_decodes-1`` are
+    decode sequences (one q row, ``kv_lens`` = context length including the
+    new token, as ``context_lens`` of qwen3.py:17-22), the rest prefill
+    sequences (q rows ``cu_seqlens_q[b] .. cu_seqlens_q[b+1]``, kv length
+    ``kv_lens[b]``, positions as qwen3.py:25-34).  ``max_seqlen_q`` bounds
+    every prefill q length."""
+    input_positions: torch.Tensor
+    slot_mapping: torch.Tensor
+    block_tables: torch.Tensor
+    cu_seqlens_q: torch.Tensor
+    kv_lens: torch.Tensor
+    num_decodes: int
+    max_seqlen_q: int
+
+
+AttentionMetadata = Union[DecodeAttentionMetadata, PrefillAttentionMetadata, MixedAttentionMetadata]
 
 
 def update_kv_cache(kv_cache: torch.Tensor, slot_mapping: torch.Tensor, k: torch.Tensor,
@@ -175,7 +196,13 @@ def attention_stored(kv_cache: torch.Tensor, q: torch.Tensor, metadata: Attentio
         raise NotImplementedError("the dense fallbacks of qwen3.py:120-169 are not part of this library")
     k_pages = kv_cache[0].permute(2, 0, 1, 3)   # [Hkv, NB, BS, d] view
     v_pages = kv_cache[1].permute(2, 0, 1, 3)
-    if isinstance(metadata, PrefillAttentionMetadata):
+    if isinstance(metadata, MixedAttentionMetadata):
+        head_dim = q.shape[-1]
+        outputs = mixed_paged_attention(
+            q, k_pages, v_pages, metadata.block_tables, metadata.cu_seqlens_q, metadata.kv_lens,
+            metadata.input_positions, metadata.num_decodes, max_seqlen_q=metadata.max_seqlen_q,
+            decode_scale=1.0 / bf16_round(float(head_dim) ** 0.5))
+    elif isinstance(metadata, PrefillAttentionMetadata):
         outputs = prefill_paged_attention(
             q, k_pages, v_pages, metadata.block_tables, metadata.cu_seqlens_q,
             metadata.slot_mapping, metadata.input_positions,

@@ -1,0 +1,306 @@
+// One launch for a mixed batch of decode and prefill sequences on gfx950.
+//
+// The reference runs a scheduler step as two jitted calls, decode then
+// prefill, each padded to a power-of-two bucket (model_runner.py:310-333,
+// 243-255, 286-292).  Here one kernel covers both halves of the batch with
+// no padding: sequences 0 .. num_decodes-1 are decode sequences (one q row
+// each, split-K over their kv length), the rest are prefill sequences (ragged
+// causal q tiles).  Every workgroup has 512 threads and the prefill item's
+// 128 KiB of LDS; the grid is cut into regions:
+//
+//   [0, r1)    prefill items of the longest q-tile levels
+//   [r1, r2)   decode items (sequence, 4096-token chunk, kv head), 8 waves
+//              each, numbered XCD-grouped like decode_split_kernel
+//   [r2, r3)   the remaining prefill items
+//   [r3, r4)   zero pass: 512 token rows per workgroup, rows no item writes
+//
+// The hardware starts workgroups in index order, so the costliest items
+// (long causal q tiles) start first, the decode chunks (HBM streams) run
+// while those tiles still occupy other CUs, and short tiles fill the tail.
+// A decode item combines its 8 waves through the LDS of the prefill ring,
+// which it does not otherwise use.  When a decode sequence can span more
+// than one chunk, decode_merge_kernel follows as a second launch.
+#include <algorithm>
+
+#include "decode_impl.h"
+#include "prefill_impl.h"
+
+namespace pa {
+
+constexpr int kMixedDecodeWaves = kWaves;     // a decode item uses the whole workgroup
+constexpr int kZeroRowsPerBlock = kThreads;   // one row per thread in the zero pass
+#ifndef PA_MIXED_COST_RATIO
+#define PA_MIXED_COST_RATIO 2.6f
+#endif
+// Time of a 64-token prefill tile (256 q rows on the MFMA) over the time of
+// a 64-token decode step of one workgroup (HBM stream), both measured on
+// MI355X: prefill levels whose items cost more than a decode chunk go first.
+constexpr float kPrefillOverDecodeTile = PA_MIXED_COST_RATIO;
+
+struct MixedParams {
+  PrefillParams pre;  // the prefill sequences (arrays start at entry num_decodes)
+  DecodeParams dec;   // the decode sequences (entries 0 .. num_decodes-1)
+  int32_t r1, r2, r3, r4;
+  int32_t pre_head;     // prefill items in region [0, r1)
+  int32_t n_dec_items;  // decode items in region [r1, r2)
+  // zero pass
+  const int32_t* cu_q;
+  int32_t batch, num_decodes, num_tokens, max_seqlen_q, num_heads;
+  uint16_t* out;
+  int64_t o_ts, o_hs;
+};
+
+// Rows of tokens [512 zb, 512 zb + 512) that no item writes: outside every
+// sequence, past the first row of a decode sequence, or at offset >=
+// max_seqlen_q in a prefill sequence.
+__device__ __forceinline__ void mixed_zero_rows(const MixedParams& m, int zb) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t base = (int64_t)zb * kZeroRowsPerBlock + 64 * wave;
+  const int64_t t = base + lane;
+  bool need = false;
+  if (t < m.num_tokens) {
+    bool covered = false;
+    if (t >= m.cu_q[0] && t < m.cu_q[m.batch]) {
+      int lo = 0, hi = m.batch;  // invariant: cu_q[lo] <= t < cu_q[hi]
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (m.cu_q[mid] <= t) lo = mid;
+        else hi = mid;
+      }
+      const int64_t off = t - m.cu_q[lo];
+      covered = lo < m.num_decodes ? off == 0 : off < m.max_seqlen_q;
+    }
+    need = !covered;
+  }
+  uint64_t todo = __builtin_amdgcn_ballot_w64(need);
+  const int chunks = m.num_heads * (kPHeadDim / 8);
+  while (todo) {
+    const int l = __builtin_ctzll(todo);
+    todo &= todo - 1;
+    uint16_t* row = m.out + (base + l) * m.o_ts;
+    for (int c = lane; c < chunks; c += 64)
+      st16(row + (int64_t)(c / (kPHeadDim / 8)) * m.o_hs + 8 * (c % (kPHeadDim / 8)), u32x4{0, 0, 0, 0});
+  }
+}
+
+template <bool kSoftCap, bool kAlignedP, bool kAlignedD>
+__global__ void __launch_bounds__(kThreads, 1)
+mixed_kernel(MixedParams m) {
+  const int bid = blockIdx.x;
+  if (bid >= m.r1 && bid < m.r2) {
+    const int item = xcd_grouped_item(bid - m.r1, m.r2 - m.r1);
+    if (item < m.n_dec_items) {
+      // [8 waves][16][d] floats fill the K ring exactly; m and l go to the V ring
+      float* red_o = reinterpret_cast<float*>(&k_lds[0][0]);
+      float* red_m = reinterpret_cast<float*>(&v_lds[0][0]);
+      decode_item<kMixedDecodeWaves, kAlignedD, kSoftCap>(m.dec, item, red_o, red_m, red_m + 16 * kMixedDecodeWaves);
+    }
+    return;
+  }
+  if (bid >= m.r3) {
+    mixed_zero_rows(m, bid - m.r3);
+    return;
+  }
+  // one call site for both prefill regions (the body is large)
+  const int pre_bid = bid < m.r1 ? bid : m.pre_head + (bid - m.r2);
+  if (bid < m.r1 && bid >= m.pre_head) return;  // padding of region 1
+  prefill_body<kSoftCap, kAlignedP>(m.pre, pre_bid);
+}
+
+static_assert(sizeof(float) * kMixedDecodeWaves * 16 * kPHeadDim <= sizeof(uint16_t) * kStages * kTileElems,
+              "decode combine must fit the K ring");
+
+// Tokens per decode item (a multiple of the 16-token step): eight waves take
+// up to twice the chunk of the four-wave decode kernel.  With 16-aligned pages
+// the chunk is whole pages, at most 64 of them (one page id per lane).
+static int mixed_decode_chunk(int page_size) {
+  constexpr int kMax = 4096;
+  if (page_size % kDecodeStep != 0) return kMax;
+  return 64 * page_size <= kMax ? 64 * page_size : (kMax / page_size) * page_size;
+}
+
+static int mixed_decode_chunks(int32_t pages_per_seq, int32_t page_size) {
+  const int64_t max_tokens = (int64_t)pages_per_seq * page_size;
+  const int chunk = mixed_decode_chunk(page_size);
+  return (int)((max_tokens + chunk - 1) / chunk);
+}
+
+static int64_t round8(int64_t x) { return (x + 7) & ~(int64_t)7; }
+
+}  // namespace pa
+
+using namespace pa;
+
+extern "C" size_t pa_mixed_workspace_size(int32_t num_decodes, int32_t num_heads, int32_t head_dim,
+                                          int32_t pages_per_seq, int32_t page_size) {
+  if (num_decodes <= 0 || num_heads <= 0 || head_dim <= 0 || pages_per_seq <= 0 || page_size <= 0) return 0;
+  const int chunks = mixed_decode_chunks(pages_per_seq, page_size);
+  if (chunks <= 1) return 0;  // every decode sequence is finished inside its item
+  return (size_t)num_decodes * num_heads * chunks * ((size_t)head_dim + 2) * sizeof(float);
+}
+
+extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                        const uint16_t* k_cache, const uint16_t* v_cache,
+                        int32_t num_pages, int32_t page_size,
+                        int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                        const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                        const int32_t* cu_seqlens_q, const int32_t* kv_lens, const int32_t* input_positions,
+                        int32_t batch, int32_t num_decodes, int32_t num_tokens, int32_t max_seqlen_q,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                        float prefill_scale, float decode_scale, float soft_cap,
+                        uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
+                        void* workspace, size_t workspace_bytes, void* stream) {
+  if (batch < 0 || num_decodes < 0 || num_decodes > batch || num_tokens < 0 || max_seqlen_q < 0 ||
+      num_heads <= 0 || num_kv_heads <= 0 || num_pages <= 0 || page_size <= 0 || pages_per_seq < 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "pa_mixed: bad sizes (batch=%d, num_decodes=%d, num_tokens=%d, max_seqlen_q=%d, num_heads=%d, "
+                "num_kv_heads=%d, num_pages=%d, page_size=%d, pages_per_seq=%d)",
+                batch, num_decodes, num_tokens, max_seqlen_q, num_heads, num_kv_heads, num_pages, page_size,
+                pages_per_seq);
+  if (num_heads % num_kv_heads != 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "pa_mixed: Number of Q heads must be divisible by number of KV heads. Got %d and %d.", num_heads,
+                num_kv_heads);
+  if (head_dim != kPHeadDim)
+    return fail(PA_ERR_UNSUPPORTED, "pa_mixed: head_dim %d not supported (only %d)", head_dim, kPHeadDim);
+  const int group = num_heads / num_kv_heads;
+  if (group > 16)
+    return fail(PA_ERR_UNSUPPORTED, "pa_mixed: %d q heads per kv head not supported (max 16)", group);
+  if (num_tokens == 0) return PA_OK;
+  if (!q || !out || !cu_seqlens_q || !input_positions ||
+      (batch > 0 && (!k_cache || !v_cache || !block_tables || !kv_lens)))
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_mixed: null pointer");
+  const uintptr_t align_bits = (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out;
+  if ((align_bits & 15u) || (q_tok_stride | q_head_stride | page_stride | slot_stride | head_stride |
+                             out_tok_stride | out_head_stride) % 8)
+    return fail(PA_ERR_UNSUPPORTED, "pa_mixed: operands must be 16-byte aligned with strides multiple of 8");
+  if ((int64_t)pages_per_seq * page_size > 0x7fffffffLL)
+    return fail(PA_ERR_UNSUPPORTED, "pa_mixed: block table spans more than 2^31 tokens");
+  const int n_chunks = pages_per_seq > 0 ? mixed_decode_chunks(pages_per_seq, page_size) : 0;
+  const size_t need = pa_mixed_workspace_size(num_decodes, num_heads, head_dim, pages_per_seq, page_size);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(PA_ERR_WORKSPACE, "pa_mixed: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  const float cap = soft_cap > 0.f ? soft_cap : 0.f;
+
+  MixedParams m;
+  // ---- prefill half: entries num_decodes .. batch-1
+  const int n_pre = batch - num_decodes;
+  PrefillParams& pp = m.pre;
+  pp.q = q;
+  pp.q_ts = q_tok_stride;
+  pp.q_hs = q_head_stride;
+  pp.k_cache = k_cache;
+  pp.v_cache = v_cache;
+  pp.num_pages = num_pages;
+  pp.page_size = page_size;
+  pp.page_stride = page_stride;
+  pp.slot_stride = slot_stride;
+  pp.head_stride = head_stride;
+  pp.block_tables = block_tables ? block_tables + (int64_t)num_decodes * bt_stride : nullptr;
+  pp.bt_stride = bt_stride;
+  pp.pages_per_seq = pages_per_seq;
+  pp.cu_q = cu_seqlens_q + num_decodes;
+  pp.cu_k = nullptr;
+  pp.kv_lens = kv_lens ? kv_lens + num_decodes : nullptr;
+  pp.positions = input_positions;
+  pp.batch = n_pre;
+  pp.num_tokens = num_tokens;
+  pp.num_heads = num_heads;
+  pp.num_kv_heads = num_kv_heads;
+  pp.group = group;
+  pp.tile_tokens = kRows / group;
+  pp.n_qtiles = n_pre > 0 ? (max_seqlen_q + pp.tile_tokens - 1) / pp.tile_tokens : 0;
+  pp.max_seqlen_q = max_seqlen_q;
+  pp.soft_cap = cap;
+  pp.logit_scale = cap > 0.f ? prefill_scale : prefill_scale * kLog2e;
+  pp.out = out;
+  pp.o_ts = out_tok_stride;
+  pp.o_hs = out_head_stride;
+  // ---- decode half: entries 0 .. num_decodes-1
+  DecodeParams& dp = m.dec;
+  dp.q = q;
+  dp.q_bs = q_tok_stride;
+  dp.q_hs = q_head_stride;
+  dp.k_cache = k_cache;
+  dp.v_cache = v_cache;
+  dp.num_pages = num_pages;
+  dp.page_size = page_size;
+  dp.page_stride = page_stride;
+  dp.slot_stride = slot_stride;
+  dp.head_stride = head_stride;
+  dp.block_tables = block_tables;
+  dp.bt_stride = bt_stride;
+  dp.pages_per_seq = pages_per_seq;
+  dp.lengths = kv_lens;
+  dp.batch = num_decodes;
+  dp.num_heads = num_heads;
+  dp.num_kv_heads = num_kv_heads;
+  dp.group = group;
+  dp.chunk = mixed_decode_chunk(page_size);
+  dp.n_chunks = n_chunks;
+  dp.soft_cap = cap;
+  dp.logit_scale = cap > 0.f ? decode_scale : decode_scale * kLog2e;
+  dp.ws_o = reinterpret_cast<float*>(workspace);
+  dp.ws_ml = need > 0 ? dp.ws_o + (size_t)num_decodes * num_heads * n_chunks * head_dim : nullptr;
+  dp.out = out;
+  dp.out_bs = out_tok_stride;
+  dp.out_hs = out_head_stride;
+  dp.rows = cu_seqlens_q;
+  dp.row_limit = num_tokens;
+  dp.zero_empty = 1;
+  // ---- zero pass
+  m.cu_q = cu_seqlens_q;
+  m.batch = batch;
+  m.num_decodes = num_decodes;
+  m.num_tokens = num_tokens;
+  m.max_seqlen_q = max_seqlen_q;
+  m.num_heads = num_heads;
+  m.out = out;
+  m.o_ts = out_tok_stride;
+  m.o_hs = out_head_stride;
+
+  // ---- regions.  Prefill level l (q tile n_qtiles-1-l) reaches kv index
+  // (n_qtiles-l)*tile_tokens; it goes before the decode items while it costs
+  // more than one decode chunk.
+  const int64_t pairs = (int64_t)n_pre * num_kv_heads;
+  const int64_t dec_tokens = std::min<int64_t>(dp.chunk, (int64_t)pages_per_seq * page_size);
+  int head_levels = 0;
+  while (head_levels < pp.n_qtiles &&
+         (float)(pp.n_qtiles - head_levels) * pp.tile_tokens * kPrefillOverDecodeTile >= (float)dec_tokens)
+    ++head_levels;
+  if (num_decodes == 0) head_levels = pp.n_qtiles;
+  const int64_t pre_items = (int64_t)pp.n_qtiles * pairs;
+  const int64_t pre_head = (int64_t)head_levels * pairs;
+  const int64_t dec_items = (int64_t)num_decodes * n_chunks * num_kv_heads;
+  const int64_t r1 = round8(pre_head);
+  const int64_t r2 = r1 + round8(dec_items);
+  const int64_t r3 = r2 + (pre_items - pre_head);
+  const int64_t r4 = r3 + (num_tokens + kZeroRowsPerBlock - 1) / kZeroRowsPerBlock;
+  if (r4 > 0x7fffffff)
+    return fail(PA_ERR_UNSUPPORTED, "pa_mixed: grid of %lld workgroups too large", (long long)r4);
+  m.r1 = (int32_t)r1;
+  m.r2 = (int32_t)r2;
+  m.r3 = (int32_t)r3;
+  m.r4 = (int32_t)r4;
+  m.pre_head = (int32_t)pre_head;
+  m.n_dec_items = (int32_t)dec_items;
+
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)r4), block(kThreads);
+  const bool aligned_p = page_size % kTileN == 0;
+  const bool aligned_d = page_size % kDecodeStep == 0;
+  if (cap > 0.f) {
+    if (aligned_p) mixed_kernel<true, true, true><<<grid, block, 0, s>>>(m);
+    else if (aligned_d) mixed_kernel<true, false, true><<<grid, block, 0, s>>>(m);
+    else mixed_kernel<true, false, false><<<grid, block, 0, s>>>(m);
+  } else {
+    if (aligned_p) mixed_kernel<false, true, true><<<grid, block, 0, s>>>(m);
+    else if (aligned_d) mixed_kernel<false, false, true><<<grid, block, 0, s>>>(m);
+    else mixed_kernel<false, false, false><<<grid, block, 0, s>>>(m);
+  }
+  int rc = launch_status("pa_mixed");
+  if (rc || need == 0 || num_decodes == 0) return rc;
+  launch_decode_merge(dp, s);
+  return launch_status("pa_mixed(merge)");
+}

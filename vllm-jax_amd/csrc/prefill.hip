@@ -1,581 +1,14 @@
-// Ragged causal GQA paged prefill for gfx950.
-//
-// Workgroup = (q tile, sequence, kv head); 8 waves x 32 rows = 256 rows, where
-// a row is a (query token, q head of this kv head) pair: row n of the tile is
-// token n / G, head n % G (G = q heads per kv head).  Packing the G heads into
-// the MFMA dimension makes every K/V tile staged in LDS serve G x tokens rows.
-// One workgroup per CU, two waves per SIMD.
-//
-// KV tiles of 64 tokens go through a 3-stage LDS ring filled by direct
-// global->LDS loads (global_load_lds_dwordx4) through the block table, issued
-// two tiles ahead of use.  Per tile and wave:
-//   S^T[t][n] = K[t][:] . Q[n][:]      v_mfma_f32_32x32x16_bf16, K rows read
-//                                       with ds_read_b128, Q^T kept in VGPRs
-//   online softmax per row n            row n = lane % 32: the row max needs one
-//                                       permlane32 swap and rescaling O is
-//                                       lane-local; the reference max only
-//                                       moves when a row max grows by more than
-//                                       2^8, so O is rarely rescaled
-//   O^T[d][n] += V^T[d][t] . P^T[t][n]  V^T operand read from the row-major V
-//                                       tile with ds_read_b64_tr_b16 (gfx950's
-//                                       transposing LDS read), P^T straight from
-//                                       the S^T accumulator registers
-// The softmax runs per 32-token half so one half's VALU work overlaps the
-// other half's MFMAs.  LDS tiles are 64 rows x 256 B with 16-byte chunks
-// XOR-swizzled per row so that both the K reads and the transposing V reads
-// are bank-conflict free.  KV tiles entirely above the causal diagonal of the
-// q tile are never loaded; the mask is evaluated only on tiles that straddle
-// it or the kv length.  Workgroups are dispatched from the last q tile down so
-// the longest causal rows start first.
-#include <type_traits>
-
-#include "pa_common.h"
-#include "pa_errors.h"
+// Ragged causal GQA paged prefill for gfx950: the kernel entry and its host
+// launcher.  The work item (one q tile of one sequence and kv head) is
+// prefill_body in prefill_impl.h.
+#include "prefill_impl.h"
 
 namespace pa {
-
-constexpr int kPHeadDim = 128;
-constexpr int kWaves = 8;         // waves per workgroup, 32 rows each
-constexpr int kThreads = 64 * kWaves;
-constexpr int kRows = 32 * kWaves;  // rows per workgroup
-constexpr int kTileN = 64;        // kv tokens per tile
-constexpr int kStages = 4;        // LDS ring depth: loads run two tiles ahead
-constexpr int kTileElems = kTileN * kPHeadDim;
-constexpr float kRescaleSlack = 8.f;  // log2 units the running max may lag
-// instruction classes of __builtin_amdgcn_sched_group_barrier
-constexpr int kSchedMfma = 0x008;
-constexpr int kSchedDsRead = 0x100;
-#ifndef PA_AHEAD_MFMA
-#define PA_AHEAD_MFMA 4
-#endif
-constexpr int kAheadMfma = PA_AHEAD_MFMA;  // MFMAs between an LDS read and the MFMA it feeds
-
-struct PrefillParams {
-  const uint16_t* q;
-  int64_t q_ts, q_hs;
-  const uint16_t* k_cache;
-  const uint16_t* v_cache;
-  int32_t num_pages, page_size;
-  int64_t page_stride, slot_stride, head_stride;
-  const int32_t* block_tables;
-  int64_t bt_stride;
-  int32_t pages_per_seq;
-  const int32_t* cu_q;
-  const int32_t* cu_k;  // may be null
-  const int32_t* positions;
-  int32_t batch, num_tokens, num_heads, num_kv_heads, group, tile_tokens, n_qtiles, max_seqlen_q;
-  float logit_scale;  // scale*log2e (soft cap off) or scale
-  float soft_cap;
-  uint16_t* out;
-  int64_t o_ts, o_hs;
-};
-
-typedef s16x4 __attribute__((address_space(3))) * lds_s16x4_ptr;
-typedef void __attribute__((address_space(3))) * lds_void_ptr;
-typedef const char __attribute__((address_space(3))) * lds_cbytes;
-
-// Transposing 8-byte LDS read (ds_read_b64_tr_b16) at LDS byte address `a`.
-__device__ __forceinline__ s16x4 ds_read_tr16(lds_cbytes a) {
-  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_ptr)(a));
-}
-
-// 16-byte LDS read (ds_read_b128) at LDS byte address `a`.
-__device__ __forceinline__ u32x4 ds_read16(lds_cbytes a) {
-  return *reinterpret_cast<const u32x4 __attribute__((address_space(3)))*>(a);
-}
-
-// Physical 16-byte chunk of logical chunk c in tile row r.
-__device__ __forceinline__ int swz(int r, int c) {
-  return c ^ (((r & 3) << 2) | ((r >> 2) & 3));
-}
-
-// Work item of workgroup `bid`: (q tile, sequence b, kv head).  Items are
-// ordered from the last q tile down (longest causal rows first).  Within one
-// q-tile level the (b, kv head) pairs are placed so that, with workgroups
-// dealt round-robin to the 8 XCDs, an XCD always serves the same pairs and
-// holds one kv head of every sequence: all q tiles of a (b, head) pair then
-// share that XCD's L2, and every XCD carries the same mix of sequence lengths.
-__device__ __forceinline__ void prefill_item(int bid, int batch, int hkv, int n_qtiles, int& qt, int& b, int& kvh) {
-  const int pairs = batch * hkv;
-  const int level = bid / pairs;
-  const int j = bid - level * pairs;
-  qt = n_qtiles - 1 - level;
-  if (hkv % 8 == 0) {
-    const int xcd = j & 7;
-    const int k = j >> 3;             // 0 .. batch*hkv/8 - 1
-    const int per_b = hkv >> 3;
-    // An XCD deals its workgroups round-robin to its shader engines, so its
-    // k-th workgroup of a level lands on the same engine at every level;
-    // rotating the sequences by level gives every engine every sequence.
-    const int bk = k / per_b;
-    b = bk + level % batch;
-    b = b >= batch ? b - batch : b;
-    kvh = 8 * (k - bk * per_b) + ((xcd - b) & 7);
-  } else {
-    b = j / hkv;
-    kvh = j - b * hkv;
-  }
-}
-
-// One 16-byte-per-lane global->LDS load (global_load_lds_dwordx4): lane l's
-// 16 bytes land at LDS byte address lds_block + 16*l.  Issued as inline asm so
-// the compiler does not insert its conservative "wait for every LDS DMA"
-// before unrelated LDS reads; completion is tracked explicitly with
-// wait_vm_lgkm0 + s_barrier before any wave reads the stage.
-__device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_block) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_block) : "memory", "m0");
-}
-
-// s_waitcnt with vmcnt = N (N < 16), lgkmcnt = 0, expcnt untouched (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-  static_assert(N >= 0 && N < 16, "vmcnt field");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8));
-}
 
 template <bool kSoftCap, bool kAligned>
 __global__ void __launch_bounds__(kThreads, 1)
 prefill_kernel(PrefillParams p) {
-  // One object per ring stage: the compiler's LDS-DMA wait tracking then sees
-  // that reads of stage s never alias loads in flight into the other stages
-  // (with a single array it waits for every DMA before any LDS read).
-  __shared__ __attribute__((aligned(1024))) uint16_t k_lds[kStages][kTileElems];
-  __shared__ __attribute__((aligned(1024))) uint16_t v_lds[kStages][kTileElems];
-  __shared__ int red_max[kWaves], red_min[kWaves];
-  auto k_stage = [&](auto c) __attribute__((always_inline)) -> uint16_t* { return k_lds[decltype(c)::value]; };
-  auto v_stage = [&](auto c) __attribute__((always_inline)) -> uint16_t* { return v_lds[decltype(c)::value]; };
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
-  const int hkv = p.num_kv_heads;
-  int qt, b, kvh;
-  prefill_item(blockIdx.x, p.batch, hkv, p.n_qtiles, qt, b, kvh);
-
-  const int q0 = p.cu_q[b];
-  const int lq = p.cu_q[b + 1] - q0;
-  // rows past max_seqlen_q are left to the zero pass; rows past the token
-  // count (malformed cu_seqlens) are never touched
-  const int lq_rows = (q0 < 0 || q0 >= p.num_tokens) ? 0 : min(min(lq, p.max_seqlen_q), p.num_tokens - q0);
-  const int tok0 = qt * p.tile_tokens;
-  if (tok0 >= lq_rows) return;  // uniform across the workgroup
-  // kv lengths past the block table's span are clamped to it
-  const int lk = min(p.cu_k ? p.cu_k[b + 1] - p.cu_k[b] : lq, p.pages_per_seq * p.page_size);
-  const int kv_pos_off = p.positions[q0] - (lk - lq);
-
-  // ---- this lane's row
-  const int n = lane & 31;
-  const int h = lane >> 5;
-  const int row = wave * 32 + n;
-  const int rtok = tok0 + row / p.group;
-  const int rhead = row % p.group;
-  const bool row_ok = row < p.tile_tokens * p.group && rtok < lq_rows;
-  const int qpos = row_ok ? p.positions[q0 + rtok] : 0;
-
-  // ---- q tile position range -> kv tile range
-  {
-    int mx = row_ok ? qpos : INT_MIN;
-    int mn = row_ok ? qpos : INT_MAX;
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-      mx = max(mx, __shfl_xor(mx, o));
-      mn = min(mn, __shfl_xor(mn, o));
-    }
-    if (lane == 0) {
-      red_max[wave] = mx;
-      red_min[wave] = mn;
-    }
-  }
-
-  // Q^T operand (B of S^T): k-step ks covers d = 16ks + 8h .. +8.
-  bf16x8 qt_op[8];
-  {
-    const uint16_t* qrow = p.q + (int64_t)(q0 + (row_ok ? rtok : 0)) * p.q_ts +
-                           (int64_t)(kvh * p.group + rhead) * p.q_hs + 8 * h;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-      qt_op[ks] = as_bf16x8(row_ok ? ld16(qrow + 16 * ks) : u32x4{0, 0, 0, 0});
-  }
-  // Retire every compiler-visible vector load here: the tile DMAs below are
-  // invisible to the compiler's wait tracking, so nothing it issued may still
-  // be in flight when they start (else it would drain them at the loop head).
-  wait_vm_lgkm0<0>();
-  __syncthreads();
-  int qpos_max = red_max[0], qpos_min = red_min[0];
-#pragma unroll
-  for (int w = 1; w < kWaves; ++w) {
-    qpos_max = max(qpos_max, red_max[w]);
-    qpos_min = min(qpos_min, red_min[w]);
-  }
-  // kv index j is visible to some row iff j < lk and j + kv_pos_off <= qpos_max
-  const int64_t kv_hi64 = min((int64_t)lk, (int64_t)qpos_max - kv_pos_off + 1);
-  const int kv_hi = kv_hi64 < 0 ? 0 : (int)kv_hi64;
-  const int n_tiles = (kv_hi + kTileN - 1) / kTileN;
-  // tiles [0, n_free) need no mask: every token is < lk and visible to every row
-  const int64_t free_hi = min((int64_t)lk, (int64_t)qpos_min - kv_pos_off + 1);
-  const int n_free = free_hi < 0 ? 0 : (int)(free_hi / kTileN);
-
-  // ---- direct global->LDS tile loader.  A tile is 16 blocks of 1 KiB
-  // (4 rows each); wave w fills blocks kBlk*w .. kBlk*w + kBlk-1 of K and V.
-  // Lane l writes LDS bytes 16*l of a block, i.e. row 4blk + l/16, physical
-  // chunk l%16, so it loads the logical chunk swz(row, l%16) of that token.
-  constexpr int kBlk = 16 / kWaves;
-  const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
-  const int ld_r = lane >> 4;            // row within a 1 KiB block
-  const int ld_p = lane & 15;            // physical chunk
-  const int64_t head_off = (int64_t)kvh * p.head_stride;
-  uint32_t ld_off[kBlk];                 // per-lane element offset of the row within a page
-#pragma unroll
-  for (int i = 0; i < kBlk; ++i) {
-    const int r = 4 * (kBlk * wave + i) + ld_r;
-    ld_off[i] = (uint32_t)(r * (int32_t)p.slot_stride + 8 * swz(r, ld_p));
-  }
-  // Tile DMA in two steps: tile_addrs() computes this wave's 2*kBlk global
-  // addresses (K block 0, V block 0, K block 1, ...), dma_issue() issues one
-  // of them, so the loads can be spread through other work.  In the aligned
-  // case the tile's page id comes in raw (read ahead of time by the caller).
-  struct TileAddrs {
-    const uint16_t* g[2 * kBlk];
-  };
-  auto page_raw = [&](int j0) __attribute__((always_inline)) {
-    const int lp = min(j0 / p.page_size, p.pages_per_seq - 1);  // stays inside the table row
-    const __attribute__((address_space(4))) int32_t* c = (const __attribute__((address_space(4))) int32_t*)bt_row;
-    return c[lp];
-  };
-  auto tile_addrs = [&](int j0, int32_t raw) __attribute__((always_inline)) {
-    TileAddrs a;
-    if constexpr (kAligned) {
-      // page_size % 64 == 0: the whole tile lies in one page
-      const int lp = j0 / p.page_size;
-      const int32_t page = raw < 0 ? 0 : (raw >= p.num_pages ? p.num_pages - 1 : raw);
-      const int64_t pbase = (int64_t)page * p.page_stride + (int64_t)(j0 - lp * p.page_size) * p.slot_stride + head_off;
-      if (j0 + kTileN <= lk) {
-#pragma unroll
-        for (int i = 0; i < kBlk; ++i) {
-          a.g[2 * i] = p.k_cache + pbase + ld_off[i];
-          a.g[2 * i + 1] = p.v_cache + pbase + ld_off[i];
-        }
-      } else {
-        const int last = lk - 1 - j0;  // clamp onto a valid token: masked, never stale
-#pragma unroll
-        for (int i = 0; i < kBlk; ++i) {
-          const int r = 4 * (kBlk * wave + i) + ld_r;
-          const int64_t o = pbase + (int64_t)min(r, last) * p.slot_stride + 8 * swz(r, ld_p);
-          a.g[2 * i] = p.k_cache + o;
-          a.g[2 * i + 1] = p.v_cache + o;
-        }
-      }
-    } else {
-      int32_t pages[kBlk];
-#pragma unroll
-      for (int i = 0; i < kBlk; ++i) {
-        const int r = 4 * (kBlk * wave + i) + ld_r;
-        const int j = min(j0 + r, lk - 1);
-        pages[i] = safe_page(bt_row, j / p.page_size, p.num_pages);
-      }
-#pragma unroll
-      for (int i = 0; i < kBlk; ++i) {
-        const int r = 4 * (kBlk * wave + i) + ld_r;
-        const int j = min(j0 + r, lk - 1);
-        const int64_t o = (int64_t)pages[i] * p.page_stride + (int64_t)(j % p.page_size) * p.slot_stride +
-                          head_off + 8 * swz(r, ld_p);
-        a.g[2 * i] = p.k_cache + o;
-        a.g[2 * i + 1] = p.v_cache + o;
-      }
-    }
-    return a;
-  };
-  const uint32_t k_lds0 = (uint32_t)(uintptr_t)(lds_void_ptr)(&k_lds[0][0]);
-  const uint32_t v_lds0 = (uint32_t)(uintptr_t)(lds_void_ptr)(&v_lds[0][0]);
-  auto dma_issue = [&](const TileAddrs& a, int i, int stage) __attribute__((always_inline)) {
-    const uint32_t base = (i & 1) ? v_lds0 : k_lds0;
-    dma16(a.g[i], base + (uint32_t)(stage * kTileElems * 2 + (kBlk * wave + (i >> 1)) * 1024));
-  };
-  auto issue_tile = [&](int j0, int stage) __attribute__((always_inline)) {
-    const TileAddrs a = tile_addrs(j0, kAligned ? page_raw(j0) : 0);
-#pragma unroll
-    for (int i = 0; i < 2 * kBlk; ++i) dma_issue(a, i, stage);
-  };
-  constexpr int kDmaPerTile = 2 * kBlk;  // vm instructions one wave issues per tile
-
-  // ---- per-lane LDS read offsets (bytes), fixed for the whole kernel.
-  // K (A of S^T): row 32mt + n, logical chunk 2ks + h; the swizzle of a row
-  // only depends on its low 4 bits, i.e. on n.
-  const int fn = ((n & 3) << 2) | ((n >> 2) & 3);
-  uint32_t koff[8];
-#pragma unroll
-  for (int ks = 0; ks < 8; ++ks) koff[ks] = n * 256 + 16 * ((2 * ks + h) ^ fn);
-  // V^T (tr16): lane = 16*gamma + s reads row tokbase + 4h + s/4 (+8) and
-  // logical column 32dt + 16(gamma%2) + 4(s%4): chunk 4dt + 2(gamma%2) +
-  // (s%4)/2, byte 8*(s%2) inside it.  tokbase is a multiple of 16, so the
-  // row's swizzle is that of tr_row (or tr_row + 8).
-  const int tr_s = lane & 15;
-  const int tr_gamma = lane >> 4;
-  const int tr_row = 4 * h + (tr_s >> 2);
-  const int f0 = ((tr_row & 3) << 2) | ((tr_row >> 2) & 3);
-  const int f1 = (((tr_row + 8) & 3) << 2) | (((tr_row + 8) >> 2) & 3);
-  uint32_t voff0[4], voff1[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt) {
-    const int c = 4 * dt + 2 * (tr_gamma & 1) + ((tr_s & 3) >> 1);
-    voff0[dt] = tr_row * 256 + 16 * (c ^ f0) + 8 * (tr_s & 1);
-    voff1[dt] = (tr_row + 8) * 256 + 16 * (c ^ f1) + 8 * (tr_s & 1);
-  }
-
-  f32x16 acc_o[4];
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc_o[dt][i] = 0.f;
-  float m_ref = -1e30f;  // reference max (log2 units) of the accumulators
-  // running row sums, one per quarter of a tile: four short dot2c chains
-  // instead of one long one
-  float l_part[4] = {0.f, 0.f, 0.f, 0.f};
-  const float cs = kSoftCap ? 1.f : p.logit_scale;  // multiplier applied inside the exponent
-  f32x16 s_acc[2];  // S^T of the tile between its QK and its softmax
-  bf16x8 pt[4];     // P^T of the tile between its softmax and its PV
-
-  // ---- work pieces.  M(t) = PV(t-1) + QK(t) is MFMA work, SM(t) = softmax of
-  // tile t is VALU work.  Waves 0-3 (group A) and 4-7 (group B) share the
-  // SIMDs pairwise and run the same sequence half a step apart:
-  //   segment 2t:   A: M(t)    B: SM(t-1)
-  //   segment 2t+1: A: SM(t)   B: M(t)
-  // with a workgroup barrier after every segment, so on every SIMD one wave
-  // feeds the matrix core while the other one does its softmax (ping-pong).
-  auto qk = [&](auto kst) __attribute__((always_inline)) {
-    const lds_cbytes kt = (lds_cbytes)(k_stage(kst));
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s_acc[mt][i] = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) {
-        const bf16x8 a = as_bf16x8(ds_read16(kt + koff[ks] + mt * 8192));
-        s_acc[mt] = mfma32(a, qt_op[ks], s_acc[mt]);
-      }
-    }
-  };
-  auto pv = [&](auto vst) __attribute__((always_inline)) {
-    const lds_cbytes vt = (lds_cbytes)(v_stage(vst));
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      // k-step u: tokens 32(u/2) + 16(u%2) + {4h + r, 8 + 4h + r}
-      const int rb = (32 * (u >> 1) + 16 * (u & 1)) * 256;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const s16x4 lo = ds_read_tr16(vt + rb + voff0[dt]);
-        const s16x4 hi = ds_read_tr16(vt + rb + voff1[dt]);
-        const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
-        const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
-        const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
-        acc_o[dt] = mfma32(as_bf16x8(a), pt[u], acc_o[dt]);
-      }
-    }
-  };
-  auto softmax = [&](int t, auto&& between) __attribute__((always_inline)) {
-    const int j0 = t * kTileN;
-    if constexpr (kSoftCap) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          s_acc[mt][i] = p.soft_cap * kLog2e * tanhf(s_acc[mt][i] * p.logit_scale / p.soft_cap);
-    }
-    // s_acc[mt][i] = S[row n][token j0 + 32mt + 8(i/4) + 4h + i%4]
-    if (t >= n_free) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int j = j0 + 32 * mt + 8 * (i >> 2) + 4 * h + (i & 3);
-          const bool vis = j < lk && j + kv_pos_off <= qpos;
-          s_acc[mt][i] = vis ? s_acc[mt][i] : -INFINITY;
-        }
-    }
-    // four independent max3 chains (one per 16-token quarter)
-    float mq[4];
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int mt = q4 >> 1, b0 = 8 * (q4 & 1);
-      float m = __builtin_fmaxf(__builtin_fmaxf(s_acc[mt][b0], s_acc[mt][b0 + 1]), s_acc[mt][b0 + 2]);
-      m = __builtin_fmaxf(__builtin_fmaxf(m, s_acc[mt][b0 + 3]), s_acc[mt][b0 + 4]);
-      m = __builtin_fmaxf(__builtin_fmaxf(m, s_acc[mt][b0 + 5]), s_acc[mt][b0 + 6]);
-      mq[q4] = __builtin_fmaxf(m, s_acc[mt][b0 + 7]);
-    }
-    float mx = __builtin_fmaxf(__builtin_fmaxf(mq[0], mq[1]), __builtin_fmaxf(mq[2], mq[3]));
-    mx = max_xor32(mx) * cs;
-    // Move the reference max only when this tile's max exceeds it by more
-    // than the slack (any lane in the wave): exponents stay <= 2^slack.
-    if (__any(mx > m_ref + kRescaleSlack)) {
-      const float m_new = fmaxf(m_ref, mx);
-      const float corr = fast_exp2(m_ref - m_new);
-      m_ref = m_new;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) l_part[u] *= corr;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) acc_o[dt] = acc_o[dt] * corr;
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      between(u);
-      const int mt = u >> 1;
-      const int base = 8 * (u & 1);
-      u32x4 w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float a = fast_exp2(__builtin_fmaf(s_acc[mt][base + 2 * e], cs, -m_ref));
-        const float c = fast_exp2(__builtin_fmaf(s_acc[mt][base + 2 * e + 1], cs, -m_ref));
-        w[e] = pack_bf16x2(a, c);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) l_part[u] = dot2_bf16_ones(w[e], l_part[u]);
-      // Materialise P here: otherwise the compiler sinks the exp work past
-      // the barrier into the next MFMA segment, undoing the ping-pong.
-      asm volatile("" : "+v"(w));
-      pt[u] = as_bf16x8(w);
-    }
-    asm volatile("" : "+v"(l_part[0]), "+v"(l_part[1]), "+v"(l_part[2]), "+v"(l_part[3]));
-  };
-  auto barrier = [&]() __attribute__((always_inline)) {
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_barrier();
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // Every wave runs the same sequence  M(0) SM(0) M(1) SM(1) ... M(n)  with a
-  // barrier after each piece; group B starts with one idle barrier (and group
-  // A ends with one), which shifts B half a step behind A: A's M(t) runs in
-  // global segment 2t, B's in 2t+1.
-  //
-  // Tile T sits in stage T % 4.  Tile DMAs are issued from the softmax
-  // segment (VALU-bound, so the memory instructions cost nothing there),
-  // never from the MFMA segment.  Group A issues its share of tile T during
-  // SM(T-2) (segment 2T-3) and waits for it at the end of iteration T-1
-  // (segment 2T-1); group B, half a step later, issues during SM(T-3)
-  // (segment 2T-4) and waits at the end of iteration T-2 (segment 2T-2).  So
-  // every share of tile T has landed before A's QK(T) in segment 2T, and the
-  // stage's previous tile T-4 was last read by B's M(T-3) in segment 2T-5.
-  const bool grp_b = wave >= kWaves / 2;
-  const int ahead = grp_b ? 3 : 2;  // tile issued during SM(t) is t + ahead
-  using T_ = std::true_type;
-  using F_ = std::false_type;
-  // One M segment + one SM segment.  kPv / kQk say whether PV(t-1) / QK(t)
-  // exist (every iteration but the first and the last has both), so that the
-  // steady-state M segment is a single block the scheduler can interleave.
-  int32_t page_next = 0;  // raw block-table entry of the next tile to load (aligned path)
-  auto iteration = [&](int t, auto st, auto has_pv, auto has_qk) __attribute__((always_inline)) {
-    constexpr int s = decltype(st)::value;
-    constexpr bool kPv = decltype(has_pv)::value;
-    constexpr bool kQk = decltype(has_qk)::value;
-    using KS = std::integral_constant<int, s>;
-    using VS = std::integral_constant<int, (s + kStages - 1) % kStages>;
-    if constexpr (kPv) pv(VS{});
-    if constexpr (kQk) qk(KS{});
-    if constexpr (kPv && kQk) {
-      // 16 PV MFMAs (2 transposing V reads each) then 16 QK MFMAs (1 K read
-      // each): every read is issued kAheadMfma MFMAs before the MFMA it feeds.
-      constexpr int A = kAheadMfma;
-      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2 * A, 0);
-#pragma unroll
-      for (int i = 1; i <= 32; ++i) {
-        const int next = i + A;  // MFMA whose operands are read now
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
-        if (next <= 16) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-        else if (next <= 32) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
-      }
-    }
-    wait_vm_lgkm0<15>();  // LDS reads of this segment retired (vmcnt untouched)
-    barrier();
-    const int ti = t + ahead;
-    const bool dma = ti < n_tiles;
-    const int dstage = grp_b ? (s + 3) % kStages : (s + 2) % kStages;
-    TileAddrs ta;
-    if (dma) ta = tile_addrs(ti * kTileN, page_next);
-    if constexpr (kAligned) page_next = page_raw((ti + 1) * kTileN);  // for the next iteration
-    // one DMA before each quarter of the softmax: a burst of them would
-    // stall on the address queue
-    auto between = [&](int u) __attribute__((always_inline)) {
-      if (dma) dma_issue(ta, u, dstage);
-    };
-    if constexpr (kQk) {
-      softmax(t, between);
-    } else {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) between(u);
-    }
-    // this wave's share of tile t + ahead - 1 has landed: at most the loads of
-    // tile t + ahead (issued above) may still be outstanding
-    if (ti < n_tiles) wait_vm_lgkm0<kDmaPerTile>();
-    else wait_vm_lgkm0<0>();
-    barrier();
-  };
-  using S0 = std::integral_constant<int, 0>;
-  using S1 = std::integral_constant<int, 1>;
-  using S2 = std::integral_constant<int, 2>;
-  using S3 = std::integral_constant<int, 3>;
-
-  // Prologue: A issues tiles 0 and 1, B tiles 0, 1 and 2.  Everyone waits for
-  // tile 0 before the first barrier; B also waits for tile 1 before its idle
-  // barrier (which ends segment 0, i.e. before A's M(1) in segment 2).
-  if (n_tiles > 0) issue_tile(0, 0);
-  if (n_tiles > 1) issue_tile(kTileN, 1);
-  if (grp_b && n_tiles > 2) issue_tile(2 * kTileN, 2);
-  // raw page id of the first tile the loop loads (tile `ahead`)
-  if (kAligned && n_tiles > 0) page_next = page_raw(ahead * kTileN);
-  const int issued = min(n_tiles, grp_b ? 3 : 2);
-  if (issued == 3) wait_vm_lgkm0<2 * kDmaPerTile>();
-  else if (issued == 2) wait_vm_lgkm0<kDmaPerTile>();
-  else wait_vm_lgkm0<0>();
-  __builtin_amdgcn_s_barrier();
-  if (grp_b) {
-    if (issued == 3) wait_vm_lgkm0<kDmaPerTile>();
-    else wait_vm_lgkm0<0>();
-    barrier();
-  }
-
-  // iterations t = 0 .. n_tiles: QK(0) alone, then PV(t-1) + QK(t), then
-  // PV(n_tiles-1) alone.  Tile t sits in stage t % 4.
-  if (n_tiles == 0) {
-    iteration(0, S0{}, F_{}, F_{});
-  } else {
-    iteration(0, S0{}, F_{}, T_{});
-    int t = 1;
-    for (; t + 4 <= n_tiles; t += 4) {
-      iteration(t, S1{}, T_{}, T_{});
-      iteration(t + 1, S2{}, T_{}, T_{});
-      iteration(t + 2, S3{}, T_{}, T_{});
-      iteration(t + 3, S0{}, T_{}, T_{});
-    }
-    if (t < n_tiles) iteration(t, S1{}, T_{}, T_{});
-    if (t + 1 < n_tiles) iteration(t + 1, S2{}, T_{}, T_{});
-    if (t + 2 < n_tiles) iteration(t + 2, S3{}, T_{}, T_{});
-    switch (n_tiles & 3) {
-      case 0: iteration(n_tiles, S0{}, T_{}, F_{}); break;
-      case 1: iteration(n_tiles, S1{}, T_{}, F_{}); break;
-      case 2: iteration(n_tiles, S2{}, T_{}, F_{}); break;
-      default: iteration(n_tiles, S3{}, T_{}, F_{}); break;
-    }
-  }
-  if (!grp_b) barrier();
-
-  // ---- epilogue: row n = (token rtok, head rhead); acc_o[dt][i] holds
-  // d = 32dt + 8(i/4) + 4h + i%4
-  const float l_run = sum_xor32((l_part[0] + l_part[1]) + (l_part[2] + l_part[3]));
-  if (row_ok) {
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-    uint16_t* orow = p.out + (int64_t)(q0 + rtok) * p.o_ts + (int64_t)(kvh * p.group + rhead) * p.o_hs + 4 * h;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        u32x2 w;
-        w[0] = pack_bf16x2(acc_o[dt][4 * i4] * inv, acc_o[dt][4 * i4 + 1] * inv);
-        w[1] = pack_bf16x2(acc_o[dt][4 * i4 + 2] * inv, acc_o[dt][4 * i4 + 3] * inv);
-        *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4) = w;
-      }
-  }
+  prefill_body<kSoftCap, kAligned>(p, blockIdx.x);
 }
 
 // Zero every output row the prefill kernel does not write: rows outside all
@@ -675,6 +108,7 @@ extern "C" int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_hea
   prm.pages_per_seq = pages_per_seq;
   prm.cu_q = cu_seqlens_q;
   prm.cu_k = cu_seqlens_k;
+  prm.kv_lens = nullptr;
   prm.positions = input_positions;
   prm.batch = batch;
   prm.num_tokens = num_tokens;

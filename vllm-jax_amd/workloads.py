@@ -94,6 +94,54 @@ class DecodeBatch:
         return 4 * self.head_dim * self.num_heads * int(np.sum(self.context_lens, dtype=np.int64))
 
 
+@dataclass
+class MixedBatch:
+    """One scheduler step, unpadded: the decode sequences of ``decode`` first
+    (one q row each), then the prefill sequences of ``prefill``."""
+    prefill: PrefillBatch
+    decode: DecodeBatch
+    block_tables: np.ndarray      # [B, P] int32, decode rows first
+    cu_seqlens_q: np.ndarray      # [B+1] int32
+    kv_lens: np.ndarray           # [B] int32
+    input_positions: np.ndarray   # [T] int32
+    slot_mapping: np.ndarray      # [T] int32
+
+    @property
+    def num_decodes(self) -> int:
+        return self.decode.batch
+
+    @property
+    def batch(self) -> int:
+        return len(self.kv_lens)
+
+    @property
+    def num_tokens(self) -> int:
+        return int(self.cu_seqlens_q[-1])
+
+    @property
+    def max_seqlen_q(self) -> int:
+        return int(self.prefill.q_lens.max()) if self.prefill.batch else 0
+
+    def flops(self) -> int:
+        return self.prefill.flops() + self.decode.flops()
+
+
+def make_mixed(pre: PrefillBatch, dec: DecodeBatch) -> MixedBatch:
+    """Concatenate a decode batch and a prefill batch over one pool."""
+    assert (pre.num_heads, pre.num_kv_heads, pre.page_size, pre.num_pages) == \
+        (dec.num_heads, dec.num_kv_heads, dec.page_size, dec.num_pages)
+    width = max(pre.block_tables.shape[1], dec.block_tables.shape[1])
+    bt = np.full((dec.batch + pre.batch, width), -1, np.int32)
+    bt[:dec.batch, :dec.block_tables.shape[1]] = dec.block_tables
+    bt[dec.batch:, :pre.block_tables.shape[1]] = pre.block_tables
+    q_lens = np.concatenate([np.ones(dec.batch, np.int64), pre.q_lens.astype(np.int64)])
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    kv = np.concatenate([dec.context_lens, np.diff(pre.cu_seqlens_k)]).astype(np.int32)
+    pos = np.concatenate([dec.input_positions, pre.input_positions[:pre.num_tokens]]).astype(np.int32)
+    slots = np.concatenate([dec.slot_mapping, pre.slot_mapping[:pre.num_tokens]]).astype(np.int32)
+    return MixedBatch(pre, dec, bt, cu, kv, pos, slots)
+
+
 def _bucket(v: int) -> int:
     return 1 if v <= 1 else 1 << (int(v) - 1).bit_length()
 
@@ -329,6 +377,24 @@ def materialize_decode(db: DecodeBatch, seed: int, device, kv_cache=None):
     return dict(kv_cache=kv_cache, q=q, k=k, v=v, block_tables=i32(db.block_tables),
                 context_lens=i32(db.context_lens), input_positions=i32(db.input_positions),
                 slot_mapping=i32(db.slot_mapping))
+
+
+def materialize_mixed(mb: MixedBatch, seed: int, device):
+    """Device tensors for a mixed step: random pool (the decode contexts),
+    q and new k/v for every row (decode rows first), int32 metadata."""
+    import torch
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    pre = mb.prefill
+    t = mb.num_tokens
+    kv_cache = _randn_bf16((2, pre.num_pages, pre.page_size, pre.num_kv_heads, pre.head_dim), gen, device)
+    q = _randn_bf16((t, pre.num_heads, pre.head_dim), gen, device)
+    k = _randn_bf16((t, pre.num_kv_heads, pre.head_dim), gen, device)
+    v = _randn_bf16((t, pre.num_kv_heads, pre.head_dim), gen, device)
+    i32 = lambda a: torch.as_tensor(np.ascontiguousarray(a), dtype=torch.int32, device=device)
+    return dict(kv_cache=kv_cache, q=q, k=k, v=v, block_tables=i32(mb.block_tables),
+                cu_seqlens_q=i32(mb.cu_seqlens_q), kv_lens=i32(mb.kv_lens),
+                input_positions=i32(mb.input_positions), slot_mapping=i32(mb.slot_mapping))
 
 
 def pool_pages_needed(lens, page_size=PAGE_SIZE) -> int:
