@@ -10,6 +10,10 @@ workload, inputs resident in HBM:
 * Qwen3-8B decode (256 sequences, ctx ~ U[512, 8192], 32 q / 8 kv heads,
   16384-page pool, seed 2): KV store of the new token + split-K decode.
   Reported under ``"decode"`` in GB/s of algorithmic HBM traffic.
+* The Qwen3-0.6B mixed scheduler step (96 decode sequences ctx ~ U[256,
+  4096] + 32 prefill sequences L ~ U[64, 2048], seed 1) as one unpadded
+  ``pa_mixed`` launch against the separate decode and prefill launches
+  (timed in its own loop): reported under ``"mixed"``.
 * The fused q/k RMSNorm + RoPE + KV store over the prefill workload's tokens
   (timed in its own loop after the step): reported under ``"qk_norm_rope"``
   in GB/s of algorithmic HBM traffic, (2 H + 4 Hkv) * 256 + 8 bytes a token.
@@ -85,7 +89,8 @@ def run_gpu(args):
 
     # ---------------- prefill: Qwen3-32B long context
     pb = wl.qwen3_32b_long_prefill(seed=4)
-    pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False) if args.only != "decode" else None
+    pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False) if args.only not in ("decode", "mixed") \
+        else None
     if pt is None:  # decode-only profiling run: keep the prefill half tiny
         pb = wl.make_prefill([64], num_heads=64, num_kv_heads=8, rng=np.random.default_rng(0))
         pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False)
@@ -102,7 +107,7 @@ def run_gpu(args):
                                     max_seqlen_bucket=pb.max_seqlen_bucket, out=out_p)
 
     # ---------------- decode: Qwen3-8B
-    db = wl.qwen3_8b_decode(seed=2) if args.only not in ("prefill", "rope") else \
+    db = wl.qwen3_8b_decode(seed=2) if args.only not in ("prefill", "rope", "mixed") else \
         wl.make_decode([64], num_heads=32, num_kv_heads=8, rng=np.random.default_rng(0))
     dt_ = wl.materialize_decode(db, seed=2, device=dev)
     kv_d = dt_["kv_cache"]
@@ -123,6 +128,7 @@ def run_gpu(args):
     run_p = args.only in (None, "prefill")
     run_d = args.only in (None, "decode")
     run_r = args.only in (None, "rope")
+    run_m = args.only in (None, "mixed")
     nop = lambda: None
     if not run_p:
         prefill_step = prefill_attn = nop
@@ -163,6 +169,7 @@ def run_gpu(args):
     d_gbs_kernel = rate(d_bytes, float(d_attn.mean()), 1e9)
 
     rope = run_rope(args, torch, pkg, pb, pt, kv_p) if run_r else None
+    mixed = run_mixed(args, torch, pkg, wl, dev) if run_m else None
 
     traffic = _load_traffic()
     res = {
@@ -228,7 +235,64 @@ def run_gpu(args):
     if rope is not None:
         rope["roofline"]["traffic"] = traffic.get("qk_norm_rope_store_kernel")
         res["qk_norm_rope"] = rope
+    if mixed is not None:
+        res["mixed"] = mixed
     return res, (pb, pt, db, dt_)
+
+
+def run_mixed(args, torch, pkg, wl, dev):
+    """Time the Qwen3-0.6B mixed step: one pa_mixed launch vs pa_decode + pa_prefill."""
+    pre, dec = wl.qwen3_06b_mixed(1)
+    mb = wl.make_mixed(pre, dec)
+    t = wl.materialize_mixed(mb, seed=1, device=dev)
+    kv = t["kv_cache"]
+    pkg.update_kv_cache(kv, t["slot_mapping"], t["k"], t["v"])
+    kp, vp = kv[0].permute(2, 0, 1, 3), kv[1].permute(2, 0, 1, 3)
+    nd, base = mb.num_decodes, int(mb.cu_seqlens_q[mb.num_decodes])
+    from vllm_jax_amd.kernels.decode_paged_attention import decode_workspace_bytes
+    ws = torch.empty(decode_workspace_bytes(nd, mb.prefill.num_heads, 128, mb.block_tables.shape[1],
+                                            mb.prefill.page_size), dtype=torch.uint8, device=dev)
+    out = torch.empty_like(t["q"])
+    qd = t["q"][:nd].contiguous()
+    od = torch.empty_like(qd)
+    op = torch.empty_like(t["q"][base:])
+    cup = t["cu_seqlens_q"][nd:] - base
+    cuk = torch.as_tensor(np.concatenate([[0], np.cumsum(mb.kv_lens[nd:])]).astype(np.int32), device=dev)
+    dscale = 1.0 / 11.3125
+
+    def one():
+        pkg.mixed_paged_attention(t["q"], kp, vp, t["block_tables"], t["cu_seqlens_q"], t["kv_lens"],
+                                  t["input_positions"], nd, max_seqlen_q=mb.max_seqlen_q, decode_scale=dscale,
+                                  out=out)
+
+    def two():
+        pkg.decode_paged_attention(qd, kp, vp, t["block_tables"][:nd], t["kv_lens"][:nd], scale=dscale,
+                                   workspace=ws, out=od)
+        pkg.prefill_paged_attention(t["q"][base:], kp, vp, t["block_tables"][nd:], cup, None,
+                                    t["input_positions"][base:], max_seqlen_bucket=mb.max_seqlen_q,
+                                    cu_seqlens_k=cuk, out=op)
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(max(args.steps, 10)):   # launches queue ahead of the host
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / max(args.steps, 10)
+
+    ms_one, ms_two = timed(one), timed(two)
+    flops, dbytes = pre.flops(), dec.hbm_bytes()
+    return {
+        "metric": "mixed step ms (one launch vs decode + prefill launches)",
+        "decode_seqs": int(nd), "prefill_seqs": int(pre.batch), "tokens": int(mb.num_tokens),
+        "prefill_gflop": round(flops / 1e9, 3), "decode_gb": round(dbytes / 1e9, 4),
+        "one_launch_ms": round(ms_one, 4), "two_launches_ms": round(ms_two, 4),
+        "speedup": round(ms_two / ms_one, 3) if ms_one > 0 else None,
+    }
 
 
 def run_rope(args, torch, pkg, pb, pt, kv):
@@ -343,7 +407,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU oracle work (total)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "rope", "copy"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "rope", "mixed", "copy"], default=None,
                     help="profiling aid: run one kernel family only (the JSON line then covers that part)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

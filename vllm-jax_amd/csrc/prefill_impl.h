@@ -177,14 +177,39 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, int bid) {
   const int rtok = tok0 + row / p.group;
   const int rhead = row % p.group;
   const bool row_ok = row < p.tile_tokens * p.group && rtok < lq_rows;
-  const int qpos = row_ok ? p.positions[q0 + rtok] : 0;
+  // Loads are unconditional from a clamped row (lq_rows >= 1 here): a load
+  // under a branch makes the compiler wait for it at the branch join.  A lane
+  // without a row computes on the clamped row's finite data; its column of S
+  // and O never mixes with other rows and is not stored.
+  const int ltok = min(rtok, lq_rows - 1);
+  const int qpos_ld = p.positions[q0 + ltok];
 
-  // ---- q tile position range -> kv tile range
+  // Q^T operand (B of S^T): k-step ks covers d = 16ks + 8h .. +8.  Issued
+  // before the position reduction below so that their latencies overlap.
+  bf16x8 qt_op[8];
+  {
+    const uint16_t* qrow = p.q + (int64_t)(q0 + ltok) * p.q_ts + (int64_t)(kvh * p.group + rhead) * p.q_hs + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qt_op[ks] = as_bf16x8(ld16(qrow + 16 * ks));
+  }
+  const int qpos = row_ok ? qpos_ld : 0;
+  // raw page ids of the first three kv tiles, read while the loads above fly
+  int32_t raw_pre[3] = {0, 0, 0};
+  if constexpr (kAligned) {
+    if (p.pages_per_seq > 0) {
+      const __attribute__((address_space(4))) int32_t* c =
+          (const __attribute__((address_space(4))) int32_t*)(p.block_tables + (int64_t)b * p.bt_stride);
+#pragma unroll
+      for (int i = 0; i < 3; ++i) raw_pre[i] = c[min(i * kTileN / p.page_size, p.pages_per_seq - 1)];
+    }
+  }
+
+  // ---- q tile position range -> kv tile range (lanes n and n + 32 hold the same row)
   {
     int mx = row_ok ? qpos : INT_MIN;
     int mn = row_ok ? qpos : INT_MAX;
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
+    for (int o = 16; o >= 1; o >>= 1) {
       mx = max(mx, __shfl_xor(mx, o));
       mn = min(mn, __shfl_xor(mn, o));
     }
@@ -194,15 +219,6 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, int bid) {
     }
   }
 
-  // Q^T operand (B of S^T): k-step ks covers d = 16ks + 8h .. +8.
-  bf16x8 qt_op[8];
-  {
-    const uint16_t* qrow = p.q + (int64_t)(q0 + (row_ok ? rtok : 0)) * p.q_ts +
-                           (int64_t)(kvh * p.group + rhead) * p.q_hs + 8 * h;
-#pragma unroll
-    for (int ks = 0; ks < 8; ++ks)
-      qt_op[ks] = as_bf16x8(row_ok ? ld16(qrow + 16 * ks) : u32x4{0, 0, 0, 0});
-  }
   // Retire every compiler-visible vector load here: the tile DMAs below are
   // invisible to the compiler's wait tracking, so nothing it issued may still
   // be in flight when they start (else it would drain them at the loop head).
@@ -298,10 +314,13 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, int bid) {
     const uint32_t base = (i & 1) ? v_lds0 : k_lds0;
     dma16(a.g[i], base + (uint32_t)(stage * kTileElems * 2 + (kBlk * wave + (i >> 1)) * 1024));
   };
-  auto issue_tile = [&](int j0, int stage) __attribute__((always_inline)) {
-    const TileAddrs a = tile_addrs(j0, kAligned ? page_raw(j0) : 0);
+  auto issue_tile_raw = [&](int j0, int32_t raw, int stage) __attribute__((always_inline)) {
+    const TileAddrs a = tile_addrs(j0, raw);
 #pragma unroll
     for (int i = 0; i < 2 * kBlk; ++i) dma_issue(a, i, stage);
+  };
+  auto issue_tile = [&](int j0, int stage) __attribute__((always_inline)) {
+    issue_tile_raw(j0, kAligned ? page_raw(j0) : 0, stage);
   };
   constexpr int kDmaPerTile = 2 * kBlk;  // vm instructions one wave issues per tile
 
@@ -526,9 +545,9 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, int bid) {
   // Prologue: A issues tiles 0 and 1, B tiles 0, 1 and 2.  Everyone waits for
   // tile 0 before the first barrier; B also waits for tile 1 before its idle
   // barrier (which ends segment 0, i.e. before A's M(1) in segment 2).
-  if (n_tiles > 0) issue_tile(0, 0);
-  if (n_tiles > 1) issue_tile(kTileN, 1);
-  if (grp_b && n_tiles > 2) issue_tile(2 * kTileN, 2);
+  if (n_tiles > 0) issue_tile_raw(0, raw_pre[0], 0);
+  if (n_tiles > 1) issue_tile_raw(kTileN, raw_pre[1], 1);
+  if (grp_b && n_tiles > 2) issue_tile_raw(2 * kTileN, raw_pre[2], 2);
   // raw page id of the first tile the loop loads (tile `ahead`)
   if (kAligned && n_tiles > 0) page_next = page_raw(ahead * kTileN);
   const int issued = min(n_tiles, grp_b ? 3 : 2);
@@ -568,20 +587,31 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, int bid) {
   if (!grp_b) barrier();
 
   // ---- epilogue: row n = (token rtok, head rhead); acc_o[dt][i] holds
-  // d = 32dt + 8(i/4) + 4h + i%4
+  // d = 32dt + 8(i/4) + 4h + i%4.  One permlane32 swap per dword pair gives
+  // lane (n, 0) d = 32dt + 16pr + 0..7 and lane (n, 1) d = 32dt + 16pr + 8..15,
+  // so every lane stores whole 16-byte pieces.  The swaps run on all lanes
+  // (lanes n and n + 32 share a row, hence row_ok).
   const float l_run = sum_xor32((l_part[0] + l_part[1]) + (l_part[2] + l_part[3]));
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+  u32x4 ow[4][2];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int pr = 0; pr < 2; ++pr) {
+      const f32x16& a = acc_o[dt];
+      const int i = 8 * pr;
+      const uint32_t x0 = pack_bf16x2(a[i] * inv, a[i + 1] * inv), x1 = pack_bf16x2(a[i + 2] * inv, a[i + 3] * inv);
+      const uint32_t y0 = pack_bf16x2(a[i + 4] * inv, a[i + 5] * inv), y1 = pack_bf16x2(a[i + 6] * inv, a[i + 7] * inv);
+      const auto s0 = __builtin_amdgcn_permlane32_swap(x0, y0, false, false);
+      const auto s1 = __builtin_amdgcn_permlane32_swap(x1, y1, false, false);
+      ow[dt][pr] = u32x4{s0[0], s1[0], s0[1], s1[1]};
+    }
   if (row_ok) {
-    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-    uint16_t* orow = p.out + (int64_t)(q0 + rtok) * p.o_ts + (int64_t)(kvh * p.group + rhead) * p.o_hs + 4 * h;
+    uint16_t* orow = p.out + (int64_t)(q0 + rtok) * p.o_ts + (int64_t)(kvh * p.group + rhead) * p.o_hs + 8 * h;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        u32x2 w;
-        w[0] = pack_bf16x2(acc_o[dt][4 * i4] * inv, acc_o[dt][4 * i4 + 1] * inv);
-        w[1] = pack_bf16x2(acc_o[dt][4 * i4 + 2] * inv, acc_o[dt][4 * i4 + 3] * inv);
-        *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i4) = w;
-      }
+      for (int pr = 0; pr < 2; ++pr) st16(orow + 32 * dt + 16 * pr, ow[dt][pr]);
   }
 }
 
