@@ -10,7 +10,10 @@ Public surface (mirrors simpissa/vllm-jax):
 * ``qk_norm_rope_store`` / ``qwen3_attention_core`` -- the q/k RMSNorm +
   RoPE + KV store step before attention, fused into one kernel;
 * ``MixedAttentionMetadata`` / ``mixed_paged_attention`` -- a step's decode
-  and prefill sequences in one unpadded launch.
+  and prefill sequences in one unpadded launch;
+* ``KVCacheManager`` / ``copy_blocks`` -- the block manager of
+  vllm/src/kv_cache_manager.py on a native allocator, with optional prefix
+  caching and fork / copy-on-write.
 
 All device work runs in ``libpaged_attention.so`` (hand-written HIP for
 gfx950, built by ``build.py``) through a C ABI; there is no CPU fallback.
@@ -22,9 +25,9 @@ module name ``vllm_jax_amd``::
         submodule_search_locations=["<repo>/vllm-jax_amd"])
 """
 from .attention import (DecodeAttentionMetadata, MixedAttentionMetadata, PrefillAttentionMetadata,  # noqa: F401
-                        attention,
-                        attention_stored, gather_kv, qk_norm_rope_store, qwen3_attention_core,
+                        attention, attention_stored, gather_kv, qk_norm_rope_store, qwen3_attention_core,
                         update_kv_cache)
 from .kernels.decode_paged_attention import decode_paged_attention  # noqa: F401
 from .kernels.mixed_paged_attention import mixed_paged_attention  # noqa: F401
 from .kernels.prefill_paged_attention import prefill_paged_attention  # noqa: F401
+from .kv_cache_manager import Block, KVCacheManager, copy_blocks  # noqa: F401

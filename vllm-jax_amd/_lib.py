@@ -73,6 +73,25 @@ SIGNATURES = {
         c_i64, c_i64, c_i64,           # page/slot/head strides
         c_vp,                          # stream
     ]),
+    # block manager (include/block_manager.h)
+    "pa_bm_create": (c_vp, [c_i32, c_i32, c_i32]),
+    "pa_bm_destroy": (None, [c_vp]),
+    "pa_bm_num_free_blocks": (c_i32, [c_vp]),
+    "pa_bm_can_allocate": (ctypes.c_int, [c_vp, c_i64, c_vp, c_i32, c_i32]),
+    "pa_bm_allocate": (ctypes.c_int, [c_vp, c_i64, c_vp, c_i32, c_i32]),
+    "pa_bm_num_cached_tokens": (c_i32, [c_vp, c_i64]),
+    "pa_bm_block_table": (c_i32, [c_vp, c_i64, c_vp, c_i32]),
+    "pa_bm_fork": (ctypes.c_int, [c_vp, c_i64, c_i64]),
+    "pa_bm_deallocate": (ctypes.c_int, [c_vp, c_i64]),
+    "pa_bm_ref_count": (c_i32, [c_vp, c_i32]),
+    "pa_bm_take_copies": (c_i32, [c_vp, c_vp, c_vp, c_i32]),
+    "pa_copy_blocks": (ctypes.c_int, [
+        c_vp, c_vp, c_i32, c_i32,      # caches, num_pages, page_size
+        c_i64, c_i64, c_i64,           # page/slot/head strides
+        c_i32, c_i32,                  # num_kv_heads, head_dim
+        c_vp, c_vp, c_i32,             # src, dst, num_copies
+        c_vp,                          # stream
+    ]),
     "pa_mixed_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
     "pa_mixed": (ctypes.c_int, [
         c_vp, c_i64, c_i64,            # q

@@ -18,7 +18,8 @@ LIB_NAME = "libpaged_attention.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = "gfx950"
 
-SOURCES = ["pa_errors.cpp", "kv_store.hip", "decode.hip", "prefill.hip", "qk_norm_rope.hip", "mixed.hip"]
+SOURCES = ["pa_errors.cpp", "block_manager.cpp", "kv_store.hip", "decode.hip", "prefill.hip", "qk_norm_rope.hip",
+           "mixed.hip"]
 
 # Packed-FP32 VALU forms are disabled for every device compile: the build
 # relies on scalar/float2 code only.  Without NaN semantics, fmaxf lowers to a

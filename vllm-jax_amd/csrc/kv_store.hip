@@ -82,6 +82,26 @@ gather_kv_kernel(const uint16_t* __restrict__ cache, int32_t num_pages, int32_t 
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Page copies for copy-on-write: page dst[i] <- page src[i] for K and V.
+// blockIdx.y = pair, x covers the page's page_size * Hkv * d/8 chunks.
+__global__ void __launch_bounds__(256)
+copy_blocks_kernel(uint16_t* __restrict__ k_cache, uint16_t* __restrict__ v_cache, int32_t num_pages,
+                   int32_t page_size, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                   int32_t chunks_per_head, int32_t chunks_per_slot,
+                   const int32_t* __restrict__ src, const int32_t* __restrict__ dst) {
+  const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= (int64_t)page_size * chunks_per_slot) return;
+  const int32_t sp = src[blockIdx.y], dp = dst[blockIdx.y];
+  if (sp < 0 || sp >= num_pages || dp < 0 || dp >= num_pages) return;
+  const int32_t slot = (int32_t)(c / chunks_per_slot);
+  const int32_t r = (int32_t)(c - (int64_t)slot * chunks_per_slot);
+  const int32_t h = r / chunks_per_head;
+  const int32_t e = (r - h * chunks_per_head) * 8;
+  const int64_t off = (int64_t)slot * slot_stride + h * head_stride + e;
+  st16(k_cache + dp * page_stride + off, ld16(k_cache + sp * page_stride + off));
+  st16(v_cache + dp * page_stride + off, ld16(v_cache + sp * page_stride + off));
+}
+
 }  // namespace pa
 
 using namespace pa;
@@ -144,4 +164,28 @@ extern "C" int pa_gather_kv(const uint16_t* cache, int32_t num_pages, int32_t pa
       cache, num_pages, page_size, page_stride, slot_stride, head_stride, block_tables, bt_stride,
       pages_per_seq, lengths, batch, head_dim, ept, out);
   return launch_status("pa_gather_kv");
+}
+
+extern "C" int pa_copy_blocks(uint16_t* k_cache, uint16_t* v_cache, int32_t num_pages, int32_t page_size,
+                              int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                              int32_t num_kv_heads, int32_t head_dim,
+                              const int32_t* src_blocks, const int32_t* dst_blocks, int32_t num_copies, void* stream) {
+  if (num_pages <= 0 || page_size <= 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 8 || num_copies < 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "pa_copy_blocks: bad sizes (num_pages=%d, page_size=%d, num_kv_heads=%d, head_dim=%d, n=%d)",
+                num_pages, page_size, num_kv_heads, head_dim, num_copies);
+  if (num_copies == 0) return PA_OK;
+  if (num_copies > 65535) return fail(PA_ERR_UNSUPPORTED, "pa_copy_blocks: at most 65535 copies per call");
+  if (!k_cache || !v_cache || !src_blocks || !dst_blocks)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_copy_blocks: null pointer");
+  if ((((uintptr_t)k_cache | (uintptr_t)v_cache) & 15u) || (page_stride | slot_stride | head_stride) % 8)
+    return fail(PA_ERR_UNSUPPORTED, "pa_copy_blocks: pools must be 16-byte aligned with strides multiple of 8");
+  const int32_t cph = head_dim / 8;
+  const int32_t cps = cph * num_kv_heads;
+  const int64_t chunks = (int64_t)page_size * cps;
+  const dim3 grid((unsigned)((chunks + 255) / 256), (unsigned)num_copies);
+  copy_blocks_kernel<<<grid, dim3(256), 0, (hipStream_t)stream>>>(k_cache, v_cache, num_pages, page_size, page_stride,
+                                                                  slot_stride, head_stride, cph, cps, src_blocks,
+                                                                  dst_blocks);
+  return launch_status("pa_copy_blocks");
 }
