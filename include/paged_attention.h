@@ -165,6 +165,48 @@ int pa_qk_norm_rope_store(const uint16_t* q, int64_t q_tok_stride, int64_t q_hea
                           void* stream);
 
 /*
+ * Quantising KV store for float8 pages: for every token t with a slot in the
+ * pool and every kv head h, the row x = k[t, h] (bf16, d = 128) is stored as
+ * e4m3fn codes e4m3(x * (448 / amax)) (round to nearest even) with scale
+ * amax / 448 (amax = max |x|; an all-zero row stores scale 1), and likewise
+ * v.  Code pools: (page, slot, head) byte strides as in pa_kv_store; scale
+ * pools: float (page, slot, head) strides, e.g. the [Hkv, NB, BS] layout of
+ * k_scales_pages (decode_paged_attention.py:206-217).  The reference reads
+ * quantised pages but has no writer; this quantiser is the library's own.
+ */
+int pa_kv_store_fp8(const uint16_t* k, int64_t k_tok_stride, int64_t k_head_stride,
+                    const uint16_t* v, int64_t v_tok_stride, int64_t v_head_stride,
+                    const int32_t* slot_mapping, int32_t num_tokens,
+                    int32_t num_kv_heads, int32_t head_dim,
+                    uint8_t* k_cache, uint8_t* v_cache, float* k_scales, float* v_scales,
+                    int32_t num_pages, int32_t page_size,
+                    int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                    int64_t scale_page_stride, int64_t scale_slot_stride, int64_t scale_head_stride,
+                    void* stream);
+
+/*
+ * pa_decode over float8 e4m3fn pages with per-token scales: the logit of
+ * token j is (q . bf16(k_j)) * k_scales[j] * scale, and P is multiplied by
+ * v_scales[j] before PV (decode_paged_attention.py:72-81,108-115, the
+ * k_scales_pages / v_scales_pages path of :300-397).  Code strides are in
+ * bytes; scales are addressed page * scale_page_stride + head *
+ * scale_head_stride + slot (slot stride 1; both strides multiples of 4).
+ * page_size must be a multiple of 16.  Same workspace as pa_decode.
+ */
+int pa_decode_fp8(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
+                  const uint8_t* k_cache, const uint8_t* v_cache,
+                  const float* k_scales, const float* v_scales,
+                  int32_t num_pages, int32_t page_size,
+                  int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                  int64_t scale_page_stride, int64_t scale_head_stride,
+                  const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                  const int32_t* lengths, int32_t batch,
+                  int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                  float scale, float soft_cap,
+                  uint16_t* out, int64_t out_batch_stride, int64_t out_head_stride,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Workspace bytes pa_mixed needs (0 when every decode sequence fits one
  * 4096-token chunk, i.e. pages_per_seq * page_size <= the chunk).
  */

@@ -141,7 +141,7 @@ def decode_k_splits(pages_per_sequence: int) -> int:
 
 
 def _split_attention_rows(qs, k_ctx, v_ctx, valid, *, k_splits, block_k,
-                          page_size, used_tokens, soft_cap, mask_value):
+                          page_size, used_tokens, soft_cap, mask_value, k_scale=None, v_scale=None):
     """One q-row block against one kv head's context, reference algebra.
 
     Restates the kernel body shared by prefill (prefill...:62-150) and decode
@@ -155,6 +155,10 @@ def _split_attention_rows(qs, k_ctx, v_ctx, valid, *, k_splits, block_k,
     qs:    [R, d] f32 (already scaled, bf16-valued)
     k_ctx: [Pmax*BS, d] f32 context in block-table order
     valid: [R, Pmax*BS] bool mask (length, causal, row-in-range)
+    k_scale / v_scale: optional [Pmax*BS] f32 per-token scales of quantized
+    pages (decode...:72-81,108-115; prefill...:84-92,120-123): logits are
+    multiplied by k_scale before the soft cap, and PV uses the float32
+    ``P * v_scale`` against float32 V (no bf16 rounding of P).
     Returns (o_parts bf16-valued f32 [S,R,d], l [S,R], m [S,R]).
     """
     r, d = qs.shape
@@ -168,11 +172,11 @@ def _split_attention_rows(qs, k_ctx, v_ctx, valid, *, k_splits, block_k,
     with np.errstate(over="ignore", invalid="ignore"):
         return _split_loop(qs, k_ctx, v_ctx, valid, o_parts, l_parts, m_parts, k_splits=k_splits,
                            ppp=ppp, used_pages=used_pages, block_k=block_k, page_size=page_size,
-                           soft_cap=soft_cap, mask_value=mask_value)
+                           soft_cap=soft_cap, mask_value=mask_value, k_scale=k_scale, v_scale=v_scale)
 
 
 def _split_loop(qs, k_ctx, v_ctx, valid, o_parts, l_parts, m_parts, *, k_splits, ppp, used_pages,
-                block_k, page_size, soft_cap, mask_value):
+                block_k, page_size, soft_cap, mask_value, k_scale=None, v_scale=None):
     r, d = qs.shape
     total = k_ctx.shape[0]
     for s in range(k_splits):
@@ -195,6 +199,10 @@ def _split_loop(qs, k_ctx, v_ctx, valid, o_parts, l_parts, m_parts, *, k_splits,
             kb[: hi - t0] = k_ctx[t0:hi]
             vb[: hi - t0] = v_ctx[t0:hi]
             logits = qs @ kb.T
+            if k_scale is not None:
+                ksb = np.zeros(block_k, np.float32)
+                ksb[: hi - t0] = k_scale[t0:hi]
+                logits = (logits * ksb[None, :]).astype(np.float32)
             if soft_cap is not None:
                 logits = (np.tanh(logits / np.float32(soft_cap)) * np.float32(soft_cap)).astype(np.float32)
             mask = np.zeros((r, block_k), bool)
@@ -205,7 +213,12 @@ def _split_loop(qs, k_ctx, v_ctx, valid, o_parts, l_parts, m_parts, *, k_splits,
             corr = np.exp2((m_i - m_next) * np.float32(LOG2E)).astype(np.float32)
             s_curr = np.exp2((logits - m_next[:, None]) * np.float32(LOG2E)).astype(np.float32)
             l_i = (corr * l_i + s_curr.sum(axis=-1, dtype=np.float32)).astype(np.float32)
-            o = corr[:, None] * o + round_bf16(s_curr) @ vb
+            if v_scale is not None:
+                vsb = np.zeros(block_k, np.float32)
+                vsb[: hi - t0] = v_scale[t0:hi]
+                o = corr[:, None] * o + (s_curr * vsb[None, :]).astype(np.float32) @ vb
+            else:
+                o = corr[:, None] * o + round_bf16(s_curr) @ vb
             m_i = m_next
         o_parts[s] = round_bf16(o)
         l_parts[s] = l_i
@@ -321,7 +334,7 @@ def prefill_attention(q, k_pages, v_pages, block_tables, cu_seqlens,
 # ----------------------------------------------------------------------------
 def decode_attention(q, k_pages, v_pages, block_tables, lengths, *,
                      k_splits=None, pages_per_compute_block=8, soft_cap=None,
-                     mask_value=DEFAULT_MASK_VALUE, seqs=None):
+                     mask_value=DEFAULT_MASK_VALUE, seqs=None, k_scales_pages=None, v_scales_pages=None):
     """Split-K paged GQA decode, restating the reference kernel.
 
     q ``[B, H, d]`` is used as given -- the reference kernel applies no scale;
@@ -332,11 +345,19 @@ def decode_attention(q, k_pages, v_pages, block_tables, lengths, *,
     ``min(ppp, 8)`` and must divide the partition (decode...:179-184).
 
     ``seqs`` (optional) restricts the computation to those sequences.
+    Quantized pages (decode...:158-159,206-217): ``k_pages`` / ``v_pages``
+    hold float8 e4m3fn codes (uint8) and ``k_scales_pages`` /
+    ``v_scales_pages`` ``[Hkv, NB, BS]`` float32 per-token scales; K is cast to
+    bf16 exactly (decode...:72-74).
     Returns bf16 bit patterns ``[B, H, d]``.
     """
     qf = round_bf16(_as_f32(q))
+    quant = k_scales_pages is not None
     kp = np.asarray(k_pages)
     vp = np.asarray(v_pages)
+    if quant:
+        ksp = np.asarray(k_scales_pages, np.float32)
+        vsp = np.asarray(v_scales_pages, np.float32)
     b_count, h, d = qf.shape
     hkv, nb, bs, _ = kp.shape
     g = h // hkv
@@ -360,14 +381,21 @@ def decode_attention(q, k_pages, v_pages, block_tables, lengths, *,
         for kh in range(hkv):
             if ln <= 0:
                 continue
-            k_ctx = _as_f32(kp[kh][safe[b]].reshape(p * bs, d))
-            v_ctx = _as_f32(vp[kh][safe[b]].reshape(p * bs, d))
+            if quant:
+                k_ctx = fp8_e4m3_decode(kp[kh][safe[b]].reshape(p * bs, d))
+                v_ctx = fp8_e4m3_decode(vp[kh][safe[b]].reshape(p * bs, d))
+                k_sc = ksp[kh][safe[b]].reshape(p * bs)
+                v_sc = vsp[kh][safe[b]].reshape(p * bs)
+            else:
+                k_ctx = _as_f32(kp[kh][safe[b]].reshape(p * bs, d))
+                v_ctx = _as_f32(vp[kh][safe[b]].reshape(p * bs, d))
+                k_sc = v_sc = None
             qs = qf[b, kh * g:(kh + 1) * g]
             vmask = np.repeat(valid, g, axis=0)
             o_p, l_p, m_p = _split_attention_rows(
                 qs, k_ctx, v_ctx, vmask, k_splits=ks, block_k=block_k,
                 page_size=bs, used_tokens=ln, soft_cap=soft_cap,
-                mask_value=mask_value)
+                mask_value=mask_value, k_scale=k_sc, v_scale=v_sc)
             out[b, kh * g:(kh + 1) * g] = _merge_splits(o_p, l_p, m_p)
     return f32_to_bf16(out)
 
@@ -578,3 +606,80 @@ def mixed_attention(q, k_pages, v_pages, block_tables, cu_seqlens_q, kv_lens, in
         sel = slice(base, base + int(cu_p[-1]))
         out[sel] = tail[:int(cu_p[-1])]
     return out
+
+
+# ----------------------------------------------------------------------------
+# f4: float8 e4m3fn KV pages with per-token scales
+# ----------------------------------------------------------------------------
+def _e4m3_table() -> np.ndarray:
+    """Values of the 256 OCP float8 e4m3fn codes (1 sign, 4 exponent bits with
+    bias 7, 3 mantissa bits; no infinities; 0x7f / 0xff are NaN)."""
+    c = np.arange(256)
+    sign = np.where(c & 0x80, -1.0, 1.0)
+    e = (c >> 3) & 0xF
+    m = c & 0x7
+    mag = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * 2.0 ** (e - 7.0))
+    v = sign * mag
+    v[(c & 0x7F) == 0x7F] = np.nan
+    return v.astype(np.float32)
+
+
+_E4M3 = _e4m3_table()
+E4M3_MAX = 448.0
+
+
+def fp8_e4m3_decode(codes) -> np.ndarray:
+    """uint8 e4m3fn codes -> float32 values (exact)."""
+    return _E4M3[np.asarray(codes, dtype=np.uint8)]
+
+
+def fp8_e4m3_encode(x) -> np.ndarray:
+    """float32 -> e4m3fn codes, round to nearest, ties to the even code,
+    negative values keeping the sign bit (so -0 for a negative underflow);
+    magnitudes above 448 saturate to 448 (the quantizer below never
+    produces them)."""
+    x = np.asarray(x, dtype=np.float32)
+    pos = _E4M3[:0x7F].astype(np.float64)          # codes 0..126, increasing
+    a = np.minimum(np.abs(x).astype(np.float64), E4M3_MAX)
+    hi = np.clip(np.searchsorted(pos, a, side="left"), 0, 126)
+    lo = np.clip(hi - 1, 0, 126)
+    dlo, dhi = a - pos[lo], pos[hi] - a
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & (hi % 2 == 0))
+    code = np.where(pick_hi, hi, lo).astype(np.uint8)
+    return np.where(np.signbit(x), code | 0x80, code).astype(np.uint8)   # -0 stays -0
+
+
+def quantize_fp8_rows(x):
+    """Per-row float8 quantisation of bf16 rows ``[..., d]`` (bit patterns):
+    ``amax = max |x|``, stored scale ``s = amax / 448`` and codes
+    ``e4m3(x * (448 / amax))``, both divisions in float32; an all-zero row
+    stores scale 1 and zero codes.  Returns (codes uint8 [..., d], scales
+    float32 [...]).  This is the library's own quantiser (the reference
+    reads quantized pages but has no writer)."""
+    xf = _as_f32(x)
+    amax = np.abs(xf).max(axis=-1)
+    nz = amax > 0
+    safe = np.where(nz, amax, np.float32(1.0)).astype(np.float32)
+    inv = np.where(nz, np.float32(E4M3_MAX) / safe, np.float32(1.0)).astype(np.float32)
+    scale = np.where(nz, safe / np.float32(E4M3_MAX), np.float32(1.0)).astype(np.float32)
+    codes = fp8_e4m3_encode((xf * inv[..., None]).astype(np.float32))
+    return codes, scale
+
+
+def kv_store_fp8(k_codes, v_codes, k_scales, v_scales, k, v, slot_mapping):
+    """Quantised KV store: the rows of token t go to flat slot
+    ``slot_mapping[t]`` (skipped outside the pool, as kv_store above).
+    Pools: codes ``[NB, BS, Hkv, d]`` uint8, scales ``[Hkv, NB, BS]`` float32
+    (the layout of k_scales_pages, decode...:206-217)."""
+    kc, vc = np.array(k_codes, copy=True), np.array(v_codes, copy=True)
+    ks, vs = np.array(k_scales, copy=True), np.array(v_scales, copy=True)
+    nb, bs, hkv, d = kc.shape
+    kq, kscale = quantize_fp8_rows(k)
+    vq, vscale = quantize_fp8_rows(v)
+    for t, slot in enumerate(np.asarray(slot_mapping, dtype=np.int64)):
+        if slot < 0 or slot >= nb * bs:
+            continue
+        pg, off = divmod(int(slot), bs)
+        kc[pg, off], vc[pg, off] = kq[t], vq[t]
+        ks[:, pg, off], vs[:, pg, off] = kscale[t], vscale[t]
+    return kc, vc, ks, vs

@@ -1,0 +1,128 @@
+"""Float8 e4m3fn KV pages on gfx950: the quantising store (bit-exact codes
+and scales) and the quantized decode (max-abs 2e-2 against the oracle over
+the same codes and scales, as for bf16 pages)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import vllm_jax_amd.workloads as wl
+from conftest import from_u16, u16
+from oracle import paged_attention_oracle as ora
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _bf16(rng, shape, scale=0.5):
+    return ora.f32_to_bf16(rng.standard_normal(shape).astype(np.float32) * scale)
+
+
+def _u8(t):
+    import torch
+    return t.detach().cpu().contiguous().view(torch.uint8).numpy()
+
+
+@pytest.mark.parametrize("nb,bs,hkv,t,seed", [(16, 256, 8, 700, 0), (40, 16, 2, 300, 1), (4, 32, 4, 1, 2)])
+def test_kv_store_fp8_bit_exact(pkg, dev, nb, bs, hkv, t, seed):
+    import torch
+    rng = np.random.default_rng(seed)
+    k = _bf16(rng, (t, hkv, 128), 2.0)
+    v = _bf16(rng, (t, hkv, 128), 0.1)
+    if t > 3:
+        k[3, 0] = 0                                   # an all-zero row: scale 1, zero codes
+    slots = rng.permutation(nb * bs)[:t].astype(np.int32)
+    if t > 9:
+        slots[::9] = -1
+    codes0 = rng.integers(0, 256, (2, nb, bs, hkv, 128)).astype(np.uint8)
+    scales0 = rng.standard_normal((2, hkv, nb, bs)).astype(np.float32)
+    codes = torch.from_numpy(codes0).to(dev).view(torch.float8_e4m3fn)
+    scales = torch.from_numpy(scales0).to(dev)
+    pkg.update_kv_cache_fp8(codes, scales, torch.as_tensor(slots, device=dev), from_u16(k, dev), from_u16(v, dev))
+    torch.cuda.synchronize()
+    kc, vc, ks, vs = ora.kv_store_fp8(codes0[0], codes0[1], scales0[0], scales0[1], k, v, slots)
+    assert np.array_equal(_u8(codes[0]), kc) and np.array_equal(_u8(codes[1]), vc)
+    assert np.array_equal(scales[0].cpu().numpy(), ks) and np.array_equal(scales[1].cpu().numpy(), vs)
+
+
+def _quantized_pool(rng, nb, bs, hkv):
+    # 0.5 * N(0, 1) as in the workloads, the scale the 2e-2 bound is stated for
+    kf, vf = _bf16(rng, (nb, bs, hkv, 128)), _bf16(rng, (nb, bs, hkv, 128))
+    kq, ks = ora.quantize_fp8_rows(kf)
+    vq, vs = ora.quantize_fp8_rows(vf)
+    # scales of the reference layout [Hkv, NB, BS]
+    return kq, vq, np.ascontiguousarray(ks.transpose(2, 0, 1)), np.ascontiguousarray(vs.transpose(2, 0, 1))
+
+
+def _run_fp8(pkg, dev, q, kq, vq, ks, vs, bt, lens, scale=1.0, soft_cap=None):
+    import torch
+    kd = torch.from_numpy(kq).to(dev).view(torch.float8_e4m3fn)
+    vd = torch.from_numpy(vq).to(dev).view(torch.float8_e4m3fn)
+    out = pkg.decode_paged_attention(from_u16(q, dev), kd.permute(2, 0, 1, 3), vd.permute(2, 0, 1, 3),
+                                     torch.as_tensor(bt, device=dev), torch.as_tensor(lens, device=dev),
+                                     k_scales_pages=torch.from_numpy(ks).to(dev),
+                                     v_scales_pages=torch.from_numpy(vs).to(dev),
+                                     scale=scale, attn_logits_soft_cap=soft_cap)
+    torch.cuda.synchronize()
+    return u16(out)
+
+
+@pytest.mark.parametrize("lens,h,hkv,bs,cap", [
+    ([1, 15, 16, 17, 300, 0], 8, 2, 16, None),       # small pages, length 0 and 1
+    ([1000, 2049, 64], 32, 8, 256, None),            # Qwen3-8B heads, two chunks
+    ([5, 40, 1500, 2100], 16, 1, 32, None),          # G = 16
+    ([700, 33], 8, 8, 64, 30.0),                     # MHA, soft cap
+])
+def test_decode_fp8_matches_oracle(pkg, dev, lens, h, hkv, bs, cap):
+    rng = np.random.default_rng(sum(lens) + h)
+    pages = [(n + bs - 1) // bs for n in lens]
+    nb = sum(pages) + 2
+    width = 1 << (max(1, max(pages)) - 1).bit_length()
+    kq, vq, ks, vs = _quantized_pool(rng, nb, bs, hkv)
+    perm = rng.permutation(nb)
+    bt = np.full((len(lens), width), -1, np.int32)
+    c = 0
+    for b, p in enumerate(pages):
+        bt[b, :p] = perm[c:c + p]
+        c += p
+    q = _bf16(rng, (len(lens), h, 128))
+    got = _run_fp8(pkg, dev, q, kq, vq, ks, vs, bt, np.asarray(lens, np.int32), soft_cap=cap)
+    want = ora.decode_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, np.asarray(lens),
+                                soft_cap=cap, k_scales_pages=ks, v_scales_pages=vs)
+    err = np.abs(ora.bf16_to_f32(got) - ora.bf16_to_f32(want)).max()
+    print(f"fp8 decode max-abs err {err:.3e}")
+    assert err <= TOL
+    assert not got[np.asarray(lens) == 0].any()
+
+
+def test_decode_fp8_qwen3_8b_full_pool(pkg, dev):
+    """The Qwen3-8B decode workload with its whole pool quantised on the
+    device; sampled sequences against the oracle over the same codes."""
+    import torch
+    db = wl.qwen3_8b_decode(seed=2)
+    t = wl.materialize_decode(db, seed=2, device=dev)
+    nb, bs, hkv = db.num_pages, db.page_size, db.num_kv_heads
+    codes = torch.empty((2, nb, bs, hkv, 128), dtype=torch.float8_e4m3fn, device=dev)
+    scales = torch.empty((2, hkv, nb, bs), dtype=torch.float32, device=dev)
+    kv = t["kv_cache"]
+    slots = torch.arange(nb * bs, dtype=torch.int32, device=dev)
+    pkg.update_kv_cache_fp8(codes, scales, slots, kv[0].reshape(-1, hkv, 128), kv[1].reshape(-1, hkv, 128))
+    out = pkg.decode_paged_attention(t["q"], codes[0].permute(2, 0, 1, 3), codes[1].permute(2, 0, 1, 3),
+                                     t["block_tables"], t["context_lens"], k_scales_pages=scales[0],
+                                     v_scales_pages=scales[1], scale=1 / 11.3125)
+    torch.cuda.synchronize()
+    got = u16(out)
+    seqs = [0, int(np.argmax(db.context_lens)), int(np.argmin(db.context_lens)), db.batch - 1]
+    used = sorted(set(int(x) for x in db.block_tables[seqs].ravel() if x >= 0))
+    remap = {blk: i for i, blk in enumerate(used)}
+    bt = np.array([[remap.get(int(x), 0) if x >= 0 else -1 for x in db.block_tables[s]] for s in seqs], np.int32)
+    idx = torch.as_tensor(used, dtype=torch.long, device=dev)
+    kq, vq = _u8(codes[0][idx]), _u8(codes[1][idx])
+    ks = scales[0][:, idx].cpu().numpy()
+    vs = scales[1][:, idx].cpu().numpy()
+    qs = ora.f32_to_bf16(ora.round_bf16(ora.bf16_to_f32(u16(t["q"][seqs])) / np.float32(11.3125)))
+    want = ora.decode_attention(qs, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, db.context_lens[seqs],
+                                k_scales_pages=ks, v_scales_pages=vs)
+    err = np.abs(ora.bf16_to_f32(got[seqs]) - ora.bf16_to_f32(want)).max()
+    print(f"fp8 Qwen3-8B decode max-abs err {err:.3e}")
+    assert err <= TOL

@@ -73,8 +73,14 @@ def test_decode_shape_errors_match_reference():
         PKG.decode_paged_attention(*a[:4], a[4].long())
     with pytest.raises(ValueError, match="block_h must divisible by 16"):
         PKG.decode_paged_attention(*a, block_h=24)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="must be given together"):
         PKG.decode_paged_attention(*a, k_scales_pages=torch.zeros(1))
+    hkv, nb, bs = a[1].shape[:3]
+    sc = torch.ones(hkv, nb, bs)
+    with pytest.raises(ValueError, match="float8_e4m3fn"):        # bf16 pages with scales
+        PKG.decode_paged_attention(*a, k_scales_pages=sc, v_scales_pages=sc)
+    with pytest.raises(ValueError, match="k_scales_pages must have shape"):
+        PKG.decode_paged_attention(*a, k_scales_pages=sc[:, :1], v_scales_pages=sc)
 
 
 def test_decode_refuses_host_tensors():

@@ -385,3 +385,71 @@ def test_mixed_decode_row_equals_prefill_last_row():
     kp, vp = kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3)
     both = ora.bf16_to_f32(ora.mixed_attention(q, kp, vp, bt, cu, kv, pos, 1))
     assert np.abs(both[0] - both[1]).max() <= 2e-2 * max(1.0, np.abs(both).max())
+
+
+# ---------------------------------------------------------------------------
+# float8 e4m3fn pages
+# ---------------------------------------------------------------------------
+def test_fp8_tables_match_torch_float8():
+    codes = np.arange(256, dtype=np.uint8)
+    want = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = ora.fp8_e4m3_decode(codes)
+    fin = np.isfinite(want)
+    assert np.array_equal(got[fin], want[fin]) and np.isnan(got[~fin]).all()
+    rng = np.random.default_rng(0)
+    x = np.concatenate([rng.standard_normal(50000) * 10.0 ** rng.uniform(-4, 2.6, 50000),
+                        ora.fp8_e4m3_decode(codes[np.isfinite(want)]),            # exact codes
+                        (ora.fp8_e4m3_decode(codes[:126]) + ora.fp8_e4m3_decode(codes[1:127])) / 2]  # ties
+                       ).astype(np.float32)
+    x = x[np.abs(x) <= 448]
+    want_c = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(ora.fp8_e4m3_encode(x), want_c)
+
+
+def test_fp8_row_quantiser():
+    rng = np.random.default_rng(1)
+    x = _bf16(rng, (50, 128), scale=3.0)
+    x[3] = 0
+    codes, sc = ora.quantize_fp8_rows(x)
+    xf = ora.bf16_to_f32(x)
+    back = ora.fp8_e4m3_decode(codes) * sc[:, None]
+    assert sc[3] == 1.0 and not codes[3].any()
+    amax = np.abs(xf).max(axis=1)
+    # the row maximum maps to +-448 and every element is within half an e4m3 step
+    assert np.all(np.abs(ora.fp8_e4m3_decode(codes)).max(axis=1)[amax > 0] == 448.0)
+    rel = np.abs(back - xf) / np.maximum(amax[:, None], 1e-30)
+    assert rel.max() <= 2.0 ** -4 * 1.0001
+
+
+def test_decode_fp8_vs_brute_force():
+    """Quantized decode == float64 attention over the dequantised context."""
+    rng = np.random.default_rng(13)
+    lens, h, hkv, bs = [5, 40, 0, 33], 8, 2, 16
+    nb = int(sum(-(-n // bs) for n in lens)) + 1
+    kf, vf = _pool(rng, nb, bs, hkv)
+    kq, ks = ora.quantize_fp8_rows(kf)            # ks [NB, BS, Hkv]
+    vq, vs = ora.quantize_fp8_rows(vf)
+    bt = _tables(rng, lens, bs, nb)
+    bt = np.concatenate([bt, np.full((len(lens), 4 - bt.shape[1]), -1, np.int32)], axis=1)
+    q = _bf16(rng, (len(lens), h, 128))
+    got = ora.bf16_to_f32(ora.decode_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, lens,
+                                               k_scales_pages=ks.transpose(2, 0, 1),
+                                               v_scales_pages=vs.transpose(2, 0, 1)))
+    kd = ora.f32_to_bf16(ora.fp8_e4m3_decode(kq))                       # exact in bf16
+    # V dequantised exactly in float32 is what the reference's f32 PV sees; compare in f64
+    vd64 = ora.fp8_e4m3_decode(vq).astype(np.float64) * vs[..., None]
+    kd64 = ora.bf16_to_f32(kd).astype(np.float64) * ks[..., None]
+    want = np.zeros_like(got, dtype=np.float64)
+    for b, n in enumerate(lens):
+        if n == 0:
+            continue
+        pages = bt[b, :(n + bs - 1) // bs]
+        kc = kd64[pages].reshape(-1, hkv, 128)[:n]
+        vc = vd64[pages].reshape(-1, hkv, 128)[:n]
+        for hh in range(h):
+            kh = hh // (h // hkv)
+            lg = kc[:, kh] @ ora.bf16_to_f32(q[b, hh]).astype(np.float64)
+            w = np.exp(lg - lg.max())
+            want[b, hh] = (w / w.sum()) @ vc[:, kh]
+    assert np.abs(got - want).max() <= BRUTE_TOL
+    assert not got[2].any()

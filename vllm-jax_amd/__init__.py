@@ -26,7 +26,7 @@ module name ``vllm_jax_amd``::
 """
 from .attention import (DecodeAttentionMetadata, MixedAttentionMetadata, PrefillAttentionMetadata,  # noqa: F401
                         attention, attention_stored, gather_kv, qk_norm_rope_store, qwen3_attention_core,
-                        update_kv_cache)
+                        update_kv_cache, update_kv_cache_fp8)
 from .kernels.decode_paged_attention import decode_paged_attention  # noqa: F401
 from .kernels.mixed_paged_attention import mixed_paged_attention  # noqa: F401
 from .kernels.prefill_paged_attention import prefill_paged_attention  # noqa: F401

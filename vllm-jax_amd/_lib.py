@@ -73,6 +73,30 @@ SIGNATURES = {
         c_i64, c_i64, c_i64,           # page/slot/head strides
         c_vp,                          # stream
     ]),
+    "pa_kv_store_fp8": (ctypes.c_int, [
+        c_vp, c_i64, c_i64,            # k
+        c_vp, c_i64, c_i64,            # v
+        c_vp, c_i32,                   # slot_mapping, num_tokens
+        c_i32, c_i32,                  # num_kv_heads, head_dim
+        c_vp, c_vp, c_vp, c_vp,        # k/v code pools, k/v scale pools
+        c_i32, c_i32,                  # num_pages, page_size
+        c_i64, c_i64, c_i64,           # code page/slot/head strides (bytes)
+        c_i64, c_i64, c_i64,           # scale page/slot/head strides (floats)
+        c_vp,                          # stream
+    ]),
+    "pa_decode_fp8": (ctypes.c_int, [
+        c_vp, c_i64, c_i64,            # q
+        c_vp, c_vp, c_vp, c_vp,        # k/v codes, k/v scales
+        c_i32, c_i32,                  # num_pages, page_size
+        c_i64, c_i64, c_i64,           # code strides (bytes)
+        c_i64, c_i64,                  # scale page/head strides (floats)
+        c_vp, c_i64, c_i32,            # block_tables, bt_stride, pages_per_seq
+        c_vp, c_i32,                   # lengths, batch
+        c_i32, c_i32, c_i32,           # heads, kv heads, head_dim
+        c_f32, c_f32,                  # scale, soft_cap
+        c_vp, c_i64, c_i64,            # out
+        c_vp, c_sz, c_vp,              # workspace, bytes, stream
+    ]),
     # block manager (include/block_manager.h)
     "pa_bm_create": (c_vp, [c_i32, c_i32, c_i32]),
     "pa_bm_destroy": (None, [c_vp]),

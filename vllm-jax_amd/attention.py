@@ -169,6 +169,40 @@ def qk_norm_rope_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm
     return out, kv_cache
 
 
+def update_kv_cache_fp8(kv_codes: torch.Tensor, kv_scales: torch.Tensor, slot_mapping: torch.Tensor,
+                        k: torch.Tensor, v: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Quantising KV store into float8 pages, in place: ``kv_codes`` is the
+    pool ``[2, NB, BS, Hkv, d]`` of float8_e4m3fn (or uint8) codes and
+    ``kv_scales`` ``[2, Hkv, NB, BS]`` float32 (index 0 = K, 1 = V; each half
+    is the reference's ``k_scales_pages`` layout).  Each (token, kv head) row
+    is scaled by 448 / max|row| and rounded to e4m3 (round to nearest even);
+    the stored scale is max|row| / 448.  Slots outside the pool are skipped.
+    Returns ``(kv_codes, kv_scales)``."""
+    for name, t in (("kv_codes", kv_codes), ("kv_scales", kv_scales), ("slot_mapping", slot_mapping),
+                    ("k", k), ("v", v)):
+        require_device(name, t)
+    require_bf16("k", k)
+    require_bf16("v", v)
+    if kv_codes.dim() != 5 or kv_codes.shape[0] != 2 or kv_codes.dtype not in (torch.float8_e4m3fn, torch.uint8):
+        raise ValueError("kv_codes must be a [2, NB, BS, Hkv, d] float8_e4m3fn / uint8 pool")
+    _, nb, bs, hkv, d = kv_codes.shape
+    if tuple(kv_scales.shape) != (2, hkv, nb, bs) or kv_scales.dtype != torch.float32:
+        raise ValueError(f"kv_scales must be float32 [2, {hkv}, {nb}, {bs}]")
+    if tuple(k.shape[1:]) != (hkv, d) or tuple(v.shape) != tuple(k.shape):
+        raise ValueError("k / v must be [T, Hkv, d]")
+    t_count = k.shape[0]
+    if slot_mapping.dtype != torch.int32 or tuple(slot_mapping.shape) != (t_count,):
+        raise ValueError("slot_mapping must be int32 of shape [T]")
+    kc, vc = kv_codes[0], kv_codes[1]
+    ks, vs = kv_scales[0], kv_scales[1]
+    sm = slot_mapping.contiguous()
+    _lib.call("pa_kv_store_fp8", k.data_ptr(), k.stride(0), k.stride(1), v.data_ptr(), v.stride(0), v.stride(1),
+              sm.data_ptr(), t_count, hkv, d, kc.data_ptr(), vc.data_ptr(), ks.data_ptr(), vs.data_ptr(),
+              nb, bs, kc.stride(0), kc.stride(1), kc.stride(2), ks.stride(1), ks.stride(2), ks.stride(0),
+              stream_handle(k))
+    return kv_codes, kv_scales
+
+
 def attention(kv_cache: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
               metadata: AttentionMetadata) -> Tuple[torch.Tensor, torch.Tensor]:
     """qwen3.py:172-218 on gfx950 kernels; returns ``(kv_cache, out)``."""

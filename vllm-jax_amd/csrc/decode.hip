@@ -5,12 +5,12 @@
 
 namespace pa {
 
-template <bool kAligned, bool kSoftCap>
+template <bool kAligned, bool kSoftCap, bool kFp8 = false>
 __global__ void __launch_bounds__(256, 2)
 decode_split_kernel(DecodeParams p) {
   __shared__ DecodeLds red;
-  decode_item<kDecodeWaves, kAligned, kSoftCap>(p, xcd_grouped_item(blockIdx.x, gridDim.x), &red.o[0][0][0],
-                                                &red.m[0][0], &red.l[0][0]);
+  decode_item<kDecodeWaves, kAligned, kSoftCap, kFp8>(p, xcd_grouped_item(blockIdx.x, gridDim.x), &red.o[0][0][0],
+                                                      &red.m[0][0], &red.l[0][0]);
 }
 
 // One wave per (sequence, q head): out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M).
@@ -67,50 +67,56 @@ extern "C" size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int
   return parts * ((size_t)head_dim + 2) * sizeof(float);
 }
 
-extern "C" int pa_decode(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
-                         const uint16_t* k_cache, const uint16_t* v_cache,
-                         int32_t num_pages, int32_t page_size,
-                         int64_t page_stride, int64_t slot_stride, int64_t head_stride,
-                         const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
-                         const int32_t* lengths, int32_t batch,
-                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
-                         float scale, float soft_cap,
-                         uint16_t* out, int64_t out_batch_stride, int64_t out_head_stride,
-                         void* workspace, size_t workspace_bytes, void* stream) {
+// Shared argument checks and launch of pa_decode / pa_decode_fp8.  `prm`
+// arrives with the cache pointers (and scales) set; the rest is filled here.
+static int decode_common(const char* name, DecodeParams& prm, bool fp8, const uint16_t* q, int64_t q_batch_stride,
+                         int64_t q_head_stride, int32_t num_pages, int32_t page_size, int64_t page_stride,
+                         int64_t slot_stride, int64_t head_stride, const int32_t* block_tables, int64_t bt_stride,
+                         int32_t pages_per_seq, const int32_t* lengths, int32_t batch, int32_t num_heads,
+                         int32_t num_kv_heads, int32_t head_dim, float scale, float soft_cap, uint16_t* out,
+                         int64_t out_batch_stride, int64_t out_head_stride, void* workspace, size_t workspace_bytes,
+                         void* stream) {
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_pages <= 0 || page_size <= 0 ||
       pages_per_seq < 0)
     return fail(PA_ERR_INVALID_ARGUMENT,
-                "pa_decode: bad sizes (batch=%d, num_heads=%d, num_kv_heads=%d, num_pages=%d, "
+                "%s: bad sizes (batch=%d, num_heads=%d, num_kv_heads=%d, num_pages=%d, "
                 "page_size=%d, pages_per_seq=%d)",
-                batch, num_heads, num_kv_heads, num_pages, page_size, pages_per_seq);
+                name, batch, num_heads, num_kv_heads, num_pages, page_size, pages_per_seq);
   if (num_heads % num_kv_heads != 0)
     return fail(PA_ERR_INVALID_ARGUMENT,
-                "pa_decode: Number of Q heads must be divisible by number of KV heads. Got %d and %d.",
+                "%s: Number of Q heads must be divisible by number of KV heads. Got %d and %d.", name,
                 num_heads, num_kv_heads);
   if (head_dim != kHeadDim)
-    return fail(PA_ERR_UNSUPPORTED, "pa_decode: head_dim %d not supported (only %d)", head_dim, kHeadDim);
+    return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported (only %d)", name, head_dim, kHeadDim);
   const int group = num_heads / num_kv_heads;
   if (group > 16)
-    return fail(PA_ERR_UNSUPPORTED, "pa_decode: %d q heads per kv head not supported (max 16)", group);
+    return fail(PA_ERR_UNSUPPORTED, "%s: %d q heads per kv head not supported (max 16)", name, group);
+  if (fp8 && page_size % kDecodeStep != 0)
+    return fail(PA_ERR_UNSUPPORTED, "%s: float8 pages need page_size %% %d == 0 (got %d)", name, kDecodeStep,
+                page_size);
   if (batch == 0) return PA_OK;
-  if (!q || !k_cache || !v_cache || !block_tables || !lengths || !out)
-    return fail(PA_ERR_INVALID_ARGUMENT, "pa_decode: null pointer");
-  const uintptr_t align_bits = (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out;
+  if (num_kv_heads == 1) {  // a size-1 dimension's stride is arbitrary (and never used)
+    head_stride = 0;
+    prm.sc_head_stride = 0;
+  }
+  const void* kc = fp8 ? (const void*)prm.k8 : (const void*)prm.k_cache;
+  const void* vc = fp8 ? (const void*)prm.v8 : (const void*)prm.v_cache;
+  if (!q || !kc || !vc || !block_tables || !lengths || !out || (fp8 && (!prm.k_scales || !prm.v_scales)))
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
+  const uintptr_t align_bits = (uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc | (uintptr_t)out |
+                               (fp8 ? ((uintptr_t)prm.k_scales | (uintptr_t)prm.v_scales) : 0);
   if ((align_bits & 15u) || (q_batch_stride | q_head_stride | page_stride | slot_stride | head_stride) % 8 ||
-      (out_batch_stride | out_head_stride) % 8)
-    return fail(PA_ERR_UNSUPPORTED, "pa_decode: operands must be 16-byte aligned with strides multiple of 8");
+      (out_batch_stride | out_head_stride) % 8 || (fp8 && (prm.sc_page_stride | prm.sc_head_stride) % 4))
+    return fail(PA_ERR_UNSUPPORTED, "%s: operands must be 16-byte aligned with strides multiple of 8", name);
   if ((int64_t)pages_per_seq * page_size > 0x7fffffffLL)
-    return fail(PA_ERR_UNSUPPORTED, "pa_decode: block table spans more than 2^31 tokens");
+    return fail(PA_ERR_UNSUPPORTED, "%s: block table spans more than 2^31 tokens", name);
   const size_t need = pa_decode_workspace_size(batch, num_heads, head_dim, pages_per_seq, page_size);
   if (pages_per_seq > 0 && (!workspace || workspace_bytes < need))
-    return fail(PA_ERR_WORKSPACE, "pa_decode: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    return fail(PA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", name, need, workspace_bytes);
 
-  DecodeParams prm;
   prm.q = q;
   prm.q_bs = q_batch_stride;
   prm.q_hs = q_head_stride;
-  prm.k_cache = k_cache;
-  prm.v_cache = v_cache;
   prm.num_pages = num_pages;
   prm.page_size = page_size;
   prm.page_stride = page_stride;
@@ -141,17 +147,64 @@ extern "C" int pa_decode(const uint16_t* q, int64_t q_batch_stride, int64_t q_he
   hipStream_t s = (hipStream_t)stream;
   const int64_t blocks = (int64_t)batch * prm.n_chunks * num_kv_heads;
   if (blocks > 0x7fffffff)
-    return fail(PA_ERR_UNSUPPORTED, "pa_decode: grid of %lld workgroups too large", (long long)blocks);
+    return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)blocks);
   if (blocks > 0) {  // no table pages: every row is zero, only the merge pass runs
     const bool aligned = page_size % kDecodeStep == 0;
+    const bool cap = prm.soft_cap > 0.f;
     const dim3 grid((unsigned)blocks), block(64 * kDecodeWaves);
-    if (aligned && prm.soft_cap == 0.f) decode_split_kernel<true, false><<<grid, block, 0, s>>>(prm);
+    if (fp8 && !cap) decode_split_kernel<true, false, true><<<grid, block, 0, s>>>(prm);
+    else if (fp8) decode_split_kernel<true, true, true><<<grid, block, 0, s>>>(prm);
+    else if (aligned && !cap) decode_split_kernel<true, false><<<grid, block, 0, s>>>(prm);
     else if (aligned) decode_split_kernel<true, true><<<grid, block, 0, s>>>(prm);
-    else if (prm.soft_cap == 0.f) decode_split_kernel<false, false><<<grid, block, 0, s>>>(prm);
+    else if (!cap) decode_split_kernel<false, false><<<grid, block, 0, s>>>(prm);
     else decode_split_kernel<false, true><<<grid, block, 0, s>>>(prm);
-    int rc = launch_status("pa_decode(split)");
+    int rc = launch_status(name);
     if (rc) return rc;
   }
   launch_decode_merge(prm, s);
-  return launch_status("pa_decode(merge)");
+  return launch_status(name);
+}
+
+extern "C" int pa_decode(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
+                         const uint16_t* k_cache, const uint16_t* v_cache,
+                         int32_t num_pages, int32_t page_size,
+                         int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                         const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                         const int32_t* lengths, int32_t batch,
+                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                         float scale, float soft_cap,
+                         uint16_t* out, int64_t out_batch_stride, int64_t out_head_stride,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+  DecodeParams prm{};
+  prm.k_cache = k_cache;
+  prm.v_cache = v_cache;
+  return decode_common("pa_decode", prm, false, q, q_batch_stride, q_head_stride, num_pages, page_size, page_stride,
+                       slot_stride, head_stride, block_tables, bt_stride, pages_per_seq, lengths, batch, num_heads,
+                       num_kv_heads, head_dim, scale, soft_cap, out, out_batch_stride, out_head_stride, workspace,
+                       workspace_bytes, stream);
+}
+
+extern "C" int pa_decode_fp8(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
+                             const uint8_t* k_cache, const uint8_t* v_cache,
+                             const float* k_scales, const float* v_scales,
+                             int32_t num_pages, int32_t page_size,
+                             int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                             int64_t scale_page_stride, int64_t scale_head_stride,
+                             const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                             const int32_t* lengths, int32_t batch,
+                             int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                             float scale, float soft_cap,
+                             uint16_t* out, int64_t out_batch_stride, int64_t out_head_stride,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  DecodeParams prm{};
+  prm.k8 = k_cache;
+  prm.v8 = v_cache;
+  prm.k_scales = k_scales;
+  prm.v_scales = v_scales;
+  prm.sc_page_stride = scale_page_stride;
+  prm.sc_head_stride = scale_head_stride;
+  return decode_common("pa_decode_fp8", prm, true, q, q_batch_stride, q_head_stride, num_pages, page_size,
+                       page_stride, slot_stride, head_stride, block_tables, bt_stride, pages_per_seq, lengths, batch,
+                       num_heads, num_kv_heads, head_dim, scale, soft_cap, out, out_batch_stride, out_head_stride,
+                       workspace, workspace_bytes, stream);
 }

@@ -33,6 +33,8 @@
 // chunk in the caller's workspace and decode_merge_kernel combines them with
 // the log-sum-exp rule of decode_paged_attention.py:274-282.
 #pragma once
+#include <type_traits>
+
 #include "pa_common.h"
 #include "pa_errors.h"
 
@@ -76,6 +78,13 @@ struct DecodeParams {
   const int32_t* rows;
   int32_t row_limit;
   int32_t zero_empty;  // write zeros for length-0 sequences here (no merge pass follows)
+  // float8 pages: e4m3 codes addressed with the strides above (in bytes), and
+  // per-token float scales addressed [page][head][slot] with slot stride 1
+  const uint8_t* k8;
+  const uint8_t* v8;
+  const float* k_scales;
+  const float* v_scales;
+  int64_t sc_page_stride, sc_head_stride;
 };
 
 __device__ __forceinline__ int64_t decode_row(const DecodeParams& p, int b) { return p.rows ? p.rows[b] : b; }
@@ -91,6 +100,9 @@ __device__ __forceinline__ bool decode_has_row(const DecodeParams& p, int b) {
 // 128-byte lines stay cacheable for the instruction that reads the other half.
 __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ u32x2 ld8_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
 }
 
 __device__ __forceinline__ f32x4 mfma16k16(const bf16x4v& a, const bf16x4v& b, const f32x4& c) {
@@ -126,10 +138,15 @@ __host__ __device__ inline int decode_chunk_tokens(int page_size) { return page_
 // red_m / red_l are LDS arrays of [kWaves][16][d] and [kWaves][16] floats.
 // kAligned: page_size % 16 == 0, so a 16-token step never crosses a page and
 // the chunk's page ids (at most 64) are read once, one per lane.
-template <int kWaves, bool kAligned, bool kSoftCap>
+// kFp8: K/V pages hold float8 e4m3 codes with per-token scales
+// (decode_paged_attention.py:72-81,108-115): K is widened to bf16 exactly
+// and its logits multiplied by the token's K scale; P is multiplied by the
+// token's V scale before PV.  Half the K/V bytes of the bf16 path.
+template <int kWaves, bool kAligned, bool kSoftCap, bool kFp8 = false>
 __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, float* red_o, float* red_m,
                                             float* red_l) {
   static_assert(kWaves == 4 || kWaves == 8, "the combine splits d over the waves");
+  static_assert(!kFp8 || kAligned, "float8 pages need 16-token aligned steps");
   constexpr int kDPerWave = kHeadDim / kWaves;  // output d values each wave finishes
   constexpr int kDPerLane = kDPerWave / 4;      // ... each lane (4 lane groups)
   const int lane = threadIdx.x & 63;
@@ -189,7 +206,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
   float m_run = -1e30f;  // finite so that exp2(x - m) never sees inf - inf
   float l_run = 0.f;
 
-  u32x4 kb[kDecodeBufs][4], vb[kDecodeBufs][4];
+  using KVBuf = std::conditional_t<kFp8, u32x2, u32x4>;  // 8 codes or 8 bf16 per load
+  KVBuf kb[kDecodeBufs][4], vb[kDecodeBufs][4];
+  u32x4 sb[kFp8 ? kDecodeBufs : 1][2];  // K and V scales of tokens t0+4g .. t0+4g+3
 
   // Loads of wave step `ks` (tokens t0 .. t0+15) into one buffer.  Tokens past
   // the sequence end are clamped onto its last token (same page in the aligned
@@ -197,11 +216,38 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
   // wave's last one still issues its 8 loads, all of the first 256 bytes of q
   // (cache hits): every buffer then sees the same number of loads issued
   // after it, and the compiler waits for exactly the buffer being consumed.
-  auto issue = [&](u32x4 (&kd)[4], u32x4 (&vd)[4], int ks) __attribute__((always_inline)) {
+  auto issue = [&](int j, int ks) __attribute__((always_inline)) {
+    KVBuf(&kd)[4] = kb[j];
+    KVBuf(&vd)[4] = vb[j];
     const bool valid = ks < my_steps;  // uniform
     const int t0 = t_begin + kDecodeStep * (kWaves * ks + wave);
     const int lim = len - 1 - t0;  // >= 0 when valid
-    if constexpr (kAligned) {
+    if constexpr (kFp8) {
+      const uint8_t* kbase = reinterpret_cast<const uint8_t*>(p.q);
+      const uint8_t* vbase = kbase;
+      const float* ksp = reinterpret_cast<const float*>(p.q);
+      const float* vsp = ksp;
+      int64_t rs = 0;
+      if (valid) {
+        const int lp = t0 / p.page_size;
+        const int32_t page = __builtin_amdgcn_readlane(my_page, lp - lp_first);
+        const int off = t0 - lp * p.page_size;
+        const int64_t base = (int64_t)page * p.page_stride + (int64_t)off * p.slot_stride + head_off;
+        kbase = p.k8 + base;
+        vbase = p.v8 + base;
+        rs = p.slot_stride;
+        const int64_t sbase = (int64_t)page * p.sc_page_stride + (int64_t)kvh * p.sc_head_stride + off + 4 * g;
+        ksp = p.k_scales + sbase;
+        vsp = p.v_scales + sbase;
+      }
+      const int64_t krow = (int64_t)min(n, lim) * rs;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kd[s] = ld8(kbase + krow + 8 * (4 * s + g));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vd[i] = ld8_stream(vbase + (int64_t)min(4 * g + i, lim) * rs + 8 * n);
+      sb[j][0] = ld16(ksp);
+      sb[j][1] = ld16(vsp);
+    } else if constexpr (kAligned) {
       const uint16_t* kbase = p.q;
       const uint16_t* vbase = p.q;
       int64_t rs = 0;
@@ -240,17 +286,25 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
     }
   };
 
-  auto consume = [&](const u32x4 (&kd)[4], const u32x4 (&vd)[4], int ks) __attribute__((always_inline)) {
+  auto consume = [&](int j, int ks) __attribute__((always_inline)) {
+    const KVBuf(&kd)[4] = kb[j];
+    const KVBuf(&vdr)[4] = vb[j];
     const int t0 = t_begin + kDecodeStep * (kWaves * ks + wave);
     f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) sc = mfma16(as_bf16x8(kd[s]), qt[s], sc);
+    for (int s = 0; s < 4; ++s) {
+      u32x4 kk;
+      if constexpr (kFp8) kk = fp8x8_to_bf16x8(kd[s]);
+      else kk = kd[s];
+      sc = mfma16(as_bf16x8(kk), qt[s], sc);
+    }
     // lane holds S[q = n][token t0 + 4g + r]
     float x[4];
     float mx = -INFINITY;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       float v = sc[r];
+      if constexpr (kFp8) v *= __uint_as_float(sb[j][0][r]);
       if constexpr (kSoftCap) v = p.soft_cap * tanhf(v * p.logit_scale / p.soft_cap) * kLog2e;
       else v = v * p.logit_scale;
       v = t0 + 4 * g + r < len ? v : -INFINITY;
@@ -272,10 +326,21 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
       x[r] = fast_exp2(x[r] - m_run);
       l_run += x[r];
     }
+    if constexpr (kFp8) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)  // past the length the scale slot is not data: select, never multiply
+        x[r] = t0 + 4 * g + r < len ? x[r] * __uint_as_float(sb[j][1][r]) : 0.f;
+    }
     u32x2 pw;
     pw[0] = pack_bf16x2(x[0], x[1]);
     pw[1] = pack_bf16x2(x[2], x[3]);
     const bf16x4v pt = __builtin_bit_cast(bf16x4v, pw);
+    u32x4 vd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if constexpr (kFp8) vd[i] = fp8x8_to_bf16x8(vdr[i]);
+      else vd[i] = vdr[i];
+    }
     // V^T tile j: lane (n, g) supplies d = 8n + j of tokens 4g .. 4g+3
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -287,13 +352,13 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
   };
 
 #pragma unroll
-  for (int j = 0; j < kDecodeBufs; ++j) issue(kb[j], vb[j], j);
+  for (int j = 0; j < kDecodeBufs; ++j) issue(j, j);
   for (int k0 = 0; k0 < my_steps; k0 += kDecodeBufs) {
 #pragma unroll
     for (int j = 0; j < kDecodeBufs; ++j) {
       const int ks = k0 + j;
-      if (ks < my_steps) consume(kb[j], vb[j], ks);
-      issue(kb[j], vb[j], ks + kDecodeBufs);
+      if (ks < my_steps) consume(j, ks);
+      issue(j, ks + kDecodeBufs);
     }
   }
 

@@ -82,6 +82,59 @@ gather_kv_kernel(const uint16_t* __restrict__ cache, int32_t num_pages, int32_t 
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Quantising KV store: one 16-lane group per (token, kv head) row of d = 128,
+// 8 values per lane.  amax over the row (16-lane butterfly), stored scale
+// amax / 448 and codes e4m3(x * (448 / amax)) with round-to-nearest-even
+// (v_cvt_pk_fp8_f32); an all-zero row stores scale 1.  Codes go to the
+// (page, slot, head) byte pool, scales to a [Hkv, NB, BS]-strided float pool.
+__global__ void __launch_bounds__(256)
+kv_store_fp8_kernel(const uint16_t* __restrict__ k, int64_t k_ts, int64_t k_hs,
+                    const uint16_t* __restrict__ v, int64_t v_ts, int64_t v_hs,
+                    const int32_t* __restrict__ slot_mapping, int32_t num_tokens, int32_t num_kv_heads,
+                    uint8_t* __restrict__ k_cache, uint8_t* __restrict__ v_cache,
+                    float* __restrict__ k_scales, float* __restrict__ v_scales,
+                    int64_t num_slots, int32_t page_size,
+                    int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                    int64_t sc_page_stride, int64_t sc_slot_stride, int64_t sc_head_stride) {
+  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;  // (token, head)
+  const int i16 = threadIdx.x & 15;
+  const int64_t t = row / num_kv_heads;
+  if (t >= num_tokens) return;  // whole 16-lane group
+  const int h = (int)(row - t * num_kv_heads);
+  const int64_t slot = slot_mapping[t];
+  if (slot < 0 || slot >= num_slots) return;
+  const int64_t page = slot / page_size;
+  const int64_t off = slot - page * page_size;
+  const int64_t dst = page * page_stride + off * slot_stride + h * head_stride + 8 * i16;
+  const int64_t sdst = page * sc_page_stride + off * sc_slot_stride + h * sc_head_stride;
+#pragma unroll
+  for (int which = 0; which < 2; ++which) {
+    const u32x4 x = ld16(which ? v + t * v_ts + h * v_hs + 8 * i16 : k + t * k_ts + h * k_hs + 8 * i16);
+    float f[8];
+    float a = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      f[2 * e] = bf16_lo(x[e]);
+      f[2 * e + 1] = bf16_hi(x[e]);
+      a = fmaxf(a, fmaxf(fabsf(f[2 * e]), fabsf(f[2 * e + 1])));
+    }
+    a = fmaxf(a, __shfl_xor(a, 1, 16));
+    a = fmaxf(a, __shfl_xor(a, 2, 16));
+    a = fmaxf(a, __shfl_xor(a, 4, 16));
+    a = fmaxf(a, __shfl_xor(a, 8, 16));
+    const bool nz = a > 0.f;
+    const float inv = nz ? 448.f / a : 1.f;
+    const float sc = nz ? a / 448.f : 1.f;
+    int lo = 0, hi = 0;
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0] * inv, f[1] * inv, lo, false);
+    lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[2] * inv, f[3] * inv, lo, true);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[4] * inv, f[5] * inv, hi, false);
+    hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[6] * inv, f[7] * inv, hi, true);
+    *reinterpret_cast<u32x2*>((which ? v_cache : k_cache) + dst) = u32x2{(uint32_t)lo, (uint32_t)hi};
+    if (i16 == 0) (which ? v_scales : k_scales)[sdst] = sc;
+  }
+}
+
 // Page copies for copy-on-write: page dst[i] <- page src[i] for K and V.
 // blockIdx.y = pair, x covers the page's page_size * Hkv * d/8 chunks.
 __global__ void __launch_bounds__(256)
@@ -188,4 +241,34 @@ extern "C" int pa_copy_blocks(uint16_t* k_cache, uint16_t* v_cache, int32_t num_
                                                                   slot_stride, head_stride, cph, cps, src_blocks,
                                                                   dst_blocks);
   return launch_status("pa_copy_blocks");
+}
+
+extern "C" int pa_kv_store_fp8(const uint16_t* k, int64_t k_tok_stride, int64_t k_head_stride,
+                               const uint16_t* v, int64_t v_tok_stride, int64_t v_head_stride,
+                               const int32_t* slot_mapping, int32_t num_tokens,
+                               int32_t num_kv_heads, int32_t head_dim,
+                               uint8_t* k_cache, uint8_t* v_cache, float* k_scales, float* v_scales,
+                               int32_t num_pages, int32_t page_size,
+                               int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                               int64_t scale_page_stride, int64_t scale_slot_stride, int64_t scale_head_stride,
+                               void* stream) {
+  if (num_tokens < 0 || num_kv_heads <= 0 || num_pages <= 0 || page_size <= 0)
+    return fail(PA_ERR_INVALID_ARGUMENT,
+                "pa_kv_store_fp8: bad sizes (num_tokens=%d, num_kv_heads=%d, num_pages=%d, page_size=%d)",
+                num_tokens, num_kv_heads, num_pages, page_size);
+  if (head_dim != 128) return fail(PA_ERR_UNSUPPORTED, "pa_kv_store_fp8: head_dim %d not supported (only 128)", head_dim);
+  if (num_tokens == 0) return PA_OK;
+  if (!k || !v || !slot_mapping || !k_cache || !v_cache || !k_scales || !v_scales)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_kv_store_fp8: null pointer");
+  if (!aligned16(k) || !aligned16(v) || ((uintptr_t)k_cache | (uintptr_t)v_cache) & 7u ||
+      ((uintptr_t)k_scales | (uintptr_t)v_scales) & 3u ||
+      (k_tok_stride | k_head_stride | v_tok_stride | v_head_stride) % 8 || (page_stride | slot_stride | head_stride) % 8)
+    return fail(PA_ERR_UNSUPPORTED, "pa_kv_store_fp8: bf16 rows must be 16-byte and code rows 8-byte aligned");
+  const int64_t groups = (int64_t)num_tokens * num_kv_heads;
+  const int64_t blocks = (groups * 16 + 255) / 256;
+  kv_store_fp8_kernel<<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(
+      k, k_tok_stride, k_head_stride, v, v_tok_stride, v_head_stride, slot_mapping, num_tokens, num_kv_heads,
+      k_cache, v_cache, k_scales, v_scales, (int64_t)num_pages * page_size, page_size, page_stride, slot_stride,
+      head_stride, scale_page_stride, scale_slot_stride, scale_head_stride);
+  return launch_status("pa_kv_store_fp8");
 }

@@ -183,7 +183,7 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
     return fail(PA_ERR_WORKSPACE, "pa_mixed: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
   const float cap = soft_cap > 0.f ? soft_cap : 0.f;
 
-  MixedParams m;
+  MixedParams m{};
   // ---- prefill half: entries num_decodes .. batch-1
   const int n_pre = batch - num_decodes;
   PrefillParams& pp = m.pre;

@@ -43,6 +43,25 @@ __device__ __forceinline__ void st16(void* p, const u32x4& v) {
   *reinterpret_cast<u32x4*>(p) = v;
 }
 
+__device__ __forceinline__ u32x2 ld8(const void* p) {
+  return *reinterpret_cast<const u32x2*>(p);
+}
+
+// Two OCP float8 e4m3fn codes (bytes 0,1 of x, or bytes 2,3 with hi) to two
+// bf16 in one dword, low byte to the low half; exact (every e4m3 value is a
+// bf16 value).
+__device__ __forceinline__ uint32_t fp8x2_to_bf16x2(uint32_t x, bool hi) {
+  const auto r = hi ? __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x, 1.0f, true)
+                    : __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x, 1.0f, false);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// Eight e4m3 codes (one u32x2) to eight bf16 (one u32x4), in order.
+__device__ __forceinline__ u32x4 fp8x8_to_bf16x8(const u32x2& c) {
+  return u32x4{fp8x2_to_bf16x2(c[0], false), fp8x2_to_bf16x2(c[0], true), fp8x2_to_bf16x2(c[1], false),
+               fp8x2_to_bf16x2(c[1], true)};
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) {
   return __builtin_bit_cast(bf16x8, v);
 }

@@ -2,7 +2,9 @@
 ``vllm/kernels/decode_paged_attention.py:decode_paged_attention``.
 
 Same arguments, shapes and ``ValueError`` checks as the reference entry
-(decode_paged_attention.py:300-372).  As in the reference, q is expected to
+(decode_paged_attention.py:300-372).  Quantized pages
+(``k_scales_pages`` / ``v_scales_pages``, decode...:158-159,206-217) are float8
+e4m3fn codes with float32 per-token scales ``[Hkv, NB, BS]``.  As in the reference, q is expected to
 be pre-scaled (the caller divides by sqrt(d), qwen3.py:207) and no scale is
 applied inside; the extra keyword ``scale`` lets a caller fold the scale into
 the kernel instead.  ``lengths=None`` attends to every slot of the block
@@ -75,14 +77,36 @@ def decode_paged_attention(
             raise ValueError(f"The dtype of `lengths` must be int32. Got {lengths.dtype}")
     if block_h % 16:
         raise ValueError(f"block_h must divisible by 16, but is {block_h}.")
-    if k_scales_pages is not None or v_scales_pages is not None:
-        raise NotImplementedError("quantized KV pages (k_scales_pages / v_scales_pages) are not supported")
+    quantized = k_scales_pages is not None or v_scales_pages is not None
+    if quantized:
+        if k_scales_pages is None or v_scales_pages is None:
+            raise ValueError("k_scales_pages and v_scales_pages must be given together")
+        for name, t in (("k_scales_pages", k_scales_pages), ("v_scales_pages", v_scales_pages)):
+            # decode...:206-217
+            if tuple(t.shape) != (num_kv_heads, total_num_pages, page_size):
+                raise ValueError(f"{name} must have shape {(num_kv_heads, total_num_pages, page_size)}, "
+                                 f"got {tuple(t.shape)}")
+            if t.dtype != torch.float32:
+                raise ValueError(f"{name} must be float32, got {t.dtype}")
+            if t.stride(2) != 1:
+                raise ValueError(f"{name} must be contiguous over the slots of a page")
+        if tuple(k_scales_pages.stride()) != tuple(v_scales_pages.stride()):
+            raise ValueError("k_scales_pages and v_scales_pages must share strides")
+        for name, t in (("k_pages", k_pages), ("v_pages", v_pages)):
+            if t.dtype not in (torch.float8_e4m3fn, torch.uint8):
+                raise ValueError(f"{name} of quantized pages must be float8_e4m3fn (or its uint8 codes), "
+                                 f"got {t.dtype}")
+            if t.stride(-1) != 1:
+                raise ValueError(f"{name} must be contiguous in its last dimension")
+        require_device("k_scales_pages", k_scales_pages)
+        require_device("v_scales_pages", v_scales_pages)
 
     for name, t in (("q", q), ("k_pages", k_pages), ("v_pages", v_pages), ("block_tables", block_tables)):
         require_device(name, t)
     require_bf16("q", q)
-    require_bf16("k_pages", k_pages)
-    require_bf16("v_pages", v_pages)
+    if not quantized:
+        require_bf16("k_pages", k_pages)
+        require_bf16("v_pages", v_pages)
     if block_tables.dtype != torch.int32:
         raise ValueError("block_tables must be int32")
     if tuple(k_pages.stride()) != tuple(v_pages.stride()):
@@ -105,6 +129,21 @@ def decode_paged_attention(
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
     soft_cap = 0.0 if attn_logits_soft_cap is None else float(attn_logits_soft_cap)
     ps, ss, hs = pages_strides(k_pages)
+    if quantized:
+        _lib.call(
+            "pa_decode_fp8",
+            q.data_ptr(), q.stride(0), q.stride(1),
+            k_pages.data_ptr(), v_pages.data_ptr(), k_scales_pages.data_ptr(), v_scales_pages.data_ptr(),
+            total_num_pages, page_size, ps, ss, hs,
+            k_scales_pages.stride(1), k_scales_pages.stride(0),
+            bt.data_ptr(), bt.stride(0), pages_per_sequence,
+            lens.data_ptr(), batch_size,
+            num_heads, num_kv_heads, head_dim,
+            float(scale), soft_cap,
+            out.data_ptr(), out.stride(0), out.stride(1),
+            workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+            stream_handle(q))
+        return out
     _lib.call(
         "pa_decode",
         q.data_ptr(), q.stride(0), q.stride(1),
