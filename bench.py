@@ -10,6 +10,10 @@ workload, inputs resident in HBM:
 * Qwen3-8B decode (256 sequences, ctx ~ U[512, 8192], 32 q / 8 kv heads,
   16384-page pool, seed 2): KV store of the new token + split-K decode.
   Reported under ``"decode"`` in GB/s of algorithmic HBM traffic.
+* The Qwen3-8B decode over float8 e4m3 pages with per-token scales (the same
+  pool quantised on the device): reported under ``"decode_fp8"`` in GB/s of
+  its own algorithmic bytes (codes + scales), with the bf16 decode time of
+  the same batch for comparison.
 * The Qwen3-0.6B mixed scheduler step (96 decode sequences ctx ~ U[256,
   4096] + 32 prefill sequences L ~ U[64, 2048], seed 1) as one unpadded
   ``pa_mixed`` launch against the separate decode and prefill launches
@@ -129,6 +133,7 @@ def run_gpu(args):
     run_d = args.only in (None, "decode")
     run_r = args.only in (None, "rope")
     run_m = args.only in (None, "mixed")
+    run_f = args.only in (None, "decode_fp8")
     nop = lambda: None
     if not run_p:
         prefill_step = prefill_attn = nop
@@ -170,6 +175,8 @@ def run_gpu(args):
 
     rope = run_rope(args, torch, pkg, pb, pt, kv_p) if run_r else None
     mixed = run_mixed(args, torch, pkg, wl, dev) if run_m else None
+    dec8 = run_decode_fp8(args, torch, pkg, db, dt_, ws, dscale, float(d_attn.mean()) if run_d else None) \
+        if run_f else None
 
     traffic = _load_traffic()
     res = {
@@ -237,7 +244,53 @@ def run_gpu(args):
         res["qk_norm_rope"] = rope
     if mixed is not None:
         res["mixed"] = mixed
+    if dec8 is not None:
+        dec8["roofline"]["traffic"] = traffic.get("decode_fp8_split_kernel")
+        res["decode_fp8"] = dec8
     return res, (pb, pt, db, dt_)
+
+
+def run_decode_fp8(args, torch, pkg, db, dt_, ws, dscale, bf16_ms):
+    """Quantise the decode pool to float8 pages on the device and time the
+    quantized split-K decode of the same batch."""
+    kv = dt_["kv_cache"]
+    nb, bs, hkv, d = kv.shape[1:]
+    codes = torch.empty((2, nb, bs, hkv, d), dtype=torch.float8_e4m3fn, device=kv.device)
+    scales = torch.empty((2, hkv, nb, bs), dtype=torch.float32, device=kv.device)
+    pkg.update_kv_cache_fp8(codes, scales, torch.arange(nb * bs, dtype=torch.int32, device=kv.device),
+                            kv[0].reshape(-1, hkv, d), kv[1].reshape(-1, hkv, d))
+    out = torch.empty_like(dt_["q"])
+    kp, vp = codes[0].permute(2, 0, 1, 3), codes[1].permute(2, 0, 1, 3)
+
+    def call():
+        pkg.decode_paged_attention(dt_["q"], kp, vp, dt_["block_tables"], dt_["context_lens"],
+                                   k_scales_pages=scales[0], v_scales_pages=scales[1], scale=dscale,
+                                   workspace=ws, out=out)
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(max(args.steps, 10)):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / max(args.steps, 10)
+    ctx = int(db.context_lens.sum())
+    pages = int(np.ceil(db.context_lens / db.page_size).sum())
+    nbytes = ctx * hkv * (2 * d + 8) + 2 * db.batch * db.num_heads * d * 2 + 4 * pages + 4 * db.batch
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "decode attn GB/s over float8 e4m3 pages",
+        "algorithmic_gb": round(nbytes / 1e9, 4),
+        "attn_ms": round(ms, 4),
+        "bf16_attn_ms": round(bf16_ms, 4) if bf16_ms else None,
+        "speedup_vs_bf16": round(bf16_ms / ms, 3) if bf16_ms else None,
+        "roofline": {"kernel": "decode_split_kernel<true, false, true> + decode_merge_kernel", "bound": "hbm",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
 
 
 def run_mixed(args, torch, pkg, wl, dev):
@@ -407,7 +460,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU oracle work (total)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "rope", "mixed", "copy"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "rope", "mixed", "decode_fp8", "copy"], default=None,
                     help="profiling aid: run one kernel family only (the JSON line then covers that part)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

@@ -106,7 +106,8 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
   const uintptr_t align_bits = (uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc | (uintptr_t)out |
                                (fp8 ? ((uintptr_t)prm.k_scales | (uintptr_t)prm.v_scales) : 0);
   if ((align_bits & 15u) || (q_batch_stride | q_head_stride | page_stride | slot_stride | head_stride) % 8 ||
-      (out_batch_stride | out_head_stride) % 8 || (fp8 && (prm.sc_page_stride | prm.sc_head_stride) % 4))
+      (out_batch_stride | out_head_stride) % 8 ||
+      (fp8 && ((page_stride | slot_stride | head_stride) % 16 || (prm.sc_page_stride | prm.sc_head_stride) % 4)))
     return fail(PA_ERR_UNSUPPORTED, "%s: operands must be 16-byte aligned with strides multiple of 8", name);
   if ((int64_t)pages_per_seq * page_size > 0x7fffffffLL)
     return fail(PA_ERR_UNSUPPORTED, "%s: block table spans more than 2^31 tokens", name);

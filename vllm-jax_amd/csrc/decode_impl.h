@@ -47,6 +47,10 @@ constexpr int kDecodeWaves = 4;     // waves per workgroup
 #define PA_DECODE_BUFS 4
 #endif
 constexpr int kDecodeBufs = PA_DECODE_BUFS;  // steps in flight per wave
+#ifndef PA_DECODE_BUFS_FP8
+#define PA_DECODE_BUFS_FP8 4
+#endif
+constexpr int kDecodeBufsFp8 = PA_DECODE_BUFS_FP8;  // ... with float8 pages (half the bytes per step)
 constexpr float kDecodeSlack = 8.f;          // lazy-rescale threshold (log2 units)
 
 typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4v;
@@ -147,6 +151,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
                                             float* red_l) {
   static_assert(kWaves == 4 || kWaves == 8, "the combine splits d over the waves");
   static_assert(!kFp8 || kAligned, "float8 pages need 16-token aligned steps");
+  constexpr int kBufs = kFp8 ? kDecodeBufsFp8 : kDecodeBufs;
   constexpr int kDPerWave = kHeadDim / kWaves;  // output d values each wave finishes
   constexpr int kDPerLane = kDPerWave / 4;      // ... each lane (4 lane groups)
   const int lane = threadIdx.x & 63;
@@ -188,14 +193,20 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
     if (lp < p.pages_per_seq) my_page = safe_page(bt_row, lp, p.num_pages);
   }
 
-  // Q^T operand: k-step s uses d chunk (4s + g) for both Q and K.
+  // Q^T operand: k-step s uses d chunk kchunk(s) for both Q and K (any
+  // bijection works for a dot product).  bf16 pages: chunk 4s + g.  Float8
+  // pages: chunk 8(s/2) + 2g + s%2, so that a lane's K chunks for steps
+  // 2r, 2r+1 are 16 adjacent bytes (one 16-byte load per pair of steps).
+  auto kchunk = [&](int s) __attribute__((always_inline)) {
+    return kFp8 ? 8 * (s >> 1) + 2 * g + (s & 1) : 4 * s + g;
+  };
   bf16x8 qt[4];
   {
     const bool live = n < p.group;
     const uint16_t* qrow = p.q + decode_row(p, b) * p.q_bs + (int64_t)(kvh * p.group + (live ? n : 0)) * p.q_hs;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      u32x4 v = live ? ld16(qrow + 8 * (4 * s + g)) : u32x4{0, 0, 0, 0};
+      u32x4 v = live ? ld16(qrow + 8 * kchunk(s)) : u32x4{0, 0, 0, 0};
       qt[s] = as_bf16x8(v);
     }
   }
@@ -206,9 +217,12 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
   float m_run = -1e30f;  // finite so that exp2(x - m) never sees inf - inf
   float l_run = 0.f;
 
-  using KVBuf = std::conditional_t<kFp8, u32x2, u32x4>;  // 8 codes or 8 bf16 per load
-  KVBuf kb[kDecodeBufs][4], vb[kDecodeBufs][4];
-  u32x4 sb[kFp8 ? kDecodeBufs : 1][2];  // K and V scales of tokens t0+4g .. t0+4g+3
+  // K: 4 loads of 8 bf16, or 2 loads of 16 float8 codes; V: 4 loads of 8 values
+  constexpr int kKLoads = kFp8 ? 2 : 4;
+  using VBuf = std::conditional_t<kFp8, u32x2, u32x4>;
+  u32x4 kb[kBufs][kKLoads];
+  VBuf vb[kBufs][4];
+  u32x4 sb[kFp8 ? kBufs : 1][2];  // K and V scales of tokens t0+4g .. t0+4g+3
 
   // Loads of wave step `ks` (tokens t0 .. t0+15) into one buffer.  Tokens past
   // the sequence end are clamped onto its last token (same page in the aligned
@@ -217,8 +231,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
   // (cache hits): every buffer then sees the same number of loads issued
   // after it, and the compiler waits for exactly the buffer being consumed.
   auto issue = [&](int j, int ks) __attribute__((always_inline)) {
-    KVBuf(&kd)[4] = kb[j];
-    KVBuf(&vd)[4] = vb[j];
+    u32x4(&kd)[kKLoads] = kb[j];
+    VBuf(&vd)[4] = vb[j];
     const bool valid = ks < my_steps;  // uniform
     const int t0 = t_begin + kDecodeStep * (kWaves * ks + wave);
     const int lim = len - 1 - t0;  // >= 0 when valid
@@ -242,7 +256,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
       }
       const int64_t krow = (int64_t)min(n, lim) * rs;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) kd[s] = ld8(kbase + krow + 8 * (4 * s + g));
+      for (int r = 0; r < kKLoads; ++r) kd[r] = ld16(kbase + krow + 64 * r + 16 * g);  // chunks kchunk(2r), kchunk(2r+1)
 #pragma unroll
       for (int i = 0; i < 4; ++i) vd[i] = ld8_stream(vbase + (int64_t)min(4 * g + i, lim) * rs + 8 * n);
       sb[j][0] = ld16(ksp);
@@ -287,15 +301,19 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
   };
 
   auto consume = [&](int j, int ks) __attribute__((always_inline)) {
-    const KVBuf(&kd)[4] = kb[j];
-    const KVBuf(&vdr)[4] = vb[j];
+    const u32x4(&kd)[kKLoads] = kb[j];
+    const VBuf(&vdr)[4] = vb[j];
     const int t0 = t_begin + kDecodeStep * (kWaves * ks + wave);
     f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       u32x4 kk;
-      if constexpr (kFp8) kk = fp8x8_to_bf16x8(kd[s]);
-      else kk = kd[s];
+      if constexpr (kFp8) {
+        const u32x4& w = kd[s >> 1];
+        kk = fp8x8_to_bf16x8((s & 1) ? u32x2{w[2], w[3]} : u32x2{w[0], w[1]});
+      } else {
+        kk = kd[s];
+      }
       sc = mfma16(as_bf16x8(kk), qt[s], sc);
     }
     // lane holds S[q = n][token t0 + 4g + r]
@@ -352,13 +370,13 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
   };
 
 #pragma unroll
-  for (int j = 0; j < kDecodeBufs; ++j) issue(j, j);
-  for (int k0 = 0; k0 < my_steps; k0 += kDecodeBufs) {
+  for (int j = 0; j < kBufs; ++j) issue(j, j);
+  for (int k0 = 0; k0 < my_steps; k0 += kBufs) {
 #pragma unroll
-    for (int j = 0; j < kDecodeBufs; ++j) {
+    for (int j = 0; j < kBufs; ++j) {
       const int ks = k0 + j;
       if (ks < my_steps) consume(j, ks);
-      issue(j, ks + kDecodeBufs);
+      issue(j, ks + kBufs);
     }
   }
 
