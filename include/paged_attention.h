@@ -206,6 +206,35 @@ int pa_decode_fp8(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stri
                   uint16_t* out, int64_t out_batch_stride, int64_t out_head_stride,
                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* Workspace bytes pa_prefill_fp8 needs: two bf16 pages per block-table
+ * entry (K and V) plus one int32 per entry. */
+size_t pa_prefill_fp8_workspace_size(int32_t batch, int32_t pages_per_seq, int32_t page_size,
+                                     int32_t num_kv_heads, int32_t head_dim);
+
+/*
+ * pa_prefill over float8 e4m3fn pages with per-token scales
+ * (prefill_paged_attention.py:169-170,255-266, in-kernel :84-92,120-123).
+ * Every page a sequence uses is first widened into the workspace as bf16
+ * (code * token scale, one rounding); the bf16 prefill then runs on those
+ * pages.  The reference scales the logits and P instead of K and V; the two
+ * differ by that one bf16 rounding.  Strides and scales as in pa_decode_fp8;
+ * the workspace (256-byte aligned) is caller-owned.
+ */
+int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                   const uint8_t* k_cache, const uint8_t* v_cache,
+                   const float* k_scales, const float* v_scales,
+                   int32_t num_pages, int32_t page_size,
+                   int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                   int64_t scale_page_stride, int64_t scale_head_stride,
+                   const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                   const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                   const int32_t* input_positions,
+                   int32_t batch, int32_t num_tokens, int32_t max_seqlen_q,
+                   int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                   float scale, float soft_cap,
+                   uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
 /*
  * Workspace bytes pa_mixed needs (0 when every decode sequence fits one
  * 4096-token chunk, i.e. pages_per_seq * page_size <= the chunk).

@@ -249,7 +249,7 @@ def _merge_splits(o_parts, l_parts, m_parts):
 def prefill_attention(q, k_pages, v_pages, block_tables, cu_seqlens,
                       input_positions, *, cu_seqlens_k=None, k_splits=8,
                       pages_per_compute_block=8, soft_cap=None,
-                      mask_value=DEFAULT_MASK_VALUE, rows=None):
+                      mask_value=DEFAULT_MASK_VALUE, rows=None, k_scales_pages=None, v_scales_pages=None):
     """Ragged causal GQA paged prefill, restating the reference kernel.
 
     Layouts follow the reference kernel entry (prefill...:407-429):
@@ -273,11 +273,18 @@ def prefill_attention(q, k_pages, v_pages, block_tables, cu_seqlens,
 
     ``rows`` (optional int array) restricts the computation to those q rows
     (other rows of the result stay 0) so large workloads can be sampled.
+    Quantized pages (prefill...:169-170,255-266, in-kernel :84-92,120-123):
+    float8 e4m3fn codes with ``[Hkv, NB, BS]`` float32 per-token scales, as in
+    decode_attention.
     Returns bf16 bit patterns ``[T, H, d]``.
     """
     qf = _as_f32(q)
+    quant = k_scales_pages is not None
     kp = np.asarray(k_pages)
     vp = np.asarray(v_pages)
+    if quant:
+        ksp = np.asarray(k_scales_pages, np.float32)
+        vsp = np.asarray(v_scales_pages, np.float32)
     t_total, h, d = qf.shape
     hkv, nb, bs, _ = kp.shape
     g = h // hkv
@@ -316,14 +323,21 @@ def prefill_attention(q, k_pages, v_pages, block_tables, cu_seqlens,
         q_pos = pos[sel]
         valid = (np.arange(p * bs)[None, :] < lk) & (kv_pos[None, :] <= q_pos[:, None])
         for kh in range(hkv):
-            k_ctx = _as_f32(kp[kh][safe[b]].reshape(p * bs, d))
-            v_ctx = _as_f32(vp[kh][safe[b]].reshape(p * bs, d))
+            if quant:
+                k_ctx = fp8_e4m3_decode(kp[kh][safe[b]].reshape(p * bs, d))
+                v_ctx = fp8_e4m3_decode(vp[kh][safe[b]].reshape(p * bs, d))
+                k_sc = ksp[kh][safe[b]].reshape(p * bs)
+                v_sc = vsp[kh][safe[b]].reshape(p * bs)
+            else:
+                k_ctx = _as_f32(kp[kh][safe[b]].reshape(p * bs, d))
+                v_ctx = _as_f32(vp[kh][safe[b]].reshape(p * bs, d))
+                k_sc = v_sc = None
             qs = qs_all[sel, kh * g:(kh + 1) * g].reshape(-1, d)
             vmask = np.repeat(valid, g, axis=0)
             o_p, l_p, m_p = _split_attention_rows(
                 qs, k_ctx, v_ctx, vmask, k_splits=ks, block_k=block_k,
                 page_size=bs, used_tokens=lk, soft_cap=soft_cap,
-                mask_value=mask_value)
+                mask_value=mask_value, k_scale=k_sc, v_scale=v_sc)
             res = _merge_splits(o_p, l_p, m_p)
             out[sel, kh * g:(kh + 1) * g] = res.reshape(sel.size, g, d)
     return f32_to_bf16(out)

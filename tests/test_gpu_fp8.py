@@ -126,3 +126,41 @@ def test_decode_fp8_qwen3_8b_full_pool(pkg, dev):
     err = np.abs(ora.bf16_to_f32(got[seqs]) - ora.bf16_to_f32(want)).max()
     print(f"fp8 Qwen3-8B decode max-abs err {err:.3e}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("lens,prefix,h,hkv,bs", [
+    ([17, 128, 300, 511], [0, 0, 0, 0], 16, 8, 256),    # the Qwen3-0.6B single-layer prefill
+    ([5, 40, 130], [0, 20, 300], 8, 2, 16),              # cached prefixes, small pages
+    ([200, 37], [64, 0], 64, 8, 64),                     # G = 8
+])
+def test_prefill_fp8_matches_oracle(pkg, dev, lens, prefix, h, hkv, bs):
+    import torch
+    rng = np.random.default_rng(sum(lens) + h)
+    kv = [p + n for p, n in zip(prefix, lens)]
+    pages = [(n + bs - 1) // bs for n in kv]
+    nb = sum(pages) + 2
+    width = max(pages)
+    kq, vq, ks, vs = _quantized_pool(rng, nb, bs, hkv)
+    perm = rng.permutation(nb)
+    bt = np.full((len(lens), width), -1, np.int32)
+    c = 0
+    for b, p in enumerate(pages):
+        bt[b, :p] = perm[c:c + p]
+        c += p
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cuk = np.concatenate([[0], np.cumsum(kv)]).astype(np.int32)
+    pos = np.concatenate([np.arange(p, p + n) for p, n in zip(prefix, lens)]).astype(np.int32)
+    q = _bf16(rng, (int(cu[-1]), h, 128))
+    i32 = lambda x: torch.as_tensor(np.ascontiguousarray(x, dtype=np.int32), device=dev)
+    kd = torch.from_numpy(kq).to(dev).view(torch.float8_e4m3fn)
+    vd = torch.from_numpy(vq).to(dev).view(torch.float8_e4m3fn)
+    out = pkg.prefill_paged_attention(from_u16(q, dev), kd.permute(2, 0, 1, 3), vd.permute(2, 0, 1, 3), i32(bt),
+                                      i32(cu), None, i32(pos), max_seqlen_bucket=max(lens), cu_seqlens_k=i32(cuk),
+                                      k_scales_pages=torch.from_numpy(ks).to(dev),
+                                      v_scales_pages=torch.from_numpy(vs).to(dev))
+    torch.cuda.synchronize()
+    want = ora.prefill_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, cu, pos,
+                                 cu_seqlens_k=cuk, k_scales_pages=ks, v_scales_pages=vs)
+    err = np.abs(ora.bf16_to_f32(u16(out)) - ora.bf16_to_f32(want)).max()
+    print(f"fp8 prefill max-abs err {err:.3e}")
+    assert err <= TOL

@@ -40,7 +40,7 @@ def test_prefill_shape_errors_match_reference():
         PKG.prefill_paged_attention(*b[:3], b[3].long(), *b[4:], max_seqlen_bucket=8)
     with pytest.raises(ValueError, match="block_h must divisible by 16"):
         PKG.prefill_paged_attention(*_prefill_args(), max_seqlen_bucket=8, block_h=8)
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(ValueError, match="must be given together"):
         PKG.prefill_paged_attention(*_prefill_args(), max_seqlen_bucket=8, k_scales_pages=torch.zeros(1))
 
 

@@ -453,3 +453,32 @@ def test_decode_fp8_vs_brute_force():
             want[b, hh] = (w / w.sum()) @ vc[:, kh]
     assert np.abs(got - want).max() <= BRUTE_TOL
     assert not got[2].any()
+
+
+def test_prefill_fp8_vs_brute_force():
+    """Quantized prefill == float64 attention over the dequantised context."""
+    rng = np.random.default_rng(14)
+    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, [12, 30, 1], 8, 2, 16, prefix=[0, 20, 47])
+    kq, ks = ora.quantize_fp8_rows(kc)
+    vq, vs = ora.quantize_fp8_rows(vc)
+    got = ora.bf16_to_f32(ora.prefill_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, cu, pos,
+                                                cu_seqlens_k=cuk, k_scales_pages=ks.transpose(2, 0, 1),
+                                                v_scales_pages=vs.transpose(2, 0, 1)))
+    sc = float(ora.round_bf16(np.float32(1 / math.sqrt(128))).reshape(-1)[0])
+    qs = ora.bf16_to_f32(ora.f32_to_bf16(ora.round_bf16(ora.bf16_to_f32(q) * np.float32(sc)))).astype(np.float64)
+    kd = ora.fp8_e4m3_decode(kq).astype(np.float64) * ks[..., None]
+    vd = ora.fp8_e4m3_decode(vq).astype(np.float64) * vs[..., None]
+    want = np.zeros_like(got, dtype=np.float64)
+    for b in range(len(cu) - 1):
+        lq, lk = cu[b + 1] - cu[b], cuk[b + 1] - cuk[b]
+        pages = bt[b, :(lk + 15) // 16]
+        kctx = kd[pages].reshape(-1, 2, 128)[:lk]
+        vctx = vd[pages].reshape(-1, 2, 128)[:lk]
+        for i in range(lq):
+            row = cu[b] + i
+            vis = np.arange(lk) + pos[cu[b]] - (lk - lq) <= pos[row]
+            for hh in range(8):
+                lg = kctx[vis, hh // 4] @ qs[row, hh]
+                w = np.exp(lg - lg.max())
+                want[row, hh] = (w / w.sum()) @ vctx[vis, hh // 4]
+    assert np.abs(got - want).max() <= BRUTE_TOL

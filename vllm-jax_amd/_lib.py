@@ -97,6 +97,21 @@ SIGNATURES = {
         c_vp, c_i64, c_i64,            # out
         c_vp, c_sz, c_vp,              # workspace, bytes, stream
     ]),
+    "pa_prefill_fp8_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "pa_prefill_fp8": (ctypes.c_int, [
+        c_vp, c_i64, c_i64,            # q
+        c_vp, c_vp, c_vp, c_vp,        # k/v codes, k/v scales
+        c_i32, c_i32,                  # num_pages, page_size
+        c_i64, c_i64, c_i64,           # code strides (bytes)
+        c_i64, c_i64,                  # scale page/head strides (floats)
+        c_vp, c_i64, c_i32,            # block_tables, bt_stride, pages_per_seq
+        c_vp, c_vp, c_vp,              # cu_seqlens_q, cu_seqlens_k, input_positions
+        c_i32, c_i32, c_i32,           # batch, num_tokens, max_seqlen_q
+        c_i32, c_i32, c_i32,           # heads, kv heads, head_dim
+        c_f32, c_f32,                  # scale, soft_cap
+        c_vp, c_i64, c_i64,            # out
+        c_vp, c_sz, c_vp,              # workspace, bytes, stream
+    ]),
     # block manager (include/block_manager.h)
     "pa_bm_create": (c_vp, [c_i32, c_i32, c_i32]),
     "pa_bm_destroy": (None, [c_vp]),

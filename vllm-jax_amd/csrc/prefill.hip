@@ -1,6 +1,8 @@
 // Ragged causal GQA paged prefill for gfx950: the kernel entry and its host
 // launcher.  The work item (one q tile of one sequence and kv head) is
 // prefill_body in prefill_impl.h.
+#include <algorithm>
+
 #include "prefill_impl.h"
 
 namespace pa {
@@ -43,51 +45,99 @@ prefill_zero_rows_kernel(const int32_t* __restrict__ cu_q, int32_t batch, int32_
   }
 }
 
+// Float8 pages for the prefill: every page a sequence uses (block-table
+// entry lp with lp * page_size < its kv length) is widened into a bf16
+// workspace pool, entry (b, lp) to workspace page b * P + lp, each element
+// bf16(code * scale of its token) (one rounding), and the new table points
+// there (-1 for unused entries, which the prefill never reads).  One
+// workgroup per table entry, 16 codes per thread and step.
+__global__ void __launch_bounds__(256)
+prefill_dequant_pages_kernel(const uint8_t* __restrict__ k8, const uint8_t* __restrict__ v8,
+                             const float* __restrict__ ks, const float* __restrict__ vs, int32_t num_pages,
+                             int32_t page_size, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                             int64_t sc_page_stride, int64_t sc_head_stride, const int32_t* __restrict__ bt,
+                             int64_t bt_stride, int32_t pages_per_seq, const int32_t* __restrict__ cu_q,
+                             const int32_t* __restrict__ cu_k, int32_t num_kv_heads, uint16_t* __restrict__ wk,
+                             uint16_t* __restrict__ wv, int32_t* __restrict__ bt_out) {
+  const int64_t e = blockIdx.x;  // table entry (b, lp)
+  const int b = (int)(e / pages_per_seq);
+  const int lp = (int)(e - (int64_t)b * pages_per_seq);
+  const int lk = cu_k ? cu_k[b + 1] - cu_k[b] : cu_q[b + 1] - cu_q[b];
+  const bool used = (int64_t)lp * page_size < lk;
+  if (threadIdx.x == 0) bt_out[e] = used ? (int32_t)e : -1;
+  if (!used) return;
+  const int32_t raw = bt[(int64_t)b * bt_stride + lp];
+  const int64_t page = raw < 0 ? 0 : (raw >= num_pages ? num_pages - 1 : raw);
+  const int rows = page_size * num_kv_heads;  // (slot, head) rows of 128 codes
+  const int64_t wbase = e * (int64_t)rows * kPHeadDim;
+  for (int c = threadIdx.x; c < rows * 8; c += 256) {
+    const int r = c >> 3, part = c & 7;  // 16 codes of row r
+    const int slot = r / num_kv_heads, h = r - slot * num_kv_heads;
+    const int64_t src = page * page_stride + (int64_t)slot * slot_stride + (int64_t)h * head_stride + 16 * part;
+    const int64_t sidx = page * sc_page_stride + (int64_t)h * sc_head_stride + slot;
+    const int64_t dst = wbase + (int64_t)r * kPHeadDim + 16 * part;
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+      const u32x4 x = ld16((which ? v8 : k8) + src);
+      const float sc = (which ? vs : ks)[sidx];
+      u32x4 o[2];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], false);
+        const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], true);
+        o[w >> 1][2 * (w & 1)] = pack_bf16x2(lo[0] * sc, lo[1] * sc);
+        o[w >> 1][2 * (w & 1) + 1] = pack_bf16x2(hi[0] * sc, hi[1] * sc);
+      }
+      uint16_t* d = (which ? wv : wk) + dst;
+      st16(d, o[0]);
+      st16(d + 8, o[1]);
+    }
+  }
+}
+
 }  // namespace pa
 
 using namespace pa;
 
-extern "C" int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
-                          const uint16_t* k_cache, const uint16_t* v_cache,
-                          int32_t num_pages, int32_t page_size,
+// Checks and launches of pa_prefill; pa_prefill_fp8 runs it on its bf16
+// workspace pool.
+static int prefill_launch(const char* name, const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                          const uint16_t* k_cache, const uint16_t* v_cache, int32_t num_pages, int32_t page_size,
                           int64_t page_stride, int64_t slot_stride, int64_t head_stride,
                           const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                          const int32_t* input_positions,
-                          int32_t batch, int32_t num_tokens, int32_t max_seqlen_q,
-                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
-                          float scale, float soft_cap,
-                          uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
-                          void* stream) {
+                          const int32_t* input_positions, int32_t batch, int32_t num_tokens, int32_t max_seqlen_q,
+                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale, float soft_cap,
+                          uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride, void* stream) {
   if (batch < 0 || num_tokens < 0 || max_seqlen_q < 0 || num_heads <= 0 || num_kv_heads <= 0 ||
       num_pages <= 0 || page_size <= 0 || pages_per_seq < 0)
     return fail(PA_ERR_INVALID_ARGUMENT,
-                "pa_prefill: bad sizes (batch=%d, num_tokens=%d, max_seqlen_q=%d, num_heads=%d, "
+                "%s: bad sizes (batch=%d, num_tokens=%d, max_seqlen_q=%d, num_heads=%d, "
                 "num_kv_heads=%d, num_pages=%d, page_size=%d, pages_per_seq=%d)",
-                batch, num_tokens, max_seqlen_q, num_heads, num_kv_heads, num_pages, page_size,
+                name, batch, num_tokens, max_seqlen_q, num_heads, num_kv_heads, num_pages, page_size,
                 pages_per_seq);
   if (num_heads % num_kv_heads != 0)
     return fail(PA_ERR_INVALID_ARGUMENT,
-                "pa_prefill: Number of Q heads must be divisible by number of KV heads. Got %d and %d.",
+                "%s: Number of Q heads must be divisible by number of KV heads. Got %d and %d.", name,
                 num_heads, num_kv_heads);
   if (head_dim != kPHeadDim)
-    return fail(PA_ERR_UNSUPPORTED, "pa_prefill: head_dim %d not supported (only %d)", head_dim, kPHeadDim);
+    return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported (only %d)", name, head_dim, kPHeadDim);
   const int group = num_heads / num_kv_heads;
   if (group > kRows)
-    return fail(PA_ERR_UNSUPPORTED, "pa_prefill: %d q heads per kv head not supported (max %d)", group, kRows);
+    return fail(PA_ERR_UNSUPPORTED, "%s: %d q heads per kv head not supported (max %d)", name, group, kRows);
   if (num_tokens == 0) return PA_OK;
   if (!q || !out || !cu_seqlens_q || !input_positions || (batch > 0 && (!k_cache || !v_cache || !block_tables)))
-    return fail(PA_ERR_INVALID_ARGUMENT, "pa_prefill: null pointer");
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
   const uintptr_t align_bits = (uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache | (uintptr_t)out;
   if ((align_bits & 15u) || (q_tok_stride | q_head_stride | page_stride | slot_stride | head_stride |
                              out_tok_stride | out_head_stride) % 8)
-    return fail(PA_ERR_UNSUPPORTED, "pa_prefill: operands must be 16-byte aligned with strides multiple of 8");
+    return fail(PA_ERR_UNSUPPORTED, "%s: operands must be 16-byte aligned with strides multiple of 8", name);
   hipStream_t s = (hipStream_t)stream;
 
   {
     prefill_zero_rows_kernel<<<dim3((unsigned)((num_tokens + 3) / 4)), dim3(256), 0, s>>>(
         cu_seqlens_q, batch, num_tokens, max_seqlen_q, num_heads, out, out_tok_stride, out_head_stride);
-    int rc = launch_status("pa_prefill(zero rows)");
+    int rc = launch_status(name);
     if (rc) return rc;
   }
   if (batch == 0 || max_seqlen_q == 0) return PA_OK;
@@ -125,7 +175,7 @@ extern "C" int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_hea
   prm.o_hs = out_head_stride;
   const int64_t blocks = (int64_t)prm.n_qtiles * batch * num_kv_heads;
   if (blocks > 0x7fffffff)
-    return fail(PA_ERR_UNSUPPORTED, "pa_prefill: grid of %lld workgroups too large", (long long)blocks);
+    return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)blocks);
   const bool aligned = page_size % kTileN == 0;
   if (prm.soft_cap > 0.f) {
     if (aligned) prefill_kernel<true, true><<<dim3((unsigned)blocks), dim3(kThreads), 0, s>>>(prm);
@@ -134,5 +184,90 @@ extern "C" int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_hea
     if (aligned) prefill_kernel<false, true><<<dim3((unsigned)blocks), dim3(kThreads), 0, s>>>(prm);
     else prefill_kernel<false, false><<<dim3((unsigned)blocks), dim3(kThreads), 0, s>>>(prm);
   }
-  return launch_status("pa_prefill");
+  return launch_status(name);
+}
+
+extern "C" int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                          const uint16_t* k_cache, const uint16_t* v_cache,
+                          int32_t num_pages, int32_t page_size,
+                          int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                          const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                          const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                          const int32_t* input_positions,
+                          int32_t batch, int32_t num_tokens, int32_t max_seqlen_q,
+                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                          float scale, float soft_cap,
+                          uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
+                          void* stream) {
+  return prefill_launch("pa_prefill", q, q_tok_stride, q_head_stride, k_cache, v_cache, num_pages, page_size,
+                        page_stride, slot_stride, head_stride, block_tables, bt_stride, pages_per_seq, cu_seqlens_q,
+                        cu_seqlens_k, input_positions, batch, num_tokens, max_seqlen_q, num_heads, num_kv_heads,
+                        head_dim, scale, soft_cap, out, out_tok_stride, out_head_stride, stream);
+}
+
+extern "C" size_t pa_prefill_fp8_workspace_size(int32_t batch, int32_t pages_per_seq, int32_t page_size,
+                                                int32_t num_kv_heads, int32_t head_dim) {
+  if (batch <= 0 || pages_per_seq <= 0 || page_size <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
+  const size_t entries = (size_t)batch * pages_per_seq;
+  const size_t page_elems = (size_t)page_size * num_kv_heads * head_dim;
+  return 2 * entries * page_elems * sizeof(uint16_t) + entries * sizeof(int32_t);
+}
+
+extern "C" int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                              const uint8_t* k_cache, const uint8_t* v_cache,
+                              const float* k_scales, const float* v_scales,
+                              int32_t num_pages, int32_t page_size,
+                              int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                              int64_t scale_page_stride, int64_t scale_head_stride,
+                              const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                              const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                              const int32_t* input_positions,
+                              int32_t batch, int32_t num_tokens, int32_t max_seqlen_q,
+                              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                              float scale, float soft_cap,
+                              uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  if (batch < 0 || num_pages <= 0 || page_size <= 0 || pages_per_seq < 0 || num_kv_heads <= 0)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_prefill_fp8: bad sizes (batch=%d, num_pages=%d, page_size=%d, "
+                "pages_per_seq=%d, num_kv_heads=%d)", batch, num_pages, page_size, pages_per_seq, num_kv_heads);
+  if (head_dim != kPHeadDim)
+    return fail(PA_ERR_UNSUPPORTED, "pa_prefill_fp8: head_dim %d not supported (only %d)", head_dim, kPHeadDim);
+  if (batch == 0 || pages_per_seq == 0 || num_tokens == 0)  // nothing to widen: zero rows only
+    return prefill_launch("pa_prefill_fp8", q, q_tok_stride, q_head_stride, nullptr, nullptr, 1, page_size,
+                          (int64_t)page_size * num_kv_heads * head_dim, (int64_t)num_kv_heads * head_dim, head_dim,
+                          block_tables, bt_stride, pages_per_seq, cu_seqlens_q, cu_seqlens_k, input_positions, 0,
+                          num_tokens, max_seqlen_q, num_heads, num_kv_heads, head_dim, scale, soft_cap, out,
+                          out_tok_stride, out_head_stride, stream);
+  if (!k_cache || !v_cache || !k_scales || !v_scales || !block_tables || !cu_seqlens_q)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_prefill_fp8: null pointer");
+  if (num_kv_heads == 1) {  // a size-1 dimension's stride is arbitrary (and never used)
+    head_stride = 0;
+    scale_head_stride = 0;
+  }
+  if ((((uintptr_t)k_cache | (uintptr_t)v_cache) & 15u) || (page_stride | slot_stride | head_stride) % 16 ||
+      (((uintptr_t)k_scales | (uintptr_t)v_scales) & 3u))
+    return fail(PA_ERR_UNSUPPORTED, "pa_prefill_fp8: code rows must be 16-byte aligned");
+  const size_t need = pa_prefill_fp8_workspace_size(batch, pages_per_seq, page_size, num_kv_heads, head_dim);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u))
+    return fail(PA_ERR_WORKSPACE, "pa_prefill_fp8: 256-byte aligned workspace of %zu bytes needed, %zu given", need,
+                workspace_bytes);
+  const int64_t entries = (int64_t)batch * pages_per_seq;
+  if (entries > 0x7fffffff)
+    return fail(PA_ERR_UNSUPPORTED, "pa_prefill_fp8: %lld table entries", (long long)entries);
+  const int64_t page_elems = (int64_t)page_size * num_kv_heads * head_dim;
+  uint16_t* wk = reinterpret_cast<uint16_t*>(workspace);
+  uint16_t* wv = wk + entries * page_elems;
+  int32_t* bt2 = reinterpret_cast<int32_t*>(wv + entries * page_elems);
+  hipStream_t s = (hipStream_t)stream;
+  prefill_dequant_pages_kernel<<<dim3((unsigned)entries), dim3(256), 0, s>>>(
+      k_cache, v_cache, k_scales, v_scales, num_pages, page_size, page_stride, slot_stride, head_stride,
+      scale_page_stride, scale_head_stride, block_tables, bt_stride, pages_per_seq, cu_seqlens_q, cu_seqlens_k,
+      num_kv_heads, wk, wv, bt2);
+  int rc = launch_status("pa_prefill_fp8(widen)");
+  if (rc) return rc;
+  return prefill_launch("pa_prefill_fp8", q, q_tok_stride, q_head_stride, wk, wv, (int32_t)std::min<int64_t>(entries, 0x7fffffff),
+                        page_size, page_elems, (int64_t)num_kv_heads * head_dim, head_dim, bt2, pages_per_seq,
+                        pages_per_seq, cu_seqlens_q, cu_seqlens_k, input_positions, batch, num_tokens, max_seqlen_q,
+                        num_heads, num_kv_heads, head_dim, scale, soft_cap, out, out_tok_stride, out_head_stride,
+                        stream);
 }

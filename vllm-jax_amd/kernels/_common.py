@@ -52,3 +52,32 @@ def pages_strides(k_pages: torch.Tensor):
     if ds != 1:
         raise ValueError("k_pages must be contiguous in head_dim")
     return ps, ss, hs
+
+
+def check_quantized_pages(k_pages: torch.Tensor, v_pages: torch.Tensor, k_scales_pages, v_scales_pages) -> bool:
+    """Validate float8 pages with per-token scales (the k_scales_pages /
+    v_scales_pages arguments of the reference kernels, decode...:206-217 and
+    prefill...:255-266); returns whether the pages are quantized."""
+    if k_scales_pages is None and v_scales_pages is None:
+        return False
+    if k_scales_pages is None or v_scales_pages is None:
+        raise ValueError("k_scales_pages and v_scales_pages must be given together")
+    num_kv_heads, total_num_pages, page_size = k_pages.shape[:3]
+    for name, t in (("k_scales_pages", k_scales_pages), ("v_scales_pages", v_scales_pages)):
+        if tuple(t.shape) != (num_kv_heads, total_num_pages, page_size):
+            raise ValueError(f"{name} must have shape {(num_kv_heads, total_num_pages, page_size)}, "
+                             f"got {tuple(t.shape)}")
+        if t.dtype != torch.float32:
+            raise ValueError(f"{name} must be float32, got {t.dtype}")
+        if t.stride(2) != 1:
+            raise ValueError(f"{name} must be contiguous over the slots of a page")
+    if tuple(k_scales_pages.stride()) != tuple(v_scales_pages.stride()):
+        raise ValueError("k_scales_pages and v_scales_pages must share strides")
+    for name, t in (("k_pages", k_pages), ("v_pages", v_pages)):
+        if t.dtype not in (torch.float8_e4m3fn, torch.uint8):
+            raise ValueError(f"{name} of quantized pages must be float8_e4m3fn (or its uint8 codes), got {t.dtype}")
+        if t.stride(-1) != 1:
+            raise ValueError(f"{name} must be contiguous in its last dimension")
+    require_device("k_scales_pages", k_scales_pages)
+    require_device("v_scales_pages", v_scales_pages)
+    return True

@@ -19,8 +19,8 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from ._common import (DEFAULT_MASK_VALUE, as_i32, pages_strides, require_bf16, require_device,
-                      stream_handle)
+from ._common import (DEFAULT_MASK_VALUE, as_i32, check_quantized_pages, pages_strides, require_bf16,
+                      require_device, stream_handle)
 
 
 def decode_workspace_bytes(batch: int, num_heads: int, head_dim: int, pages_per_seq: int,
@@ -77,29 +77,7 @@ def decode_paged_attention(
             raise ValueError(f"The dtype of `lengths` must be int32. Got {lengths.dtype}")
     if block_h % 16:
         raise ValueError(f"block_h must divisible by 16, but is {block_h}.")
-    quantized = k_scales_pages is not None or v_scales_pages is not None
-    if quantized:
-        if k_scales_pages is None or v_scales_pages is None:
-            raise ValueError("k_scales_pages and v_scales_pages must be given together")
-        for name, t in (("k_scales_pages", k_scales_pages), ("v_scales_pages", v_scales_pages)):
-            # decode...:206-217
-            if tuple(t.shape) != (num_kv_heads, total_num_pages, page_size):
-                raise ValueError(f"{name} must have shape {(num_kv_heads, total_num_pages, page_size)}, "
-                                 f"got {tuple(t.shape)}")
-            if t.dtype != torch.float32:
-                raise ValueError(f"{name} must be float32, got {t.dtype}")
-            if t.stride(2) != 1:
-                raise ValueError(f"{name} must be contiguous over the slots of a page")
-        if tuple(k_scales_pages.stride()) != tuple(v_scales_pages.stride()):
-            raise ValueError("k_scales_pages and v_scales_pages must share strides")
-        for name, t in (("k_pages", k_pages), ("v_pages", v_pages)):
-            if t.dtype not in (torch.float8_e4m3fn, torch.uint8):
-                raise ValueError(f"{name} of quantized pages must be float8_e4m3fn (or its uint8 codes), "
-                                 f"got {t.dtype}")
-            if t.stride(-1) != 1:
-                raise ValueError(f"{name} must be contiguous in its last dimension")
-        require_device("k_scales_pages", k_scales_pages)
-        require_device("v_scales_pages", v_scales_pages)
+    quantized = check_quantized_pages(k_pages, v_pages, k_scales_pages, v_scales_pages)
 
     for name, t in (("q", q), ("k_pages", k_pages), ("v_pages", v_pages), ("block_tables", block_tables)):
         require_device(name, t)

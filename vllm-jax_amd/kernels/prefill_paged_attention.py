@@ -19,7 +19,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from ._common import (DEFAULT_MASK_VALUE, as_i32, inv_sqrt_head_dim_bf16, pages_strides,
+from ._common import (DEFAULT_MASK_VALUE, as_i32, check_quantized_pages, inv_sqrt_head_dim_bf16, pages_strides,
                       require_bf16, require_device, stream_handle)
 
 
@@ -48,6 +48,7 @@ def prefill_paged_attention(
         cu_seqlens_k: torch.Tensor | None = None,
         scale: float | None = None,
         out: torch.Tensor | None = None,
+        workspace: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Paged prefill attention; returns ``[T, H, d]`` bf16.
 
@@ -56,15 +57,15 @@ def prefill_paged_attention(
       * ``cu_seqlens_k`` -- per-sequence kv lengths including a cached prefix;
         kv index j then sits at position ``j + pos0 - (Lk - Lq)``;
       * ``scale`` -- logit scale (default: bf16(1/sqrt(d)) as prefill...:60);
-      * ``out`` -- preallocated output.
+      * ``out`` -- preallocated output;
+      * ``workspace`` -- for quantized pages (float8 e4m3fn codes with float32
+        ``[Hkv, NB, BS]`` per-token scales): device bytes for the pages widened
+        to bf16 (``pa_prefill_fp8_workspace_size``); allocated when absent.
     """
     del slot_mapping, block_m, pages_per_compute_block, k_splits, num_warps, num_stages
     del interpret, debug, mask_value
     if block_h % 16:
         raise ValueError(f"block_h must divisible by 16, but is {block_h}.")
-    if k_scales_pages is not None or v_scales_pages is not None:
-        raise NotImplementedError("quantized KV pages (k_scales_pages / v_scales_pages) are not supported")
-
     total_tokens, num_heads, head_dim = q.shape
     num_kv_heads, total_num_pages, page_size, head_dim_k = k_pages.shape
     batch, pages_per_sequence = block_tables.shape
@@ -87,12 +88,14 @@ def prefill_paged_attention(
     if cu_seqlens_k is not None and tuple(cu_seqlens_k.shape) != (batch + 1,):
         raise ValueError("cu_seqlens_k must have shape [batch + 1]")
 
+    quantized = check_quantized_pages(k_pages, v_pages, k_scales_pages, v_scales_pages)
     for name, t in (("q", q), ("k_pages", k_pages), ("v_pages", v_pages), ("block_tables", block_tables),
                     ("cu_seqlens", cu_seqlens), ("input_positions", input_positions)):
         require_device(name, t)
     require_bf16("q", q)
-    require_bf16("k_pages", k_pages)
-    require_bf16("v_pages", v_pages)
+    if not quantized:
+        require_bf16("k_pages", k_pages)
+        require_bf16("v_pages", v_pages)
     if tuple(k_pages.stride()) != tuple(v_pages.stride()):
         raise ValueError("k_pages and v_pages must share strides")
     bt = block_tables if block_tables.stride(-1) == 1 else block_tables.contiguous()
@@ -110,6 +113,26 @@ def prefill_paged_attention(
         scale = inv_sqrt_head_dim_bf16(head_dim)
     soft_cap = 0.0 if attn_logits_soft_cap is None else float(attn_logits_soft_cap)
     ps, ss, hs = pages_strides(k_pages)
+    if quantized:
+        need = int(_lib.load().pa_prefill_fp8_workspace_size(batch, pages_per_sequence, page_size, num_kv_heads,
+                                                              head_dim))
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+        _lib.call(
+            "pa_prefill_fp8",
+            q.data_ptr(), q.stride(0), q.stride(1),
+            k_pages.data_ptr(), v_pages.data_ptr(), k_scales_pages.data_ptr(), v_scales_pages.data_ptr(),
+            total_num_pages, page_size, ps, ss, hs,
+            k_scales_pages.stride(1), k_scales_pages.stride(0),
+            bt.data_ptr(), bt.stride(0), pages_per_sequence,
+            cu.data_ptr(), cuk.data_ptr() if cuk is not None else None, pos.data_ptr(),
+            batch, total_tokens, int(max_seqlen_bucket),
+            num_heads, num_kv_heads, head_dim,
+            float(scale), soft_cap,
+            out.data_ptr(), out.stride(0), out.stride(1),
+            workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+            stream_handle(q))
+        return out
     _lib.call(
         "pa_prefill",
         q.data_ptr(), q.stride(0), q.stride(1),
