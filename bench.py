@@ -10,6 +10,9 @@ workload, inputs resident in HBM:
 * Qwen3-8B decode (256 sequences, ctx ~ U[512, 8192], 32 q / 8 kv heads,
   16384-page pool, seed 2): KV store of the new token + split-K decode.
   Reported under ``"decode"`` in GB/s of algorithmic HBM traffic.
+* The Qwen3-8B prefix-cached prefill (64 sequences, cached prefixes
+  U[0, 4096] in shared blocks, new chunks U[128, 1024], 32 q / 8 kv heads,
+  seed 3): reported under ``"prefix_prefill"`` in TFLOP/s.
 * The Qwen3-8B decode over float8 e4m3 pages with per-token scales (the same
   pool quantised on the device): reported under ``"decode_fp8"`` in GB/s of
   its own algorithmic bytes (codes + scales), with the bf16 decode time of
@@ -93,8 +96,8 @@ def run_gpu(args):
 
     # ---------------- prefill: Qwen3-32B long context
     pb = wl.qwen3_32b_long_prefill(seed=4)
-    pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False) if args.only not in ("decode", "mixed") \
-        else None
+    pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False) \
+        if args.only not in ("decode", "mixed", "decode_fp8", "prefix") else None
     if pt is None:  # decode-only profiling run: keep the prefill half tiny
         pb = wl.make_prefill([64], num_heads=64, num_kv_heads=8, rng=np.random.default_rng(0))
         pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False)
@@ -111,7 +114,7 @@ def run_gpu(args):
                                     max_seqlen_bucket=pb.max_seqlen_bucket, out=out_p)
 
     # ---------------- decode: Qwen3-8B
-    db = wl.qwen3_8b_decode(seed=2) if args.only not in ("prefill", "rope", "mixed") else \
+    db = wl.qwen3_8b_decode(seed=2) if args.only not in ("prefill", "rope", "mixed", "prefix") else \
         wl.make_decode([64], num_heads=32, num_kv_heads=8, rng=np.random.default_rng(0))
     dt_ = wl.materialize_decode(db, seed=2, device=dev)
     kv_d = dt_["kv_cache"]
@@ -134,6 +137,7 @@ def run_gpu(args):
     run_r = args.only in (None, "rope")
     run_m = args.only in (None, "mixed")
     run_f = args.only in (None, "decode_fp8")
+    run_x = args.only in (None, "prefix")
     nop = lambda: None
     if not run_p:
         prefill_step = prefill_attn = nop
@@ -175,6 +179,7 @@ def run_gpu(args):
 
     rope = run_rope(args, torch, pkg, pb, pt, kv_p) if run_r else None
     mixed = run_mixed(args, torch, pkg, wl, dev) if run_m else None
+    prefix = run_prefix(args, torch, pkg, wl, dev) if run_x else None
     dec8 = run_decode_fp8(args, torch, pkg, db, dt_, ws, dscale, float(d_attn.mean()) if run_d else None) \
         if run_f else None
 
@@ -244,6 +249,8 @@ def run_gpu(args):
         res["qk_norm_rope"] = rope
     if mixed is not None:
         res["mixed"] = mixed
+    if prefix is not None:
+        res["prefix_prefill"] = prefix
     if dec8 is not None:
         dec8["roofline"]["traffic"] = traffic.get("decode_fp8_split_kernel")
         res["decode_fp8"] = dec8
@@ -290,6 +297,45 @@ def run_decode_fp8(args, torch, pkg, db, dt_, ws, dscale, bf16_ms):
         "roofline": {"kernel": "decode_split_kernel<true, false, true> + decode_merge_kernel", "bound": "hbm",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+
+
+def run_prefix(args, torch, pkg, wl, dev):
+    """Time the Qwen3-8B prefix-cached prefill: new tokens stored, then the
+    causal prefill over cached + new K/V."""
+    pb = wl.qwen3_8b_prefix_prefill(seed=3)
+    t = wl.materialize_prefill(pb, seed=3, device=dev, fill_pool=True)
+    kv = t["kv_cache"]
+    kp, vp = kv[0].permute(2, 0, 1, 3), kv[1].permute(2, 0, 1, 3)
+    out = torch.empty_like(t["q"])
+
+    def store():
+        pkg.update_kv_cache(kv, t["slot_mapping"], t["k"], t["v"])
+
+    def attn():
+        pkg.prefill_paged_attention(t["q"], kp, vp, t["block_tables"], t["cu_seqlens_q"], t["slot_mapping"],
+                                    t["input_positions"], max_seqlen_bucket=pb.max_seqlen_bucket,
+                                    cu_seqlens_k=t["cu_seqlens_k"], out=out)
+
+    for _ in range(args.warmup):
+        store(); attn()
+    torch.cuda.synchronize()
+    n = max(args.steps, 10)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+           torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for e in ev:
+        e[0].record(); store(); e[1].record(); attn(); e[2].record()
+    torch.cuda.synchronize()
+    st = float(np.mean([e[0].elapsed_time(e[1]) for e in ev]))
+    at = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
+    flops = pb.flops()
+    tf = flops / (at * 1e-3) / 1e12
+    return {
+        "metric": "prefix-cached prefill attn TFLOP/s",
+        "seqs": int(pb.batch), "new_tokens": int(pb.num_tokens),
+        "cached_tokens": int(pb.prefix_lens.sum()), "algorithmic_tflop": round(flops / 1e12, 4),
+        "kv_store_ms": round(st, 4), "attn_ms": round(at, 4),
+        "attn_tflops": round(tf, 2), "frac_of_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
     }
 
 
@@ -460,7 +506,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU oracle work (total)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "rope", "mixed", "decode_fp8", "copy"], default=None,
+    ap.add_argument("--only", choices=["prefill", "decode", "rope", "mixed", "decode_fp8", "prefix", "copy"],
+                    default=None,
                     help="profiling aid: run one kernel family only (the JSON line then covers that part)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

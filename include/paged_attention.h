@@ -122,6 +122,10 @@ int pa_decode(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
  * Replaces prefill_paged_attention (prefill_paged_attention.py:407-453),
  * which scales q by 1/sqrt(d) itself (prefill_paged_attention.py:60).
  * q/out: [num_tokens, H, d] with (tok, head) strides.
+ * workspace (256-byte aligned, pa_prefill_workspace_size bytes, or NULL)
+ * holds a work list that orders the (q tile, sequence, kv head) items by
+ * their kv length, longest first; it changes no result.  Without it (or for
+ * batch > 2048) items run from the last q tile down.
  */
 int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
                const uint16_t* k_cache, const uint16_t* v_cache,
@@ -134,7 +138,12 @@ int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
                int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                float scale, float soft_cap,
                uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
-               void* stream);
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes of pa_prefill's work list (0 for bad sizes); no
+ * counterpart in the reference, whose grid order is fixed. */
+size_t pa_prefill_workspace_size(int32_t batch, int32_t max_seqlen_q, int32_t num_heads,
+                                 int32_t num_kv_heads);
 
 /*
  * The layer step between the q/k/v projections and attention, fused:
@@ -207,9 +216,10 @@ int pa_decode_fp8(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stri
                   void* workspace, size_t workspace_bytes, void* stream);
 
 /* Workspace bytes pa_prefill_fp8 needs: two bf16 pages per block-table
- * entry (K and V) plus one int32 per entry. */
+ * entry (K and V), one int32 per entry, then pa_prefill's work list. */
 size_t pa_prefill_fp8_workspace_size(int32_t batch, int32_t pages_per_seq, int32_t page_size,
-                                     int32_t num_kv_heads, int32_t head_dim);
+                                     int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_q,
+                                     int32_t num_heads);
 
 /*
  * pa_prefill over float8 e4m3fn pages with per-token scales

@@ -41,7 +41,7 @@ def test_error_codes_match_header():
 
 
 def test_abi_version():
-    assert PKG._lib.load().pa_abi_version() == 1
+    assert PKG._lib.load().pa_abi_version() == PKG._lib.ABI_VERSION == 2
 
 
 def _decode_args(**over):
@@ -68,7 +68,7 @@ def test_decode_rejects_bad_arguments_without_a_device():
 def test_prefill_rejects_bad_arguments_without_a_device():
     lib = PKG._lib.load()
     args = [None, 2048, 128, None, None, 16, 256, 262144, 1024, 128, None, 4, 4, None, None, None,
-            2, 100, 64, 16, 8, 128, 0.088, 0.0, None, 2048, 128, None]
+            2, 100, 64, 16, 8, 128, 0.088, 0.0, None, 2048, 128, None, 0, None]
     bad_div = list(args)
     bad_div[19] = 15
     assert lib.pa_prefill(*bad_div) == -1
@@ -81,6 +81,32 @@ def test_prefill_rejects_bad_arguments_without_a_device():
     nulls = list(args)  # valid sizes but null pointers
     assert lib.pa_prefill(*nulls) == -1
     assert "null" in lib.pa_last_error().decode()
+    # Non-null (never dereferenced) pointers: the work-list checks come first.
+    fake = list(args)
+    for i in (0, 3, 4, 10, 13, 15, 24):
+        fake[i] = 1 << 20
+    need = lib.pa_prefill_workspace_size(2, 64, 16, 8)
+    small = list(fake)
+    small[27], small[28] = 1 << 20, need - 1
+    assert lib.pa_prefill(*small) == -3
+    assert "workspace" in lib.pa_last_error().decode()
+    misaligned = list(fake)
+    misaligned[27], misaligned[28] = (1 << 20) + 16, need
+    assert lib.pa_prefill(*misaligned) == -3
+
+
+def test_prefill_workspace_size():
+    lib = PKG._lib.load()
+    # G = 2: 128-token q tiles; 2 sequences x ceil(300 / 128) = 6 pairs; a
+    # 256-byte header, then a 32-byte record per pair
+    assert lib.pa_prefill_workspace_size(2, 300, 16, 8) == 256 + 32 * 6
+    # G = 8: 32-token q tiles
+    assert lib.pa_prefill_workspace_size(64, 1024, 64, 8) == 256 + 32 * 64 * 32
+    assert lib.pa_prefill_workspace_size(0, 1024, 64, 8) == 256
+    assert lib.pa_prefill_workspace_size(2, 300, 15, 8) == 0   # heads not a multiple of kv heads
+    fp8 = lib.pa_prefill_fp8_workspace_size(2, 4, 256, 8, 128, 300, 16)
+    widened = 2 * 8 * 256 * 8 * 128 * 2 + 8 * 4
+    assert fp8 == (widened + 255) // 256 * 256 + 256 + 32 * 6
 
 
 def test_kv_store_edge_arguments_without_a_device():

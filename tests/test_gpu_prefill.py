@@ -134,3 +134,88 @@ def test_prefill_many_sequences(pkg, dev):
     pb = wl.make_prefill(lens, num_heads=16, num_kv_heads=8, page_size=64, rng=rng)
     rows = np.unique(np.concatenate([pb.cu_seqlens_q[1:] - 1, rng.integers(0, pb.num_tokens, 64)]))
     _prefill(pkg, dev, pb, seed=22, rows=rows)
+
+
+def _raw_prefill(pkg, t, pb, workspace, max_seqlen=None):
+    """pa_prefill through the C ABI, with a caller workspace or none."""
+    import torch
+    kv = t["kv_cache"]
+    kp, vp = kv[0].permute(2, 0, 1, 3), kv[1].permute(2, 0, 1, 3)
+    hs, ps, ss, _ = kp.stride()
+    q, bt = t["q"], t["block_tables"]
+    out = torch.full_like(q, 7.0)
+    cuk = t["cu_seqlens_k"]
+    ws = (None, 0) if workspace is None else (workspace.data_ptr(), workspace.numel())
+    pkg._lib.call("pa_prefill", q.data_ptr(), q.stride(0), q.stride(1), kp.data_ptr(), vp.data_ptr(), pb.num_pages,
+                  pb.page_size, ps, ss, hs, bt.data_ptr(), bt.stride(0), bt.shape[1], t["cu_seqlens_q"].data_ptr(),
+                  cuk.data_ptr() if cuk is not None else None, t["input_positions"].data_ptr(), pb.batch,
+                  q.shape[0], int(max_seqlen or pb.max_seqlen_bucket), pb.num_heads, pb.num_kv_heads, 128,
+                  0.08837890625, 0.0, out.data_ptr(), out.stride(0), out.stride(1), *ws,
+                  torch.cuda.current_stream().cuda_stream)
+    return out
+
+
+def _expected_list(pb, num_tokens, max_seqlen):
+    """Per (sequence, q tile) pair with rows: its geometry and kv-tile cost
+    (contiguous-position estimate), as the work list must hold them."""
+    g = pb.num_heads // pb.num_kv_heads
+    tt = 256 // g
+    nq = -(-max_seqlen // tt)
+    cu = pb.cu_seqlens_q.astype(np.int64)
+    cuk = pb.cu_seqlens_k if pb.cu_seqlens_k is not None else cu
+    span = pb.block_tables.shape[1] * pb.page_size
+    want = {}
+    for b in range(pb.batch):
+        q0, lq = int(cu[b]), int(cu[b + 1] - cu[b])
+        rows = 0 if (q0 < 0 or q0 >= num_tokens) else min(lq, max_seqlen, num_tokens - q0)
+        lk = min(int(cuk[b + 1] - cuk[b]), span)
+        for qt in range(nq):
+            if qt * tt >= rows:
+                continue
+            off = int(pb.input_positions[q0]) - (lk - lq)
+            hi = min(lk, lk - lq + min(qt * tt + tt, rows))
+            cost = min((-(-hi // 64) if hi > 0 else 0) + 1, 4095)
+            want[(b, qt)] = (q0, rows, lk, off, cost)
+    return want
+
+
+@pytest.mark.parametrize("case", ["prefix", "many", "padded"])
+def test_prefill_work_list(pkg, dev, case):
+    """The work list (caller workspace) holds every (sequence, q tile) pair
+    with rows once, with its geometry, in non-increasing cost; and the
+    output with the list is bit-identical to the grid-order output without."""
+    import torch
+    if case == "prefix":
+        pb = wl.make_prefix_prefill([0, 300, 512, 40, 1500, 3], [130, 64, 200, 1, 700, 260], num_heads=32,
+                                    num_kv_heads=8, rng=np.random.default_rng(7), shared_prefix_tokens=1600)
+    elif case == "many":
+        rng = np.random.default_rng(23)
+        pb = wl.make_prefill(rng.integers(1, 300, 90).tolist(), num_heads=16, num_kv_heads=8, page_size=64, rng=rng)
+    else:
+        pb = wl.make_prefill([100, 23, 7], num_heads=16, num_kv_heads=8, page_size=16, num_pages=20,
+                             rng=np.random.default_rng(3), pad_tokens_to=256, pad_batch_to=4)
+    t = wl.materialize_prefill(pb, 11, dev)
+    pkg.update_kv_cache(t["kv_cache"], t["slot_mapping"], t["k"], t["v"])
+    need = pkg._lib.load().pa_prefill_workspace_size(pb.batch, pb.max_seqlen_bucket, pb.num_heads,
+                                                     pb.num_kv_heads)
+    ws = torch.full((need,), 0xAB, dtype=torch.uint8, device=dev)
+    print(f"case {case}: batch {pb.batch} tokens {pb.num_tokens} workspace {need} B", flush=True)
+    got = _raw_prefill(pkg, t, pb, ws)
+    base = _raw_prefill(pkg, t, pb, None)
+    torch.cuda.synchronize()
+    assert np.array_equal(u16(got), u16(base)), "work-list order changed the output"
+    plan = ws.view(torch.int32).cpu().numpy()
+    want = _expected_list(pb, t["q"].shape[0], pb.max_seqlen_bucket)
+    count = int(plan[0])
+    assert count == len(want)
+    rec = plan[64:64 + 8 * count].reshape(count, 8)
+    seen = set()
+    costs = []
+    for r in rec:
+        key = (int(r[0]), int(r[1]))
+        assert key in want and key not in seen, key
+        seen.add(key)
+        q0, rows, lk, off, cost = want[key]
+        assert tuple(int(x) for x in r[2:6]) == (q0, rows, lk, off), (key, r)
+        costs.append(cost)
+    assert all(a >= b for a, b in zip(costs, costs[1:])), "work list not in non-increasing cost"

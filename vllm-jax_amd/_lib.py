@@ -13,13 +13,14 @@ from . import build as _build
 
 _LOCK = threading.Lock()
 _LIB = None
+ABI_VERSION = 2  # pa_abi_version() of a library these bindings fit
 
 c_i32, c_i64, c_f32, c_sz, c_vp = ctypes.c_int32, ctypes.c_int64, ctypes.c_float, ctypes.c_size_t, ctypes.c_void_p
 
 # name -> (restype, argtypes)
 SIGNATURES = {
     "pa_last_error": (ctypes.c_char_p, []),
-    "pa_abi_version": (ctypes.c_int, []),
+    "pa_abi_version": (ctypes.c_int, []),  # must equal ABI_VERSION
     "pa_kv_store": (ctypes.c_int, [
         c_vp, c_i64, c_i64,            # k, k_tok_stride, k_head_stride
         c_vp, c_i64, c_i64,            # v, ...
@@ -58,8 +59,10 @@ SIGNATURES = {
         c_i32, c_i32, c_i32,           # heads, kv heads, head_dim
         c_f32, c_f32,                  # scale, soft_cap
         c_vp, c_i64, c_i64,            # out
+        c_vp, c_sz,                    # workspace (work list, may be NULL), bytes
         c_vp,                          # stream
     ]),
+    "pa_prefill_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32]),
     "pa_qk_norm_rope_store": (ctypes.c_int, [
         c_vp, c_i64, c_i64,            # q
         c_vp, c_i64, c_i64,            # k
@@ -97,7 +100,7 @@ SIGNATURES = {
         c_vp, c_i64, c_i64,            # out
         c_vp, c_sz, c_vp,              # workspace, bytes, stream
     ]),
-    "pa_prefill_fp8_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "pa_prefill_fp8_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_i32]),
     "pa_prefill_fp8": (ctypes.c_int, [
         c_vp, c_i64, c_i64,            # q
         c_vp, c_vp, c_vp, c_vp,        # k/v codes, k/v scales
@@ -180,6 +183,9 @@ def load():
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
+        if lib.pa_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{path} has ABI version {lib.pa_abi_version()}, these bindings expect "
+                               f"{ABI_VERSION}: rebuild the library")
         _LIB = lib
     return _LIB
 

@@ -19,4 +19,4 @@ void clear_error() { g_last_error[0] = '\0'; }
 
 extern "C" const char* pa_last_error(void) { return pa::g_last_error; }
 
-extern "C" int pa_abi_version(void) { return 1; }
+extern "C" int pa_abi_version(void) { return 2; }

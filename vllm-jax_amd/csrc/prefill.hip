@@ -13,20 +13,111 @@ prefill_kernel(PrefillParams p) {
   prefill_body<kSoftCap, kAligned>(p, blockIdx.x);
 }
 
-// Zero every output row the prefill kernel does not write: rows outside all
-// sequences (before cu_q[0], from cu_q[batch] on) and rows at offset >=
-// max_seqlen_q inside their sequence (the reference drops those too: its
-// scatter only covers the first max_seqlen_bucket rows, prefill...:384-388).
-// One wave per token row.
-__global__ void __launch_bounds__(256)
-prefill_zero_rows_kernel(const int32_t* __restrict__ cu_q, int32_t batch, int32_t num_tokens,
-                         int32_t max_seqlen_q, int32_t num_heads, uint16_t* __restrict__ out,
-                         int64_t o_ts, int64_t o_hs) {
+constexpr int kPrepThreads = 1024;
+constexpr int kPlanBins = 4096;       // cost classes of the work list (kv tiles + 1, clamped)
+constexpr int kPlanMaxBatch = 2048;   // sequences whose geometry the planner keeps in LDS
+
+// Work list of the prefill (run by one workgroup).  A pair (sequence b,
+// q tile qt) is listed when the tile has rows; its cost is the number of kv
+// tiles its last row sees, estimated as if positions were contiguous (the
+// list orders the work and changes no result).  Pairs are counting-sorted by
+// cost, largest first, so the longest items start first and no long item is
+// left for the end.  Per sequence, q0 / lq_rows / lk / kv_pos_off are derived
+// exactly as prefill_body derives them without a list.
+__device__ void prefill_plan(const PrefillParams& p, int32_t* __restrict__ plan) {
+  __shared__ int32_t hist[kPlanBins];
+  __shared__ int4 seqs[kPlanMaxBatch];  // q0, lq_rows, lk, kv_pos_off
+  __shared__ int32_t lag[kPlanMaxBatch];  // lk - lq
+  __shared__ int32_t scan[kPrepThreads];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kPlanBins; i += kPrepThreads) hist[i] = 0;
+  for (int b = tid; b < p.batch; b += kPrepThreads) {
+    const int q0 = p.cu_q[b];
+    const int lq = p.cu_q[b + 1] - q0;
+    const int lq_rows = (q0 < 0 || q0 >= p.num_tokens) ? 0 : min(min(lq, p.max_seqlen_q), p.num_tokens - q0);
+    const int lk = min(p.kv_lens ? p.kv_lens[b] : (p.cu_k ? p.cu_k[b + 1] - p.cu_k[b] : lq),
+                       p.pages_per_seq * p.page_size);
+    const int off = lq_rows > 0 ? p.positions[q0] - (lk - lq) : 0;
+    seqs[b] = make_int4(q0, lq_rows, lk, off);
+    lag[b] = lk - lq;
+  }
+  __syncthreads();
+  const int nq = p.n_qtiles, T = p.tile_tokens;
+  const int pairs = p.batch * nq;
+  // cost bin of pair i (0: no rows)
+  auto bin_of = [&](int i) -> int {
+    const int b = i / nq, qt = i - b * nq;
+    const int rows = seqs[b].y;
+    if (qt * T >= rows) return 0;
+    const int64_t kv_hi = min((int64_t)seqs[b].z, (int64_t)lag[b] + min(qt * T + T, rows));
+    const int64_t tiles = kv_hi <= 0 ? 0 : (kv_hi + kTileN - 1) / kTileN;
+    return (int)min<int64_t>(tiles + 1, kPlanBins - 1);
+  };
+  for (int i = tid; i < pairs; i += kPrepThreads) {
+    const int c = bin_of(i);
+    if (c) atomicAdd(&hist[c], 1);
+  }
+  __syncthreads();
+  // thread t owns bins kPlanBins-1-4t .. kPlanBins-4-4t (largest first)
+  constexpr int kPer = kPlanBins / kPrepThreads;
+  int cnt[kPer], local = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    cnt[j] = hist[kPlanBins - 1 - (kPer * tid + j)];
+    local += cnt[j];
+  }
+  scan[tid] = local;
+  for (int o = 1; o < kPrepThreads; o <<= 1) {
+    __syncthreads();
+    const int v = tid >= o ? scan[tid - o] : 0;
+    __syncthreads();
+    scan[tid] += v;
+  }
+  __syncthreads();
+  int run = scan[tid] - local;  // pairs in larger bins
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    hist[kPlanBins - 1 - (kPer * tid + j)] = run;  // first rank of the bin
+    run += cnt[j];
+  }
+  const int count = scan[kPrepThreads - 1];
+  __syncthreads();
+  for (int i = tid; i < pairs; i += kPrepThreads) {
+    const int c = bin_of(i);
+    if (!c) continue;
+    const int rank = atomicAdd(&hist[c], 1);
+    const int b = i / nq;
+    const int4 sq = seqs[b];
+    int32_t* r = plan + kPlanHeader + 8 * rank;
+    st16(r, u32x4{(uint32_t)b, (uint32_t)(i - b * nq), (uint32_t)sq.x, (uint32_t)sq.y});
+    st16(r + 4, u32x4{(uint32_t)sq.z, (uint32_t)sq.w, 0u, 0u});
+  }
+  if (tid == 0) plan[0] = count;
+}
+
+// Before the prefill: workgroup 0 builds the work list (when `plan` is
+// given); the others zero every output row the prefill kernel does not write:
+// rows outside all sequences (before cu_q[0], from cu_q[batch] on) and rows
+// at offset >= max_seqlen_q inside their sequence (the reference drops those
+// too: its scatter only covers the first max_seqlen_bucket rows,
+// prefill...:384-388).  One wave per token row.
+__global__ void __launch_bounds__(kPrepThreads)
+prefill_prep_kernel(PrefillParams p, int32_t* __restrict__ plan) {
+  int zb = blockIdx.x;
+  if (plan) {
+    if (zb == 0) {
+      prefill_plan(p, plan);
+      return;
+    }
+    --zb;
+  }
   const int lane = threadIdx.x & 63;
-  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= num_tokens) return;
+  const int64_t t = (int64_t)zb * (kPrepThreads / 64) + (threadIdx.x >> 6);
+  if (t >= p.num_tokens) return;
+  const int32_t* cu_q = p.cu_q;
+  const int batch = p.batch;
   bool covered = false;
-  if (t >= cu_q[0] && t < cu_q[batch]) {
+  if (batch > 0 && t >= cu_q[0] && t < cu_q[batch]) {
     // last b with cu_q[b] <= t
     int lo = 0, hi = batch;  // invariant: cu_q[lo] <= t < cu_q[hi]
     while (hi - lo > 1) {
@@ -34,14 +125,14 @@ prefill_zero_rows_kernel(const int32_t* __restrict__ cu_q, int32_t batch, int32_
       if (cu_q[mid] <= t) lo = mid;
       else hi = mid;
     }
-    covered = t - cu_q[lo] < max_seqlen_q;
+    covered = t - cu_q[lo] < p.max_seqlen_q;
   }
   if (covered) return;
   const int chunks_per_head = kPHeadDim / 8;
-  for (int c = lane; c < num_heads * chunks_per_head; c += 64) {
+  for (int c = lane; c < p.num_heads * chunks_per_head; c += 64) {
     const int hh = c / chunks_per_head;
     const int e = (c - hh * chunks_per_head) * 8;
-    st16(out + t * o_ts + hh * o_hs + e, u32x4{0, 0, 0, 0});
+    st16(p.out + t * p.o_ts + hh * p.o_hs + e, u32x4{0, 0, 0, 0});
   }
 }
 
@@ -108,7 +199,8 @@ static int prefill_launch(const char* name, const uint16_t* q, int64_t q_tok_str
                           const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
                           const int32_t* input_positions, int32_t batch, int32_t num_tokens, int32_t max_seqlen_q,
                           int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale, float soft_cap,
-                          uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride, void* stream) {
+                          uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride, void* workspace,
+                          size_t workspace_bytes, void* stream) {
   if (batch < 0 || num_tokens < 0 || max_seqlen_q < 0 || num_heads <= 0 || num_kv_heads <= 0 ||
       num_pages <= 0 || page_size <= 0 || pages_per_seq < 0)
     return fail(PA_ERR_INVALID_ARGUMENT,
@@ -132,17 +224,15 @@ static int prefill_launch(const char* name, const uint16_t* q, int64_t q_tok_str
   if ((align_bits & 15u) || (q_tok_stride | q_head_stride | page_stride | slot_stride | head_stride |
                              out_tok_stride | out_head_stride) % 8)
     return fail(PA_ERR_UNSUPPORTED, "%s: operands must be 16-byte aligned with strides multiple of 8", name);
+  if (workspace) {
+    const size_t need = pa_prefill_workspace_size(batch, max_seqlen_q, num_heads, num_kv_heads);
+    if (workspace_bytes < need || ((uintptr_t)workspace & 255u))
+      return fail(PA_ERR_WORKSPACE, "%s: 256-byte aligned workspace of %zu bytes needed, %zu given", name, need,
+                  workspace_bytes);
+  }
   hipStream_t s = (hipStream_t)stream;
 
-  {
-    prefill_zero_rows_kernel<<<dim3((unsigned)((num_tokens + 3) / 4)), dim3(256), 0, s>>>(
-        cu_seqlens_q, batch, num_tokens, max_seqlen_q, num_heads, out, out_tok_stride, out_head_stride);
-    int rc = launch_status(name);
-    if (rc) return rc;
-  }
-  if (batch == 0 || max_seqlen_q == 0) return PA_OK;
-
-  PrefillParams prm;
+  PrefillParams prm{};
   prm.q = q;
   prm.q_ts = q_tok_stride;
   prm.q_hs = q_head_stride;
@@ -173,9 +263,21 @@ static int prefill_launch(const char* name, const uint16_t* q, int64_t q_tok_str
   prm.out = out;
   prm.o_ts = out_tok_stride;
   prm.o_hs = out_head_stride;
-  const int64_t blocks = (int64_t)prm.n_qtiles * batch * num_kv_heads;
-  if (blocks > 0x7fffffff)
-    return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)blocks);
+  const int64_t items = (int64_t)prm.n_qtiles * batch * num_kv_heads;
+  if (items > 0x7fffffff)
+    return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)items);
+  // the work list needs every sequence's geometry in the planner's LDS
+  const bool planned = workspace && batch > 0 && max_seqlen_q > 0 && batch <= kPlanMaxBatch;
+  int32_t* plan = planned ? reinterpret_cast<int32_t*>(workspace) : nullptr;
+  {
+    const int64_t zero_blocks = (num_tokens + kPrepThreads / 64 - 1) / (kPrepThreads / 64) + (planned ? 1 : 0);
+    prefill_prep_kernel<<<dim3((unsigned)zero_blocks), dim3(kPrepThreads), 0, s>>>(prm, plan);
+    int rc = launch_status(name);
+    if (rc) return rc;
+  }
+  if (batch == 0 || max_seqlen_q == 0) return PA_OK;
+  prm.plan = plan;
+  const int64_t blocks = items;  // with a list, items past its count return at once
   const bool aligned = page_size % kTileN == 0;
   if (prm.soft_cap > 0.f) {
     if (aligned) prefill_kernel<true, true><<<dim3((unsigned)blocks), dim3(kThreads), 0, s>>>(prm);
@@ -185,6 +287,16 @@ static int prefill_launch(const char* name, const uint16_t* q, int64_t q_tok_str
     else prefill_kernel<false, false><<<dim3((unsigned)blocks), dim3(kThreads), 0, s>>>(prm);
   }
   return launch_status(name);
+}
+
+extern "C" size_t pa_prefill_workspace_size(int32_t batch, int32_t max_seqlen_q, int32_t num_heads,
+                                            int32_t num_kv_heads) {
+  if (batch < 0 || max_seqlen_q < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads ||
+      num_heads / num_kv_heads > kRows)
+    return 0;
+  const int64_t tile_tokens = kRows / (num_heads / num_kv_heads);
+  const int64_t pairs = (int64_t)batch * ((max_seqlen_q + tile_tokens - 1) / tile_tokens);
+  return (size_t)(kPlanHeader + 8 * pairs) * sizeof(int32_t);
 }
 
 extern "C" int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
@@ -198,19 +310,30 @@ extern "C" int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_hea
                           int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                           float scale, float soft_cap,
                           uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
-                          void* stream) {
+                          void* workspace, size_t workspace_bytes, void* stream) {
   return prefill_launch("pa_prefill", q, q_tok_stride, q_head_stride, k_cache, v_cache, num_pages, page_size,
                         page_stride, slot_stride, head_stride, block_tables, bt_stride, pages_per_seq, cu_seqlens_q,
                         cu_seqlens_k, input_positions, batch, num_tokens, max_seqlen_q, num_heads, num_kv_heads,
-                        head_dim, scale, soft_cap, out, out_tok_stride, out_head_stride, stream);
+                        head_dim, scale, soft_cap, out, out_tok_stride, out_head_stride, workspace, workspace_bytes,
+                        stream);
+}
+
+// Widened K and V pages, their block table, then (256-byte aligned) the
+// prefill's work list.
+static size_t fp8_widened_bytes(int32_t batch, int32_t pages_per_seq, int32_t page_size, int32_t num_kv_heads,
+                                int32_t head_dim) {
+  const size_t entries = (size_t)batch * pages_per_seq;
+  const size_t page_elems = (size_t)page_size * num_kv_heads * head_dim;
+  return (2 * entries * page_elems * sizeof(uint16_t) + entries * sizeof(int32_t) + 255) / 256 * 256;
 }
 
 extern "C" size_t pa_prefill_fp8_workspace_size(int32_t batch, int32_t pages_per_seq, int32_t page_size,
-                                                int32_t num_kv_heads, int32_t head_dim) {
+                                                int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_q,
+                                                int32_t num_heads) {
   if (batch <= 0 || pages_per_seq <= 0 || page_size <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
-  const size_t entries = (size_t)batch * pages_per_seq;
-  const size_t page_elems = (size_t)page_size * num_kv_heads * head_dim;
-  return 2 * entries * page_elems * sizeof(uint16_t) + entries * sizeof(int32_t);
+  const size_t plan = pa_prefill_workspace_size(batch, max_seqlen_q, num_heads, num_kv_heads);
+  if (!plan) return 0;
+  return fp8_widened_bytes(batch, pages_per_seq, page_size, num_kv_heads, head_dim) + plan;
 }
 
 extern "C" int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
@@ -237,7 +360,7 @@ extern "C" int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q
                           (int64_t)page_size * num_kv_heads * head_dim, (int64_t)num_kv_heads * head_dim, head_dim,
                           block_tables, bt_stride, pages_per_seq, cu_seqlens_q, cu_seqlens_k, input_positions, 0,
                           num_tokens, max_seqlen_q, num_heads, num_kv_heads, head_dim, scale, soft_cap, out,
-                          out_tok_stride, out_head_stride, stream);
+                          out_tok_stride, out_head_stride, nullptr, 0, stream);
   if (!k_cache || !v_cache || !k_scales || !v_scales || !block_tables || !cu_seqlens_q)
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_prefill_fp8: null pointer");
   if (num_kv_heads == 1) {  // a size-1 dimension's stride is arbitrary (and never used)
@@ -247,7 +370,11 @@ extern "C" int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q
   if ((((uintptr_t)k_cache | (uintptr_t)v_cache) & 15u) || (page_stride | slot_stride | head_stride) % 16 ||
       (((uintptr_t)k_scales | (uintptr_t)v_scales) & 3u))
     return fail(PA_ERR_UNSUPPORTED, "pa_prefill_fp8: code rows must be 16-byte aligned");
-  const size_t need = pa_prefill_fp8_workspace_size(batch, pages_per_seq, page_size, num_kv_heads, head_dim);
+  const size_t need = pa_prefill_fp8_workspace_size(batch, pages_per_seq, page_size, num_kv_heads, head_dim,
+                                                    max_seqlen_q, num_heads);
+  if (!need)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_prefill_fp8: bad sizes (max_seqlen_q=%d, num_heads=%d, "
+                "num_kv_heads=%d)", max_seqlen_q, num_heads, num_kv_heads);
   if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u))
     return fail(PA_ERR_WORKSPACE, "pa_prefill_fp8: 256-byte aligned workspace of %zu bytes needed, %zu given", need,
                 workspace_bytes);
@@ -269,5 +396,6 @@ extern "C" int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q
                         page_size, page_elems, (int64_t)num_kv_heads * head_dim, head_dim, bt2, pages_per_seq,
                         pages_per_seq, cu_seqlens_q, cu_seqlens_k, input_positions, batch, num_tokens, max_seqlen_q,
                         num_heads, num_kv_heads, head_dim, scale, soft_cap, out, out_tok_stride, out_head_stride,
-                        stream);
+                        (char*)workspace + fp8_widened_bytes(batch, pages_per_seq, page_size, num_kv_heads, head_dim),
+                        need - fp8_widened_bytes(batch, pages_per_seq, page_size, num_kv_heads, head_dim), stream);
 }

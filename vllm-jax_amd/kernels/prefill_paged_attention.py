@@ -58,9 +58,11 @@ def prefill_paged_attention(
         kv index j then sits at position ``j + pos0 - (Lk - Lq)``;
       * ``scale`` -- logit scale (default: bf16(1/sqrt(d)) as prefill...:60);
       * ``out`` -- preallocated output;
-      * ``workspace`` -- for quantized pages (float8 e4m3fn codes with float32
-        ``[Hkv, NB, BS]`` per-token scales): device bytes for the pages widened
-        to bf16 (``pa_prefill_fp8_workspace_size``); allocated when absent.
+      * ``workspace`` -- device bytes for the work list that orders the
+        kernel's items by kv length (``pa_prefill_workspace_size``) and, for
+        quantized pages (float8 e4m3fn codes with float32 ``[Hkv, NB, BS]``
+        per-token scales), the pages widened to bf16 ahead of it
+        (``pa_prefill_fp8_workspace_size``); allocated when absent or too small.
     """
     del slot_mapping, block_m, pages_per_compute_block, k_splits, num_warps, num_stages
     del interpret, debug, mask_value
@@ -113,11 +115,16 @@ def prefill_paged_attention(
         scale = inv_sqrt_head_dim_bf16(head_dim)
     soft_cap = 0.0 if attn_logits_soft_cap is None else float(attn_logits_soft_cap)
     ps, ss, hs = pages_strides(k_pages)
+    lib = _lib.load()
     if quantized:
-        need = int(_lib.load().pa_prefill_fp8_workspace_size(batch, pages_per_sequence, page_size, num_kv_heads,
-                                                              head_dim))
-        if workspace is None or workspace.numel() * workspace.element_size() < need:
-            workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+        need = int(lib.pa_prefill_fp8_workspace_size(batch, pages_per_sequence, page_size, num_kv_heads, head_dim,
+                                                     int(max_seqlen_bucket), num_heads))
+    else:
+        need = int(lib.pa_prefill_workspace_size(batch, int(max_seqlen_bucket), num_heads, num_kv_heads))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    ws_bytes = workspace.numel() * workspace.element_size()
+    if quantized:
         _lib.call(
             "pa_prefill_fp8",
             q.data_ptr(), q.stride(0), q.stride(1),
@@ -130,7 +137,7 @@ def prefill_paged_attention(
             num_heads, num_kv_heads, head_dim,
             float(scale), soft_cap,
             out.data_ptr(), out.stride(0), out.stride(1),
-            workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+            workspace.data_ptr(), ws_bytes,
             stream_handle(q))
         return out
     _lib.call(
@@ -144,5 +151,6 @@ def prefill_paged_attention(
         num_heads, num_kv_heads, head_dim,
         float(scale), soft_cap,
         out.data_ptr(), out.stride(0), out.stride(1),
+        workspace.data_ptr(), ws_bytes,
         stream_handle(q))
     return out
