@@ -180,6 +180,8 @@ def run_gpu(args):
     rope = run_rope(args, torch, pkg, pb, pt, kv_p) if run_r else None
     mixed = run_mixed(args, torch, pkg, wl, dev) if run_m else None
     prefix = run_prefix(args, torch, pkg, wl, dev) if run_x else None
+    if prefix is not None:
+        prefix["roofline"]["traffic"] = _load_traffic().get("prefill_kernel_prefix_cached")
     dec8 = run_decode_fp8(args, torch, pkg, db, dt_, ws, dscale, float(d_attn.mean()) if run_d else None) \
         if run_f else None
 
@@ -336,6 +338,9 @@ def run_prefix(args, torch, pkg, wl, dev):
         "cached_tokens": int(pb.prefix_lens.sum()), "algorithmic_tflop": round(flops / 1e12, 4),
         "kv_store_ms": round(st, 4), "attn_ms": round(at, 4),
         "attn_tflops": round(tf, 2), "frac_of_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+        "roofline": {"kernel": "prefill_kernel", "bound": "mfma", "achieved": round(tf, 2),
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": None},
     }
 
 
