@@ -83,7 +83,11 @@ int pa_gather_kv(const uint16_t* cache, int32_t num_pages, int32_t page_size,
 
 /*
  * Decode workspace in bytes for a launch of `batch` sequences whose block
- * tables are `pages_per_seq` wide (f32 split partials + their max/sum).
+ * tables are `pages_per_seq` wide: f32 split partials and their max/sum,
+ * then a work list of (sequence, chunk) pairs.  From 2048 workgroups on,
+ * pa_decode orders the pairs by length and deals them over the XCDs (one
+ * extra launch); the output does not depend on the order.  The workspace is
+ * 256-byte aligned.
  */
 size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_dim,
                                 int32_t pages_per_seq, int32_t page_size);

@@ -124,9 +124,13 @@ def test_kv_store_edge_arguments_without_a_device():
 def test_decode_workspace_size():
     lib = PKG._lib.load()
     # 2048-token work items: ceil(32 pages * 256 / 2048) = 4 chunks per sequence
-    assert lib.pa_decode_workspace_size(256, 32, 128, 32, 256) == 256 * 32 * 4 * (128 + 2) * 4
+    r256 = lambda n: (n + 255) // 256 * 256
+    r8 = lambda n: (n + 7) // 8 * 8
+    # partials (256-byte aligned), then a 256-byte header and one int per (sequence, chunk) pair
+    assert lib.pa_decode_workspace_size(256, 32, 128, 32, 256) == r256(256 * 32 * 4 * (128 + 2) * 4) + 256 + 4 * 1024
     # 16-token pages: 1024-token items (64 page ids per chunk), ceil(100 * 16 / 1024) = 2 chunks
-    assert lib.pa_decode_workspace_size(4, 8, 128, 100, 16) == 4 * 8 * 2 * (128 + 2) * 4
+    assert lib.pa_decode_workspace_size(4, 8, 128, 100, 16) == r256(4 * 8 * 2 * (128 + 2) * 4) + 256 + 4 * r8(8)
+    assert lib.pa_decode_workspace_size(3, 8, 128, 100, 16) == r256(3 * 8 * 2 * (128 + 2) * 4) + 256 + 4 * r8(6)
     assert lib.pa_decode_workspace_size(0, 32, 128, 32, 256) == 0
 
 

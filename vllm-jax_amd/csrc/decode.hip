@@ -5,12 +5,79 @@
 
 namespace pa {
 
+constexpr int kPlanThreads = 1024;
+constexpr int kPlanBins = 512;  // cost classes: 16-token steps of the pair + 1, clamped
+
+// Work list of the decode (one workgroup).  Pair (b, c) = chunk c of
+// sequence b is listed when it holds tokens (and chunk 0 of an empty
+// sequence when its zeros are written here); its cost is its number of
+// 16-token steps.  Pairs are counting-sorted by cost, largest first.
+__global__ void __launch_bounds__(kPlanThreads)
+decode_plan_kernel(DecodeParams p, int32_t* __restrict__ plan) {
+  __shared__ int32_t hist[kPlanBins];
+  __shared__ int32_t scan[kPlanThreads];
+  const int tid = threadIdx.x;
+  for (int i = tid; i < kPlanBins; i += kPlanThreads) hist[i] = 0;
+  __syncthreads();
+  const int nc = p.n_chunks;
+  const int pairs = p.batch * nc;
+  const int span = p.pages_per_seq * p.page_size;
+  auto bin_of = [&](int i) -> int {  // 0: not listed
+    const int b = i / nc, c = i - b * nc;
+    const int len = min(p.lengths[b], span);
+    const int t0 = c * p.chunk;
+    if (t0 >= len) return (c == 0 && p.zero_empty) ? 1 : 0;
+    const int steps = (min(len - t0, p.chunk) + kDecodeStep - 1) / kDecodeStep;
+    return min(steps + 1, kPlanBins - 1);
+  };
+  for (int i = tid; i < pairs; i += kPlanThreads) {
+    const int c = bin_of(i);
+    if (c) atomicAdd(&hist[c], 1);
+  }
+  __syncthreads();
+  // thread t < kPlanBins owns bin kPlanBins - 1 - t (largest first)
+  const int local = tid < kPlanBins ? hist[kPlanBins - 1 - tid] : 0;
+  scan[tid] = local;
+  for (int o = 1; o < kPlanThreads; o <<= 1) {
+    __syncthreads();
+    const int v = tid >= o ? scan[tid - o] : 0;
+    __syncthreads();
+    scan[tid] += v;
+  }
+  __syncthreads();
+  if (tid < kPlanBins) hist[kPlanBins - 1 - tid] = scan[tid] - local;  // first rank of the bin
+  const int count = scan[kPlanThreads - 1];
+  __syncthreads();
+  for (int i = tid; i < pairs; i += kPlanThreads) {
+    const int c = bin_of(i);
+    if (c) plan[kDecodePlanHeader + atomicAdd(&hist[c], 1)] = i;
+  }
+  if (tid == 0) plan[0] = count;
+}
+
 template <bool kAligned, bool kSoftCap, bool kFp8 = false>
 __global__ void __launch_bounds__(256, 2)
 decode_split_kernel(DecodeParams p) {
   __shared__ DecodeLds red;
-  decode_item<kDecodeWaves, kAligned, kSoftCap, kFp8>(p, xcd_grouped_item(blockIdx.x, gridDim.x), &red.o[0][0][0],
-                                                      &red.m[0][0], &red.l[0][0]);
+  int item;
+  if (p.plan) {
+    // XCD x = bid % 8 takes ranks x, x + 8, x + 16, ... of the list, all
+    // kv heads of a rank in a row: the XCDs get near-equal token counts,
+    // and the kv heads of a token row (adjacent slices of one pool row) are
+    // read by one XCD at nearly the same time.
+    const int hkv = p.num_kv_heads;
+    const int k = blockIdx.x >> 3;
+    const int kr = k / hkv;
+    const int r = 8 * kr + (blockIdx.x & 7);
+    const __attribute__((address_space(4))) int32_t* pl = (const __attribute__((address_space(4))) int32_t*)p.plan;
+    const int count = pl[0];
+    const int pair = pl[kDecodePlanHeader + r];  // the list has room for every rank of the grid
+    if (r >= count) return;  // uniform over the workgroup
+    item = pair * hkv + (k - kr * hkv);
+  } else {
+    item = xcd_grouped_item(blockIdx.x, gridDim.x);
+  }
+  decode_item<kDecodeWaves, kAligned, kSoftCap, kFp8>(p, item, &red.o[0][0][0], &red.m[0][0], &red.l[0][0]);
 }
 
 // One wave per (sequence, q head): out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M).
@@ -50,6 +117,8 @@ void launch_decode_merge(const DecodeParams& p, hipStream_t s) {
   decode_merge_kernel<<<dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s>>>(p);
 }
 
+constexpr int64_t kDecodePlanMinItems = 2048;  // workgroups from which pa_decode builds a work list
+
 static int decode_chunks(int32_t pages_per_seq, int32_t page_size) {
   const int64_t max_tokens = (int64_t)pages_per_seq * page_size;
   const int chunk = decode_chunk_tokens(page_size);
@@ -60,11 +129,19 @@ static int decode_chunks(int32_t pages_per_seq, int32_t page_size) {
 
 using namespace pa;
 
+// Partials (o, then max / sum), then at a 256-byte boundary the work list:
+// a header and one int per pair, the pair count rounded up to 8.
+static size_t decode_partials_bytes(int32_t batch, int32_t num_heads, int32_t head_dim, int32_t n_chunks) {
+  const size_t parts = (size_t)batch * num_heads * n_chunks;
+  return (parts * ((size_t)head_dim + 2) * sizeof(float) + 255) / 256 * 256;
+}
+
 extern "C" size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_dim,
                                            int32_t pages_per_seq, int32_t page_size) {
   if (batch <= 0 || num_heads <= 0 || head_dim <= 0 || pages_per_seq <= 0 || page_size <= 0) return 0;
-  const size_t parts = (size_t)batch * num_heads * decode_chunks(pages_per_seq, page_size);
-  return parts * ((size_t)head_dim + 2) * sizeof(float);
+  const int n_chunks = decode_chunks(pages_per_seq, page_size);
+  const size_t pairs8 = ((size_t)batch * n_chunks + 7) / 8 * 8;
+  return decode_partials_bytes(batch, num_heads, head_dim, n_chunks) + (kDecodePlanHeader + pairs8) * sizeof(int32_t);
 }
 
 // Shared argument checks and launch of pa_decode / pa_decode_fp8.  `prm`
@@ -112,8 +189,9 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
   if ((int64_t)pages_per_seq * page_size > 0x7fffffffLL)
     return fail(PA_ERR_UNSUPPORTED, "%s: block table spans more than 2^31 tokens", name);
   const size_t need = pa_decode_workspace_size(batch, num_heads, head_dim, pages_per_seq, page_size);
-  if (pages_per_seq > 0 && (!workspace || workspace_bytes < need))
-    return fail(PA_ERR_WORKSPACE, "%s: workspace of %zu bytes needed, %zu given", name, need, workspace_bytes);
+  if (pages_per_seq > 0 && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u)))
+    return fail(PA_ERR_WORKSPACE, "%s: 256-byte aligned workspace of %zu bytes needed, %zu given", name, need,
+                workspace_bytes);
 
   prm.q = q;
   prm.q_bs = q_batch_stride;
@@ -146,9 +224,21 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
   prm.zero_empty = 0;
 
   hipStream_t s = (hipStream_t)stream;
-  const int64_t blocks = (int64_t)batch * prm.n_chunks * num_kv_heads;
+  const int64_t pairs = (int64_t)batch * prm.n_chunks;
+  // The work list pays for its launch once the grid is several waves of
+  // workgroups deep (two per CU, 256 CUs).
+  const bool planned = pairs > 0 && pairs * num_kv_heads >= kDecodePlanMinItems;
+  const int64_t blocks = planned ? (pairs + 7) / 8 * 8 * num_kv_heads : pairs * num_kv_heads;
   if (blocks > 0x7fffffff)
     return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)blocks);
+  if (planned) {
+    int32_t* plan = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) +
+                                               decode_partials_bytes(batch, num_heads, head_dim, prm.n_chunks));
+    decode_plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, s>>>(prm, plan);
+    int rc = launch_status(name);
+    if (rc) return rc;
+    prm.plan = plan;
+  }
   if (blocks > 0) {  // no table pages: every row is zero, only the merge pass runs
     const bool aligned = page_size % kDecodeStep == 0;
     const bool cap = prm.soft_cap > 0.f;

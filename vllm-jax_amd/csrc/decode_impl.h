@@ -89,7 +89,12 @@ struct DecodeParams {
   const float* k_scales;
   const float* v_scales;
   int64_t sc_page_stride, sc_head_stride;
+  // Work list (may be null): plan[0] = number of listed (sequence, chunk)
+  // pairs, plan[kDecodePlanHeader + r] = pair index b * n_chunks + c of rank
+  // r, most tokens first.
+  const int32_t* plan;
 };
+constexpr int kDecodePlanHeader = 64;  // ints before the first entry (256 bytes)
 
 __device__ __forceinline__ int64_t decode_row(const DecodeParams& p, int b) { return p.rows ? p.rows[b] : b; }
 
