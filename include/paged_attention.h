@@ -250,10 +250,14 @@ int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_strid
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * Workspace bytes pa_mixed needs (0 when every decode sequence fits one
- * 4096-token chunk, i.e. pages_per_seq * page_size <= the chunk).
+ * Workspace bytes pa_mixed needs (0 for bad sizes): decode partials when a
+ * decode sequence can span more than one 4096-token chunk, then a work list
+ * of (decode chunk | prefill q tile) pairs.  From 2048 workgroups on,
+ * pa_mixed orders the pairs by their measured cost and deals them over the
+ * XCDs (one extra launch); the output does not depend on the order.
  */
-size_t pa_mixed_workspace_size(int32_t num_decodes, int32_t num_heads, int32_t head_dim,
+size_t pa_mixed_workspace_size(int32_t batch, int32_t num_decodes, int32_t max_seqlen_q,
+                               int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                int32_t pages_per_seq, int32_t page_size);
 
 /*

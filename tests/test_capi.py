@@ -134,6 +134,20 @@ def test_decode_workspace_size():
     assert lib.pa_decode_workspace_size(0, 32, 128, 32, 256) == 0
 
 
+def test_mixed_workspace_size():
+    lib = PKG._lib.load()
+    r256 = lambda n: (n + 255) // 256 * 256
+    # Qwen3-0.6B step: 96 decode + 32 prefill sequences, 16-page tables of 256-token pages:
+    # one 4096-token chunk per decode sequence (no partials); G = 2 -> 128-token q tiles,
+    # 16 per prefill sequence; a 256-byte header, 32 bytes per pair (count rounded up to 8)
+    assert lib.pa_mixed_workspace_size(128, 96, 2048, 16, 8, 128, 16, 256) == 256 + 32 * (96 + 32 * 16)
+    # 40-page tables: 3 chunks per decode sequence, partials for 3 sequences x 16 heads
+    part = r256(3 * 16 * 3 * (128 + 2) * 4)
+    assert lib.pa_mixed_workspace_size(5, 3, 300, 16, 8, 128, 40, 256) == part + 256 + 32 * 16
+    assert lib.pa_mixed_workspace_size(5, 6, 300, 16, 8, 128, 40, 256) == 0   # more decodes than sequences
+    assert lib.pa_mixed_workspace_size(5, 3, 300, 15, 8, 128, 40, 256) == 0   # heads not a multiple of kv heads
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     """No silent fallback: a missing .so is an error, not a CPU path."""
     import importlib

@@ -134,7 +134,7 @@ SIGNATURES = {
         c_vp, c_vp, c_i32,             # src, dst, num_copies
         c_vp,                          # stream
     ]),
-    "pa_mixed_workspace_size": (c_sz, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "pa_mixed_workspace_size": (c_sz, [c_i32] * 8),
     "pa_mixed": (ctypes.c_int, [
         c_vp, c_i64, c_i64,            # q
         c_vp, c_vp, c_i32, c_i32,      # caches, num_pages, page_size

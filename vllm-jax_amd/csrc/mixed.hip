@@ -20,6 +20,11 @@
 // A decode item combines its 8 waves through the LDS of the prefill ring,
 // which it does not otherwise use.  When a decode sequence can span more
 // than one chunk, decode_merge_kernel follows as a second launch.
+//
+// Large steps instead take their items from a work list built by
+// mixed_plan_kernel (a launch of one workgroup before the step): decode
+// chunks and prefill q tiles priced on one measured time scale and sorted,
+// costliest first, then dealt over the XCDs; the zero pass follows them.
 #include <algorithm>
 
 #include "decode_impl.h"
@@ -37,9 +42,27 @@ constexpr int kZeroRowsPerBlock = kThreads;   // one row per thread in the zero 
 // MI355X: prefill levels whose items cost more than a decode chunk go first.
 constexpr float kPrefillOverDecodeTile = PA_MIXED_COST_RATIO;
 
+// Item costs of the work list in units of 1/8 us, from per-workgroup
+// timestamps of the Qwen3-0.6B mixed step on MI355X: a decode item takes
+// 8.0 us + 1.03 us per 64 tokens, a prefill item 11.2 us + 1.86 us per
+// 64-token kv tile.
+constexpr int kDecodeItemCost = 64;
+constexpr int kDecodeStepCost = 2;  // per 16-token step
+constexpr int kPrefillItemCost = 90;
+constexpr int kPrefillTileCost = 15;
+constexpr int kMixedPlanThreads = 1024;
+constexpr int kMixedPlanBins = 4096;
+constexpr int kMixedPlanMaxPrefill = 2048;          // prefill sequences the planner keeps in LDS
+constexpr int64_t kMixedPlanMinItems = 2048;        // workgroups from which pa_mixed builds a work list
+
 struct MixedParams {
   PrefillParams pre;  // the prefill sequences (arrays start at entry num_decodes)
   DecodeParams dec;   // the decode sequences (entries 0 .. num_decodes-1)
+  // Work list (may be null): plan[0] = entries, records of 8 ints from
+  // kPlanHeader on, costliest first: {0, b, qt, q0, lq_rows, lk, kv_pos_off}
+  // for a prefill q tile, {1, b, chunk} for a decode chunk.  With a list,
+  // [0, r3) are list items and [r3, r4) the zero pass.
+  const int32_t* plan;
   int32_t r1, r2, r3, r4;
   int32_t pre_head;     // prefill items in region [0, r1)
   int32_t n_dec_items;  // decode items in region [r1, r2)
@@ -84,28 +107,132 @@ __device__ __forceinline__ void mixed_zero_rows(const MixedParams& m, int zb) {
   }
 }
 
+// Work list of a mixed step (one workgroup).  Decode pairs (sequence b,
+// chunk c) come first in the index space, then prefill pairs (sequence b,
+// q tile qt); a pair is listed when it has work (chunk 0 of a decode
+// sequence always: it writes the zeros of an empty one).  Counting sort by
+// cost, largest first.
+__global__ void __launch_bounds__(kMixedPlanThreads)
+mixed_plan_kernel(MixedParams m, int32_t* __restrict__ plan) {
+  __shared__ int32_t hist[kMixedPlanBins];
+  __shared__ int4 seqs[kMixedPlanMaxPrefill];
+  __shared__ int32_t lag[kMixedPlanMaxPrefill];
+  __shared__ int32_t scan[kMixedPlanThreads];
+  const int tid = threadIdx.x;
+  const PrefillParams& pp = m.pre;
+  const DecodeParams& dp = m.dec;
+  for (int i = tid; i < kMixedPlanBins; i += kMixedPlanThreads) hist[i] = 0;
+  for (int b = tid; b < pp.batch; b += kMixedPlanThreads) prefill_seq_geometry(pp, b, seqs[b], lag[b]);
+  __syncthreads();
+  const int nc = dp.n_chunks, nq = pp.n_qtiles;
+  const int dec_pairs = dp.batch * nc;
+  const int pairs = dec_pairs + pp.batch * nq;
+  const int span = dp.pages_per_seq * dp.page_size;
+  auto bin_of = [&](int i) -> int {  // 0: nothing to do
+    int cost;
+    if (i < dec_pairs) {
+      const int b = i / nc, c = i - b * nc;
+      const int t0 = c * dp.chunk;
+      const int len = min(dp.lengths[b], span);
+      if (t0 >= len && c > 0) return 0;
+      const int steps = t0 >= len ? 0 : (min(len - t0, dp.chunk) + kDecodeStep - 1) / kDecodeStep;
+      cost = kDecodeItemCost + kDecodeStepCost * steps;
+    } else {
+      const int j = i - dec_pairs, b = j / nq;
+      const int tiles = prefill_pair_tiles(seqs[b], lag[b], j - b * nq, pp.tile_tokens);
+      if (tiles < 0) return 0;
+      cost = kPrefillItemCost + kPrefillTileCost * tiles;
+    }
+    return min(cost, kMixedPlanBins - 1);
+  };
+  for (int i = tid; i < pairs; i += kMixedPlanThreads) {
+    const int c = bin_of(i);
+    if (c) atomicAdd(&hist[c], 1);
+  }
+  __syncthreads();
+  constexpr int kPer = kMixedPlanBins / kMixedPlanThreads;  // thread t owns bins from the top
+  int cnt[kPer], local = 0;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    cnt[j] = hist[kMixedPlanBins - 1 - (kPer * tid + j)];
+    local += cnt[j];
+  }
+  int count;
+  int run = block_exclusive_scan<kMixedPlanThreads>(local, scan, count);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    hist[kMixedPlanBins - 1 - (kPer * tid + j)] = run;  // first rank of the bin
+    run += cnt[j];
+  }
+  __syncthreads();
+  for (int i = tid; i < pairs; i += kMixedPlanThreads) {
+    const int c = bin_of(i);
+    if (!c) continue;
+    int32_t* r = plan + kPlanHeader + 8 * atomicAdd(&hist[c], 1);
+    if (i < dec_pairs) {
+      const int b = i / nc;
+      st16(r, u32x4{1u, (uint32_t)b, (uint32_t)(i - b * nc), 0u});
+      st16(r + 4, u32x4{0u, 0u, 0u, 0u});
+    } else {
+      const int j = i - dec_pairs, b = j / nq;
+      const int4 g = seqs[b];
+      st16(r, u32x4{0u, (uint32_t)b, (uint32_t)(j - b * nq), (uint32_t)g.x});
+      st16(r + 4, u32x4{(uint32_t)g.y, (uint32_t)g.z, (uint32_t)g.w, 0u});
+    }
+  }
+  if (tid == 0) plan[0] = count;
+}
+
 template <bool kSoftCap, bool kAlignedP, bool kAlignedD>
 __global__ void __launch_bounds__(kThreads, 1)
 mixed_kernel(MixedParams m) {
   const int bid = blockIdx.x;
-  if (bid >= m.r1 && bid < m.r2) {
-    const int item = xcd_grouped_item(bid - m.r1, m.r2 - m.r1);
-    if (item < m.n_dec_items) {
-      // [8 waves][16][d] floats fill the K ring exactly; m and l go to the V ring
-      float* red_o = reinterpret_cast<float*>(&k_lds[0][0]);
-      float* red_m = reinterpret_cast<float*>(&v_lds[0][0]);
-      decode_item<kMixedDecodeWaves, kAlignedD, kSoftCap>(m.dec, item, red_o, red_m, red_m + 16 * kMixedDecodeWaves);
-    }
-    return;
-  }
   if (bid >= m.r3) {
     mixed_zero_rows(m, bid - m.r3);
     return;
   }
-  // one call site for both prefill regions (the body is large)
-  const int pre_bid = bid < m.r1 ? bid : m.pre_head + (bid - m.r2);
-  if (bid < m.r1 && bid >= m.pre_head) return;  // padding of region 1
-  prefill_body<kSoftCap, kAlignedP>(m.pre, pre_bid);
+  // one call site each for the decode item and the prefill item (both are large)
+  int dec = -1;
+  PrefillWork w;
+  bool pre = false;
+  if (m.plan) {
+    // XCD x = bid % 8 takes ranks x, x + 8, ... of the list, all kv heads of
+    // a rank in a row: the XCDs get near-equal work, workgroups an XCD
+    // receives in a row cost the same, and the kv heads of a decode token
+    // row are read by one XCD at nearly the same time.
+    const int hkv = m.pre.num_kv_heads;
+    const int k = bid >> 3;
+    const int kr = k / hkv;
+    const int r = 8 * kr + (bid & 7);
+    const int h = k - kr * hkv;
+    const __attribute__((address_space(4))) int32_t* pl = (const __attribute__((address_space(4))) int32_t*)m.plan;
+    const int count = pl[0];
+    const __attribute__((address_space(4))) int32_t* e = pl + kPlanHeader + 8 * r;  // room for every rank
+    const int kind = e[0], b = e[1], sub = e[2];
+    if (r >= count) return;  // uniform over the workgroup
+    if (kind) {
+      dec = (b * m.dec.n_chunks + sub) * hkv + h;
+    } else {
+      w = PrefillWork{b, sub, h, e[3], e[4], e[5], e[6]};
+      pre = true;
+    }
+  } else if (bid >= m.r1 && bid < m.r2) {
+    const int item = xcd_grouped_item(bid - m.r1, m.r2 - m.r1);
+    if (item >= m.n_dec_items) return;
+    dec = item;
+  } else {
+    const int pre_bid = bid < m.r1 ? bid : m.pre_head + (bid - m.r2);
+    if (bid < m.r1 && bid >= m.pre_head) return;  // padding of region 1
+    pre = prefill_resolve(m.pre, pre_bid, w);
+  }
+  if (dec >= 0) {
+    // [8 waves][16][d] floats fill the K ring exactly; m and l go to the V ring
+    float* red_o = reinterpret_cast<float*>(&k_lds[0][0]);
+    float* red_m = reinterpret_cast<float*>(&v_lds[0][0]);
+    decode_item<kMixedDecodeWaves, kAlignedD, kSoftCap>(m.dec, dec, red_o, red_m, red_m + 16 * kMixedDecodeWaves);
+    return;
+  }
+  if (pre) prefill_run<kSoftCap, kAlignedP>(m.pre, w);
 }
 
 static_assert(sizeof(float) * kMixedDecodeWaves * 16 * kPHeadDim <= sizeof(uint16_t) * kStages * kTileElems,
@@ -132,12 +259,34 @@ static int64_t round8(int64_t x) { return (x + 7) & ~(int64_t)7; }
 
 using namespace pa;
 
-extern "C" size_t pa_mixed_workspace_size(int32_t num_decodes, int32_t num_heads, int32_t head_dim,
+// Decode partials (none when every decode sequence fits one chunk), then at
+// a 256-byte boundary the work list: a header and 8 ints per pair, the pair
+// count rounded up to 8.
+static size_t mixed_partials_bytes(int32_t num_decodes, int32_t num_heads, int32_t head_dim, int chunks) {
+  if (num_decodes <= 0 || chunks <= 1) return 0;  // every decode sequence is finished inside its item
+  return ((size_t)num_decodes * num_heads * chunks * ((size_t)head_dim + 2) * sizeof(float) + 255) / 256 * 256;
+}
+
+static int64_t mixed_pairs(int32_t batch, int32_t num_decodes, int32_t max_seqlen_q, int32_t num_heads,
+                           int32_t num_kv_heads, int32_t pages_per_seq, int32_t page_size) {
+  const int chunks = pages_per_seq > 0 ? mixed_decode_chunks(pages_per_seq, page_size) : 0;
+  const int64_t tile_tokens = kRows / (num_heads / num_kv_heads);
+  const int64_t n_pre = batch - num_decodes;
+  const int64_t n_qtiles = n_pre > 0 ? (max_seqlen_q + tile_tokens - 1) / tile_tokens : 0;
+  return (int64_t)num_decodes * chunks + n_pre * n_qtiles;
+}
+
+extern "C" size_t pa_mixed_workspace_size(int32_t batch, int32_t num_decodes, int32_t max_seqlen_q,
+                                          int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                           int32_t pages_per_seq, int32_t page_size) {
-  if (num_decodes <= 0 || num_heads <= 0 || head_dim <= 0 || pages_per_seq <= 0 || page_size <= 0) return 0;
-  const int chunks = mixed_decode_chunks(pages_per_seq, page_size);
-  if (chunks <= 1) return 0;  // every decode sequence is finished inside its item
-  return (size_t)num_decodes * num_heads * chunks * ((size_t)head_dim + 2) * sizeof(float);
+  if (batch < 0 || num_decodes < 0 || num_decodes > batch || max_seqlen_q < 0 || num_heads <= 0 ||
+      num_kv_heads <= 0 || num_heads % num_kv_heads || head_dim <= 0 || pages_per_seq < 0 || page_size <= 0)
+    return 0;
+  const int chunks = pages_per_seq > 0 ? mixed_decode_chunks(pages_per_seq, page_size) : 0;
+  const int64_t pairs = mixed_pairs(batch, num_decodes, max_seqlen_q, num_heads, num_kv_heads, pages_per_seq,
+                                    page_size);
+  return mixed_partials_bytes(num_decodes, num_heads, head_dim, chunks) +
+         (size_t)(kPlanHeader + 8 * ((pairs + 7) / 8 * 8)) * sizeof(int32_t);
 }
 
 extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
@@ -178,9 +327,12 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
   if ((int64_t)pages_per_seq * page_size > 0x7fffffffLL)
     return fail(PA_ERR_UNSUPPORTED, "pa_mixed: block table spans more than 2^31 tokens");
   const int n_chunks = pages_per_seq > 0 ? mixed_decode_chunks(pages_per_seq, page_size) : 0;
-  const size_t need = pa_mixed_workspace_size(num_decodes, num_heads, head_dim, pages_per_seq, page_size);
-  if (need > 0 && (!workspace || workspace_bytes < need))
-    return fail(PA_ERR_WORKSPACE, "pa_mixed: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+  const size_t need = pa_mixed_workspace_size(batch, num_decodes, max_seqlen_q, num_heads, num_kv_heads, head_dim,
+                                              pages_per_seq, page_size);
+  if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u))
+    return fail(PA_ERR_WORKSPACE, "pa_mixed: 256-byte aligned workspace of %zu bytes needed, %zu given", need,
+                workspace_bytes);
+  const size_t partials = mixed_partials_bytes(num_decodes, num_heads, head_dim, n_chunks);
   const float cap = soft_cap > 0.f ? soft_cap : 0.f;
 
   MixedParams m{};
@@ -242,7 +394,7 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
   dp.soft_cap = cap;
   dp.logit_scale = cap > 0.f ? decode_scale : decode_scale * kLog2e;
   dp.ws_o = reinterpret_cast<float*>(workspace);
-  dp.ws_ml = need > 0 ? dp.ws_o + (size_t)num_decodes * num_heads * n_chunks * head_dim : nullptr;
+  dp.ws_ml = partials > 0 ? dp.ws_o + (size_t)num_decodes * num_heads * n_chunks * head_dim : nullptr;
   dp.out = out;
   dp.out_bs = out_tok_stride;
   dp.out_hs = out_head_stride;
@@ -276,17 +428,31 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
   const int64_t r1 = round8(pre_head);
   const int64_t r2 = r1 + round8(dec_items);
   const int64_t r3 = r2 + (pre_items - pre_head);
-  const int64_t r4 = r3 + (num_tokens + kZeroRowsPerBlock - 1) / kZeroRowsPerBlock;
+  const int64_t zero_blocks = (num_tokens + kZeroRowsPerBlock - 1) / kZeroRowsPerBlock;
+  // the work list: every (decode chunk | prefill q tile) pair, all kv heads
+  const int64_t list_pairs = mixed_pairs(batch, num_decodes, max_seqlen_q, num_heads, num_kv_heads, pages_per_seq,
+                                         page_size);
+  const bool planned = list_pairs > 0 && list_pairs * num_kv_heads >= kMixedPlanMinItems &&
+                       n_pre <= kMixedPlanMaxPrefill;
+  const int64_t list_items = (list_pairs + 7) / 8 * 8 * num_kv_heads;
+  const int64_t r4 = (planned ? list_items : r3) + zero_blocks;
   if (r4 > 0x7fffffff)
     return fail(PA_ERR_UNSUPPORTED, "pa_mixed: grid of %lld workgroups too large", (long long)r4);
   m.r1 = (int32_t)r1;
   m.r2 = (int32_t)r2;
-  m.r3 = (int32_t)r3;
+  m.r3 = (int32_t)(planned ? list_items : r3);
   m.r4 = (int32_t)r4;
   m.pre_head = (int32_t)pre_head;
   m.n_dec_items = (int32_t)dec_items;
 
   hipStream_t s = (hipStream_t)stream;
+  if (planned) {
+    int32_t* plan = reinterpret_cast<int32_t*>(reinterpret_cast<char*>(workspace) + partials);
+    mixed_plan_kernel<<<dim3(1), dim3(kMixedPlanThreads), 0, s>>>(m, plan);
+    int rc = launch_status("pa_mixed(plan)");
+    if (rc) return rc;
+    m.plan = plan;
+  }
   const dim3 grid((unsigned)r4), block(kThreads);
   const bool aligned_p = page_size % kTileN == 0;
   const bool aligned_d = page_size % kDecodeStep == 0;
@@ -300,7 +466,7 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
     else mixed_kernel<false, false, false><<<grid, block, 0, s>>>(m);
   }
   int rc = launch_status("pa_mixed");
-  if (rc || need == 0 || num_decodes == 0) return rc;
+  if (rc || partials == 0 || num_decodes == 0) return rc;
   launch_decode_merge(dp, s);
   return launch_status("pa_mixed(merge)");
 }

@@ -23,7 +23,7 @@ constexpr int kPlanMaxBatch = 2048;   // sequences whose geometry the planner ke
 // list orders the work and changes no result).  Pairs are counting-sorted by
 // cost, largest first, so the longest items start first and no long item is
 // left for the end.  Per sequence, q0 / lq_rows / lk / kv_pos_off are derived
-// exactly as prefill_body derives them without a list.
+// exactly as prefill_resolve derives them without a list.
 __device__ void prefill_plan(const PrefillParams& p, int32_t* __restrict__ plan) {
   __shared__ int32_t hist[kPlanBins];
   __shared__ int4 seqs[kPlanMaxBatch];  // q0, lq_rows, lk, kv_pos_off
@@ -31,27 +31,14 @@ __device__ void prefill_plan(const PrefillParams& p, int32_t* __restrict__ plan)
   __shared__ int32_t scan[kPrepThreads];
   const int tid = threadIdx.x;
   for (int i = tid; i < kPlanBins; i += kPrepThreads) hist[i] = 0;
-  for (int b = tid; b < p.batch; b += kPrepThreads) {
-    const int q0 = p.cu_q[b];
-    const int lq = p.cu_q[b + 1] - q0;
-    const int lq_rows = (q0 < 0 || q0 >= p.num_tokens) ? 0 : min(min(lq, p.max_seqlen_q), p.num_tokens - q0);
-    const int lk = min(p.kv_lens ? p.kv_lens[b] : (p.cu_k ? p.cu_k[b + 1] - p.cu_k[b] : lq),
-                       p.pages_per_seq * p.page_size);
-    const int off = lq_rows > 0 ? p.positions[q0] - (lk - lq) : 0;
-    seqs[b] = make_int4(q0, lq_rows, lk, off);
-    lag[b] = lk - lq;
-  }
+  for (int b = tid; b < p.batch; b += kPrepThreads) prefill_seq_geometry(p, b, seqs[b], lag[b]);
   __syncthreads();
-  const int nq = p.n_qtiles, T = p.tile_tokens;
+  const int nq = p.n_qtiles;
   const int pairs = p.batch * nq;
-  // cost bin of pair i (0: no rows)
-  auto bin_of = [&](int i) -> int {
-    const int b = i / nq, qt = i - b * nq;
-    const int rows = seqs[b].y;
-    if (qt * T >= rows) return 0;
-    const int64_t kv_hi = min((int64_t)seqs[b].z, (int64_t)lag[b] + min(qt * T + T, rows));
-    const int64_t tiles = kv_hi <= 0 ? 0 : (kv_hi + kTileN - 1) / kTileN;
-    return (int)min<int64_t>(tiles + 1, kPlanBins - 1);
+  auto bin_of = [&](int i) -> int {  // 0: no rows
+    const int b = i / nq;
+    const int tiles = prefill_pair_tiles(seqs[b], lag[b], i - b * nq, p.tile_tokens);
+    return tiles < 0 ? 0 : min(tiles + 1, kPlanBins - 1);
   };
   for (int i = tid; i < pairs; i += kPrepThreads) {
     const int c = bin_of(i);
@@ -66,21 +53,13 @@ __device__ void prefill_plan(const PrefillParams& p, int32_t* __restrict__ plan)
     cnt[j] = hist[kPlanBins - 1 - (kPer * tid + j)];
     local += cnt[j];
   }
-  scan[tid] = local;
-  for (int o = 1; o < kPrepThreads; o <<= 1) {
-    __syncthreads();
-    const int v = tid >= o ? scan[tid - o] : 0;
-    __syncthreads();
-    scan[tid] += v;
-  }
-  __syncthreads();
-  int run = scan[tid] - local;  // pairs in larger bins
+  int count;
+  int run = block_exclusive_scan<kPrepThreads>(local, scan, count);  // pairs in larger bins
 #pragma unroll
   for (int j = 0; j < kPer; ++j) {
     hist[kPlanBins - 1 - (kPer * tid + j)] = run;  // first rank of the bin
     run += cnt[j];
   }
-  const int count = scan[kPrepThreads - 1];
   __syncthreads();
   for (int i = tid; i < pairs; i += kPrepThreads) {
     const int c = bin_of(i);

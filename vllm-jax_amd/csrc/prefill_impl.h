@@ -155,18 +155,59 @@ static __shared__ __attribute__((aligned(1024))) uint16_t k_lds[kStages][kTileEl
 static __shared__ __attribute__((aligned(1024))) uint16_t v_lds[kStages][kTileElems];
 static __shared__ int red_max[kWaves], red_min[kWaves];
 
-// One prefill work item (q tile, sequence, kv head) numbered `bid`, run by a
-// whole 512-thread workgroup.
-template <bool kSoftCap, bool kAligned>
-__device__ __forceinline__ void prefill_body(const PrefillParams& p, int bid) {
-  auto k_stage = [&](auto c) __attribute__((always_inline)) -> uint16_t* { return k_lds[decltype(c)::value]; };
-  auto v_stage = [&](auto c) __attribute__((always_inline)) -> uint16_t* { return v_lds[decltype(c)::value]; };
+// Row range and kv geometry of prefill sequence b, as prefill_resolve
+// derives them without a work list: g = (q0, lq_rows, lk, kv_pos_off), and
+// lag = lk - lq (kv index of the first q row when positions are contiguous).
+__device__ __forceinline__ void prefill_seq_geometry(const PrefillParams& p, int b, int4& g, int& lag) {
+  const int q0 = p.cu_q[b];
+  const int lq = p.cu_q[b + 1] - q0;
+  const int lq_rows = (q0 < 0 || q0 >= p.num_tokens) ? 0 : min(min(lq, p.max_seqlen_q), p.num_tokens - q0);
+  const int lk = min(p.kv_lens ? p.kv_lens[b] : (p.cu_k ? p.cu_k[b + 1] - p.cu_k[b] : lq),
+                     p.pages_per_seq * p.page_size);
+  const int off = lq_rows > 0 ? p.positions[q0] - (lk - lq) : 0;
+  g = make_int4(q0, lq_rows, lk, off);
+  lag = lk - lq;
+}
 
+// kv tiles the last row of q tile qt of a sequence with geometry (g, lag)
+// sees, if positions are contiguous; -1 when the tile has no rows.
+__device__ __forceinline__ int prefill_pair_tiles(const int4& g, int lag, int qt, int tile_tokens) {
+  const int rows = g.y;
+  if (qt * tile_tokens >= rows) return -1;
+  const int64_t kv_hi = min((int64_t)g.z, (int64_t)lag + min(qt * tile_tokens + tile_tokens, rows));
+  return kv_hi <= 0 ? 0 : (int)((kv_hi + kTileN - 1) / kTileN);
+}
+
+// Exclusive scan over the workgroup (blockDim.x == kScanThreads) of one
+// value per thread; `tmp` is kScanThreads ints of LDS.  Returns the sum of
+// the values of lower threads; `total` receives the sum of all.
+template <int kScanThreads>
+__device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int& total) {
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  tmp[tid] = v;
+  for (int o = 1; o < kScanThreads; o <<= 1) {
+    __syncthreads();
+    const int u = tid >= o ? tmp[tid - o] : 0;
+    __syncthreads();
+    tmp[tid] += u;
+  }
+  __syncthreads();
+  total = tmp[kScanThreads - 1];
+  const int excl = tmp[tid] - v;
+  __syncthreads();
+  return excl;
+}
+
+// A resolved work item: kv head kvh of q tile qt of sequence b, with the
+// sequence's row range and kv geometry.
+struct PrefillWork {
+  int b, qt, kvh, q0, lq_rows, lk, kv_pos_off;
+};
+
+// Work item of workgroup `bid` (from the work list when there is one);
+// false when the workgroup has nothing to do.
+__device__ __forceinline__ bool prefill_resolve(const PrefillParams& p, int bid, PrefillWork& w) {
   const int hkv = p.num_kv_heads;
-  int qt, b, kvh, q0, lq_rows, lk, kv_pos_off;
   if (p.plan) {
     // Workgroups are dealt round-robin to the 8 XCDs, and an XCD deals its
     // own round-robin to its four shader engines, waiting whenever the next
@@ -185,33 +226,47 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, int bid) {
       sub = r - rank * per;
     } else {
       rank = bid / hkv;
-      kvh = bid - rank * hkv;
+      w.kvh = bid - rank * hkv;
     }
     const __attribute__((address_space(4))) int32_t* pl = (const __attribute__((address_space(4))) int32_t*)p.plan;
     const int count = pl[0];
     // the list has room for every rank of the grid; entries past count are
     // never used
     const __attribute__((address_space(4))) int32_t* r = pl + kPlanHeader + 8 * rank;
-    b = r[0];
-    qt = r[1];
-    q0 = r[2];
-    lq_rows = r[3];
-    lk = r[4];
-    kv_pos_off = r[5];
-    if (rank >= count) return;  // uniform across the workgroup
-    if (by_xcd) kvh = 8 * sub + (((bid & 7) - b) & 7);
-  } else {
-    prefill_item(bid, p.batch, hkv, p.n_qtiles, qt, b, kvh);
-    q0 = p.cu_q[b];
-    const int lq = p.cu_q[b + 1] - q0;
-    // rows past max_seqlen_q are left to the zero pass; rows past the token
-    // count (malformed cu_seqlens) are never touched
-    lq_rows = (q0 < 0 || q0 >= p.num_tokens) ? 0 : min(min(lq, p.max_seqlen_q), p.num_tokens - q0);
-    if (qt * p.tile_tokens >= lq_rows) return;  // uniform across the workgroup
-    // kv lengths past the block table's span are clamped to it
-    lk = min(p.kv_lens ? p.kv_lens[b] : (p.cu_k ? p.cu_k[b + 1] - p.cu_k[b] : lq), p.pages_per_seq * p.page_size);
-    kv_pos_off = p.positions[q0] - (lk - lq);
+    w.b = r[0];
+    w.qt = r[1];
+    w.q0 = r[2];
+    w.lq_rows = r[3];
+    w.lk = r[4];
+    w.kv_pos_off = r[5];
+    if (rank >= count) return false;  // uniform across the workgroup
+    if (by_xcd) w.kvh = 8 * sub + (((bid & 7) - w.b) & 7);
+    return true;
   }
+  prefill_item(bid, p.batch, hkv, p.n_qtiles, w.qt, w.b, w.kvh);
+  w.q0 = p.cu_q[w.b];
+  const int lq = p.cu_q[w.b + 1] - w.q0;
+  // rows past max_seqlen_q are left to the zero pass; rows past the token
+  // count (malformed cu_seqlens) are never touched
+  w.lq_rows = (w.q0 < 0 || w.q0 >= p.num_tokens) ? 0 : min(min(lq, p.max_seqlen_q), p.num_tokens - w.q0);
+  if (w.qt * p.tile_tokens >= w.lq_rows) return false;  // uniform across the workgroup
+  // kv lengths past the block table's span are clamped to it
+  w.lk = min(p.kv_lens ? p.kv_lens[w.b] : (p.cu_k ? p.cu_k[w.b + 1] - p.cu_k[w.b] : lq),
+             p.pages_per_seq * p.page_size);
+  w.kv_pos_off = p.positions[w.q0] - (w.lk - lq);
+  return true;
+}
+
+// One prefill work item, run by a whole 512-thread workgroup.
+template <bool kSoftCap, bool kAligned>
+__device__ __forceinline__ void prefill_run(const PrefillParams& p, const PrefillWork& w) {
+  auto k_stage = [&](auto c) __attribute__((always_inline)) -> uint16_t* { return k_lds[decltype(c)::value]; };
+  auto v_stage = [&](auto c) __attribute__((always_inline)) -> uint16_t* { return v_lds[decltype(c)::value]; };
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const int b = w.b, qt = w.qt, kvh = w.kvh, q0 = w.q0, lq_rows = w.lq_rows, lk = w.lk, kv_pos_off = w.kv_pos_off;
   const int tok0 = qt * p.tile_tokens;
 
   // ---- this lane's row
@@ -657,6 +712,13 @@ __device__ __forceinline__ void prefill_body(const PrefillParams& p, int bid) {
 #pragma unroll
       for (int pr = 0; pr < 2; ++pr) st16(orow + 32 * dt + 16 * pr, ow[dt][pr]);
   }
+}
+
+// The work item numbered `bid`, resolved and run.
+template <bool kSoftCap, bool kAligned>
+__device__ __forceinline__ void prefill_body(const PrefillParams& p, int bid) {
+  PrefillWork w;
+  if (prefill_resolve(p, bid, w)) prefill_run<kSoftCap, kAligned>(p, w);
 }
 
 }  // namespace pa

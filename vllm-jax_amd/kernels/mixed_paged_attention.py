@@ -18,11 +18,12 @@ from ._common import (as_i32, inv_sqrt_head_dim_bf16, pages_strides, require_bf1
                       stream_handle)
 
 
-def mixed_workspace_bytes(num_decodes: int, num_heads: int, head_dim: int, pages_per_seq: int,
-                          page_size: int) -> int:
-    """Workspace ``mixed_paged_attention`` needs (0 when every decode context
-    fits one 4096-token chunk)."""
-    return int(_lib.load().pa_mixed_workspace_size(num_decodes, num_heads, head_dim, pages_per_seq, page_size))
+def mixed_workspace_bytes(batch: int, num_decodes: int, max_seqlen_q: int, num_heads: int, num_kv_heads: int,
+                          head_dim: int, pages_per_seq: int, page_size: int) -> int:
+    """Workspace ``mixed_paged_attention`` needs: decode partials (when a
+    decode context can span more than one 4096-token chunk) and the work list."""
+    return int(_lib.load().pa_mixed_workspace_size(batch, num_decodes, max_seqlen_q, num_heads, num_kv_heads,
+                                                   head_dim, pages_per_seq, page_size))
 
 
 def mixed_paged_attention(
@@ -93,11 +94,12 @@ def mixed_paged_attention(
         require_bf16("out", out)
         if tuple(out.shape) != tuple(q.shape):
             raise ValueError(f"out must have shape {tuple(q.shape)}")
-    need = mixed_workspace_bytes(int(num_decodes), num_heads, head_dim, pages_per_sequence, page_size)
-    if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
-    ws_ptr = workspace.data_ptr() if (need > 0 and workspace is not None) else None
-    ws_bytes = workspace.numel() * workspace.element_size() if ws_ptr is not None else 0
+    need = mixed_workspace_bytes(batch, int(num_decodes), int(max_seqlen_q), num_heads, num_kv_heads, head_dim,
+                                 pages_per_sequence, page_size)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    ws_ptr = workspace.data_ptr()
+    ws_bytes = workspace.numel() * workspace.element_size()
     if prefill_scale is None:
         prefill_scale = inv_sqrt_head_dim_bf16(head_dim)
     soft_cap = 0.0 if attn_logits_soft_cap is None else float(attn_logits_soft_cap)
