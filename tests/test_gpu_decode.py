@@ -132,3 +132,17 @@ def test_decode_through_attention_seam(pkg, dev):
     got = ora.bf16_to_f32(u16(out))
     assert float(np.abs(got - ora.bf16_to_f32(ref)).max()) <= TOL
     assert not got[3].any()  # length-0 (padded) sequence
+
+
+def test_decode_work_list_all_sequences(pkg, dev):
+    """A launch large enough for the decode work list (96 sequences x 3 chunks
+    x 8 kv heads = 2304 workgroups), every sequence against the oracle:
+    lengths 0 and 1, chunk boundaries, ragged rest."""
+    rng = np.random.default_rng(31)
+    lens = rng.integers(2, 6000, 96)
+    lens[:8] = [0, 1, 2047, 2048, 2049, 4096, 4097, 6000]
+    width = 1 << (int(-(-6000 // 256)) - 1).bit_length()
+    db = wl.make_decode(lens.tolist(), num_heads=32, num_kv_heads=8, page_size=256, rng=rng, table_width=width)
+    print(f"decode work list: {db.batch} sequences, table width {width}", flush=True)
+    out, _ = _run_and_check(pkg, dev, db, seed=31)
+    assert not u16(out)[0].any()

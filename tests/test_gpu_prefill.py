@@ -219,3 +219,13 @@ def test_prefill_work_list(pkg, dev, case):
         assert tuple(int(x) for x in r[2:6]) == (q0, rows, lk, off), (key, r)
         costs.append(cost)
     assert all(a >= b for a, b in zip(costs, costs[1:])), "work list not in non-increasing cost"
+
+
+def test_prefill_more_sequences_than_the_planner_holds(pkg, dev):
+    """2100 sequences of 1-3 tokens: above the work list's 2048-sequence
+    limit pa_prefill runs in grid order; every row against the oracle."""
+    rng = np.random.default_rng(41)
+    lens = rng.integers(1, 4, 2100).tolist()
+    pb = wl.make_prefill(lens, num_heads=16, num_kv_heads=8, page_size=16, rng=rng)
+    print(f"prefill {pb.batch} sequences, {pb.num_tokens} tokens", flush=True)
+    _prefill(pkg, dev, pb, seed=41, use_seam=False)
