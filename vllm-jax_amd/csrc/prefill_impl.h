@@ -359,18 +359,22 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   struct TileAddrs {
     const uint16_t* g[2 * kBlk];
   };
-  auto page_raw = [&](int j0) __attribute__((always_inline)) {
-    const int lp = min(j0 / p.page_size, p.pages_per_seq - 1);  // stays inside the table row
+  // Aligned pages hold tpp whole tiles: tile j0 = 64 (tpp lp + r) is tile r
+  // of table entry lp.  The loop walks (lp, r) incrementally, so no division
+  // sits on the softmax wave's path.
+  const int tpp = kAligned ? p.page_size / kTileN : 1;
+  const int64_t tile_stride = (int64_t)kTileN * p.slot_stride;
+  auto page_raw_at = [&](int lp) __attribute__((always_inline)) {
     const __attribute__((address_space(4))) int32_t* c = (const __attribute__((address_space(4))) int32_t*)bt_row;
-    return c[lp];
+    return c[min(lp, p.pages_per_seq - 1)];  // stays inside the table row
   };
-  auto tile_addrs = [&](int j0, int32_t raw) __attribute__((always_inline)) {
+  // rin: (aligned) the tile's index inside its page
+  auto tile_addrs = [&](int j0, int32_t raw, int rin) __attribute__((always_inline)) {
     TileAddrs a;
     if constexpr (kAligned) {
       // page_size % 64 == 0: the whole tile lies in one page
-      const int lp = j0 / p.page_size;
       const int32_t page = raw < 0 ? 0 : (raw >= p.num_pages ? p.num_pages - 1 : raw);
-      const int64_t pbase = (int64_t)page * p.page_stride + (int64_t)(j0 - lp * p.page_size) * p.slot_stride + head_off;
+      const int64_t pbase = (int64_t)page * p.page_stride + rin * tile_stride + head_off;
       if (j0 + kTileN <= lk) {
 #pragma unroll
         for (int i = 0; i < kBlk; ++i) {
@@ -414,12 +418,9 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     dma16(a.g[i], base + (uint32_t)(stage * kTileElems * 2 + (kBlk * wave + (i >> 1)) * 1024));
   };
   auto issue_tile_raw = [&](int j0, int32_t raw, int stage) __attribute__((always_inline)) {
-    const TileAddrs a = tile_addrs(j0, raw);
+    const TileAddrs a = tile_addrs(j0, raw, (j0 / kTileN) % tpp);
 #pragma unroll
     for (int i = 0; i < 2 * kBlk; ++i) dma_issue(a, i, stage);
-  };
-  auto issue_tile = [&](int j0, int stage) __attribute__((always_inline)) {
-    issue_tile_raw(j0, kAligned ? page_raw(j0) : 0, stage);
   };
   constexpr int kDmaPerTile = 2 * kBlk;  // vm instructions one wave issues per tile
 
@@ -590,6 +591,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   // exist (every iteration but the first and the last has both), so that the
   // steady-state M segment is a single block the scheduler can interleave.
   int32_t page_next = 0;  // raw block-table entry of the next tile to load (aligned path)
+  int nx_lp = 0, nx_r = 0;  // (aligned) table entry and in-page index of that tile
   auto iteration = [&](int t, auto st, auto has_pv, auto has_qk) __attribute__((always_inline)) {
     constexpr int s = decltype(st)::value;
     constexpr bool kPv = decltype(has_pv)::value;
@@ -617,8 +619,14 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     const bool dma = ti < n_tiles;
     const int dstage = grp_b ? (s + 3) % kStages : (s + 2) % kStages;
     TileAddrs ta;
-    if (dma) ta = tile_addrs(ti * kTileN, page_next);
-    if constexpr (kAligned) page_next = page_raw((ti + 1) * kTileN);  // for the next iteration
+    if (dma) ta = tile_addrs(ti * kTileN, page_next, nx_r);
+    if constexpr (kAligned) {  // for the next iteration: tile ti + 1
+      if (++nx_r == tpp) {
+        nx_r = 0;
+        ++nx_lp;
+      }
+      page_next = page_raw_at(nx_lp);
+    }
     // one DMA before each quarter of the softmax: a burst of them would
     // stall on the address queue
     auto between = [&](int u) __attribute__((always_inline)) {
@@ -648,7 +656,11 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   if (n_tiles > 1) issue_tile_raw(kTileN, raw_pre[1], 1);
   if (grp_b && n_tiles > 2) issue_tile_raw(2 * kTileN, raw_pre[2], 2);
   // raw page id of the first tile the loop loads (tile `ahead`)
-  if (kAligned && n_tiles > 0) page_next = page_raw(ahead * kTileN);
+  if (kAligned && n_tiles > 0) {
+    nx_lp = ahead / tpp;
+    nx_r = ahead - nx_lp * tpp;
+    page_next = page_raw_at(nx_lp);
+  }
   const int issued = min(n_tiles, grp_b ? 3 : 2);
   if (issued == 3) wait_vm_lgkm0<2 * kDmaPerTile>();
   else if (issued == 2) wait_vm_lgkm0<kDmaPerTile>();
