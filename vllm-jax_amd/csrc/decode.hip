@@ -30,7 +30,8 @@ decode_plan_kernel(DecodeParams p, int32_t* __restrict__ plan) {
     const int steps = (min(len - t0, p.chunk) + kDecodeStep - 1) / kDecodeStep;
     return min(steps + 1, kPlanBins - 1);
   };
-  for (int i = tid; i < pairs; i += kPlanThreads) {
+  for (int64_t ii = tid; ii < pairs; ii += kPlanThreads) {
+    const int i = (int)ii;
     const int c = bin_of(i);
     if (c) atomicAdd(&hist[c], 1);
   }
@@ -48,7 +49,8 @@ decode_plan_kernel(DecodeParams p, int32_t* __restrict__ plan) {
   if (tid < kPlanBins) hist[kPlanBins - 1 - tid] = scan[tid] - local;  // first rank of the bin
   const int count = scan[kPlanThreads - 1];
   __syncthreads();
-  for (int i = tid; i < pairs; i += kPlanThreads) {
+  for (int64_t ii = tid; ii < pairs; ii += kPlanThreads) {
+    const int i = (int)ii;
     const int c = bin_of(i);
     if (c) plan[kDecodePlanHeader + atomicAdd(&hist[c], 1)] = i;
   }

@@ -145,7 +145,8 @@ mixed_plan_kernel(MixedParams m, int32_t* __restrict__ plan) {
     }
     return min(cost, kMixedPlanBins - 1);
   };
-  for (int i = tid; i < pairs; i += kMixedPlanThreads) {
+  for (int64_t ii = tid; ii < pairs; ii += kMixedPlanThreads) {
+    const int i = (int)ii;
     const int c = bin_of(i);
     if (c) atomicAdd(&hist[c], 1);
   }
@@ -165,7 +166,8 @@ mixed_plan_kernel(MixedParams m, int32_t* __restrict__ plan) {
     run += cnt[j];
   }
   __syncthreads();
-  for (int i = tid; i < pairs; i += kMixedPlanThreads) {
+  for (int64_t ii = tid; ii < pairs; ii += kMixedPlanThreads) {
+    const int i = (int)ii;
     const int c = bin_of(i);
     if (!c) continue;
     int32_t* r = plan + kPlanHeader + 8 * atomicAdd(&hist[c], 1);

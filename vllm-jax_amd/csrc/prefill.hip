@@ -40,7 +40,8 @@ __device__ void prefill_plan(const PrefillParams& p, int32_t* __restrict__ plan)
     const int tiles = prefill_pair_tiles(seqs[b], lag[b], i - b * nq, p.tile_tokens);
     return tiles < 0 ? 0 : min(tiles + 1, kPlanBins - 1);
   };
-  for (int i = tid; i < pairs; i += kPrepThreads) {
+  for (int64_t ii = tid; ii < pairs; ii += kPrepThreads) {
+    const int i = (int)ii;
     const int c = bin_of(i);
     if (c) atomicAdd(&hist[c], 1);
   }
@@ -61,7 +62,8 @@ __device__ void prefill_plan(const PrefillParams& p, int32_t* __restrict__ plan)
     run += cnt[j];
   }
   __syncthreads();
-  for (int i = tid; i < pairs; i += kPrepThreads) {
+  for (int64_t ii = tid; ii < pairs; ii += kPrepThreads) {
+    const int i = (int)ii;
     const int c = bin_of(i);
     if (!c) continue;
     const int rank = atomicAdd(&hist[c], 1);
