@@ -105,6 +105,26 @@ __device__ __forceinline__ float sum_xor16(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Max and min of `mx` / `mn` over the 32 lanes of each wave half (lanes i
+// and i ^ k, k < 32), in VALU: two quad permutations, the 8- and 16-lane
+// row mirrors (DPP), then one permlane16 swap.  Every lane ends with the
+// result of its half.
+template <int kCtrl>
+__device__ __forceinline__ void minmax_dpp(int& mx, int& mn) {
+  mx = max(mx, __builtin_amdgcn_update_dpp(mx, mx, kCtrl, 0xF, 0xF, false));
+  mn = min(mn, __builtin_amdgcn_update_dpp(mn, mn, kCtrl, 0xF, 0xF, false));
+}
+__device__ __forceinline__ void minmax32(int& mx, int& mn) {
+  minmax_dpp<0xB1>(mx, mn);   // quad_perm(1, 0, 3, 2)
+  minmax_dpp<0x4E>(mx, mn);   // quad_perm(2, 3, 0, 1)
+  minmax_dpp<0x141>(mx, mn);  // row_half_mirror
+  minmax_dpp<0x140>(mx, mn);  // row_mirror
+  const auto a = __builtin_amdgcn_permlane16_swap((uint32_t)mx, (uint32_t)mx, false, false);
+  const auto b = __builtin_amdgcn_permlane16_swap((uint32_t)mn, (uint32_t)mn, false, false);
+  mx = max((int)a[0], (int)a[1]);
+  mn = min((int)b[0], (int)b[1]);
+}
+
 // acc + lo + hi of a packed bf16 pair (v_dot2c_f32_bf16 against (1, 1)).
 __device__ __forceinline__ float dot2_bf16_ones(uint32_t pair, float acc) {
   const bf16x2 ones = {(__bf16)1.0f, (__bf16)1.0f};

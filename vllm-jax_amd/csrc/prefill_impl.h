@@ -307,11 +307,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   {
     int mx = row_ok ? qpos : INT_MIN;
     int mn = row_ok ? qpos : INT_MAX;
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) {
-      mx = max(mx, __shfl_xor(mx, o));
-      mn = min(mn, __shfl_xor(mn, o));
-    }
+    minmax32(mx, mn);
     if (lane == 0) {
       red_max[wave] = mx;
       red_min[wave] = mn;
