@@ -38,16 +38,9 @@ decode_plan_kernel(DecodeParams p, int32_t* __restrict__ plan) {
   __syncthreads();
   // thread t < kPlanBins owns bin kPlanBins - 1 - t (largest first)
   const int local = tid < kPlanBins ? hist[kPlanBins - 1 - tid] : 0;
-  scan[tid] = local;
-  for (int o = 1; o < kPlanThreads; o <<= 1) {
-    __syncthreads();
-    const int v = tid >= o ? scan[tid - o] : 0;
-    __syncthreads();
-    scan[tid] += v;
-  }
-  __syncthreads();
-  if (tid < kPlanBins) hist[kPlanBins - 1 - tid] = scan[tid] - local;  // first rank of the bin
-  const int count = scan[kPlanThreads - 1];
+  int count;
+  const int first = block_exclusive_scan<kPlanThreads>(local, scan, count);
+  if (tid < kPlanBins) hist[kPlanBins - 1 - tid] = first;  // first rank of the bin
   __syncthreads();
   for (int64_t ii = tid; ii < pairs; ii += kPlanThreads) {
     const int i = (int)ii;

@@ -105,6 +105,26 @@ __device__ __forceinline__ float sum_xor16(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Exclusive scan over the workgroup (blockDim.x == kScanThreads) of one
+// value per thread; `tmp` is kScanThreads ints of LDS.  Returns the sum of
+// the values of lower threads; `total` receives the sum of all.
+template <int kScanThreads>
+__device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int& total) {
+  const int tid = threadIdx.x;
+  tmp[tid] = v;
+  for (int o = 1; o < kScanThreads; o <<= 1) {
+    __syncthreads();
+    const int u = tid >= o ? tmp[tid - o] : 0;
+    __syncthreads();
+    tmp[tid] += u;
+  }
+  __syncthreads();
+  total = tmp[kScanThreads - 1];
+  const int excl = tmp[tid] - v;
+  __syncthreads();
+  return excl;
+}
+
 // Max and min of `mx` / `mn` over the 32 lanes of each wave half (lanes i
 // and i ^ k, k < 32), in VALU: two quad permutations, the 8- and 16-lane
 // row mirrors (DPP), then one permlane16 swap.  Every lane ends with the

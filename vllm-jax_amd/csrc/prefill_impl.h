@@ -178,26 +178,6 @@ __device__ __forceinline__ int prefill_pair_tiles(const int4& g, int lag, int qt
   return kv_hi <= 0 ? 0 : (int)((kv_hi + kTileN - 1) / kTileN);
 }
 
-// Exclusive scan over the workgroup (blockDim.x == kScanThreads) of one
-// value per thread; `tmp` is kScanThreads ints of LDS.  Returns the sum of
-// the values of lower threads; `total` receives the sum of all.
-template <int kScanThreads>
-__device__ __forceinline__ int block_exclusive_scan(int v, int* tmp, int& total) {
-  const int tid = threadIdx.x;
-  tmp[tid] = v;
-  for (int o = 1; o < kScanThreads; o <<= 1) {
-    __syncthreads();
-    const int u = tid >= o ? tmp[tid - o] : 0;
-    __syncthreads();
-    tmp[tid] += u;
-  }
-  __syncthreads();
-  total = tmp[kScanThreads - 1];
-  const int excl = tmp[tid] - v;
-  __syncthreads();
-  return excl;
-}
-
 // A resolved work item: kv head kvh of q tile qt of sequence b, with the
 // sequence's row range and kv geometry.
 struct PrefillWork {
