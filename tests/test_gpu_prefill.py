@@ -229,3 +229,33 @@ def test_prefill_more_sequences_than_the_planner_holds(pkg, dev):
     pb = wl.make_prefill(lens, num_heads=16, num_kv_heads=8, page_size=16, rng=rng)
     print(f"prefill {pb.batch} sequences, {pb.num_tokens} tokens", flush=True)
     _prefill(pkg, dev, pb, seed=41, use_seam=False)
+
+
+@pytest.mark.parametrize("with_list", [True, False])
+def test_prefill_rows_past_max_seqlen_are_zero(pkg, dev, with_list):
+    """max_seqlen_q below a sequence's length: its rows at offset >=
+    max_seqlen_q are written as zeros (the reference's scatter covers only
+    the first max_seqlen_bucket rows, prefill...:384-388); the rows before
+    are unchanged by the truncation (causal rows see only earlier kv)."""
+    import torch
+    pb = wl.make_prefill([100, 300, 40], num_heads=16, num_kv_heads=8, page_size=64, rng=np.random.default_rng(51))
+    t = wl.materialize_prefill(pb, 51, dev)
+    kv = pkg.update_kv_cache(t["kv_cache"], t["slot_mapping"], t["k"], t["v"])
+    ws = None
+    if with_list:
+        ws = torch.empty(pkg._lib.load().pa_prefill_workspace_size(pb.batch, 128, 16, 8), dtype=torch.uint8,
+                         device=dev)
+    out = _raw_prefill(pkg, t, pb, ws, max_seqlen=128)
+    torch.cuda.synchronize()
+    got = ora.bf16_to_f32(u16(out))
+    cu = pb.cu_seqlens_q
+    kept = np.concatenate([np.arange(cu[b], min(cu[b + 1], cu[b] + 128)) for b in range(pb.batch)])
+    dropped = np.setdiff1d(np.arange(pb.num_tokens), kept)
+    assert len(dropped) == 300 - 128
+    assert not got[dropped].any()
+    kh = u16(kv)
+    ref = ora.prefill_attention(u16(t["q"]), kh[0].transpose(2, 0, 1, 3), kh[1].transpose(2, 0, 1, 3),
+                                pb.block_tables, pb.cu_seqlens_q, pb.input_positions, rows=kept)
+    err = float(np.abs(got[kept] - ora.bf16_to_f32(ref)[kept]).max())
+    print(f"truncated prefill max-abs err {err:.3e}")
+    assert err <= TOL
