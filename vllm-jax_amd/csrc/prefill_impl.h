@@ -487,14 +487,15 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     }
     // s_acc[mt][i] = S[row n][token j0 + 32mt + 8(i/4) + 4h + i%4]
     if (t >= n_free) {
+      // token j = j0 + 4h + c is visible iff j < lk and j + kv_pos_off <=
+      // qpos, i.e. iff c < lim: one compare and one select per element
+      const int64_t hi = min((int64_t)lk, (int64_t)qpos - kv_pos_off + 1) - j0 - 4 * h;
+      const int lim = (int)max((int64_t)0, min(hi, (int64_t)kTileN));
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int j = j0 + 32 * mt + 8 * (i >> 2) + 4 * h + (i & 3);
-          const bool vis = j < lk && j + kv_pos_off <= qpos;
-          s_acc[mt][i] = vis ? s_acc[mt][i] : -INFINITY;
-        }
+        for (int i = 0; i < 16; ++i)
+          s_acc[mt][i] = 32 * mt + 8 * (i >> 2) + (i & 3) < lim ? s_acc[mt][i] : -INFINITY;
     }
     // four independent max3 chains (one per 16-token quarter)
     float mq[4];
