@@ -490,7 +490,8 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
       // token j = j0 + 4h + c is visible iff j < lk and j + kv_pos_off <=
       // qpos, i.e. iff c < lim: one compare and one select per element
       const int64_t hi = min((int64_t)lk, (int64_t)qpos - kv_pos_off + 1) - j0 - 4 * h;
-      const int lim = (int)max((int64_t)0, min(hi, (int64_t)kTileN));
+      int lim = (int)max((int64_t)0, min(hi, (int64_t)kTileN));
+      asm volatile("" : "+v"(lim));  // keeps the compares 32-bit (the compiler widens them otherwise)
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -536,8 +537,8 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
       for (int e = 0; e < 4; ++e) l_part[u] = dot2_bf16_ones(w[e], l_part[u]);
       // Materialise P here: otherwise the compiler sinks the exp work past
       // the barrier into the next MFMA segment, undoing the ping-pong.
-      asm volatile("" : "+v"(w));
       pt[u] = as_bf16x8(w);
+      asm volatile("" : "+v"(pt[u]));
     }
     asm volatile("" : "+v"(l_part[0]), "+v"(l_part[1]), "+v"(l_part[2]), "+v"(l_part[3]));
   };
