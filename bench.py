@@ -517,7 +517,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this paged-attention path is built and measured on a single "
-              "MI355X (it would shard over kv heads or sequences with no exchange; see DESIGN.md). "
+              "MI355X (it would shard over kv heads or sequences with no exchange between GPUs). "
               f"--gpus {args.gpus} is not supported.", file=sys.stderr)
         sys.exit(2)
     if args.only == "copy":

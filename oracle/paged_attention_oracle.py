@@ -3,7 +3,7 @@ ragged causal GQA prefill, split-K decode).
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product package imports this
 module: only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline``
-leg of ``bench.py`` may use it, and only as the checker.  The HIP path never
+leg of ``bench.py`` may use it, and only to check results.  The HIP path never
 falls back to it.
 
 Every function restates, in numpy, the algorithm of the reference file:line
