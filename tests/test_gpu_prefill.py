@@ -66,6 +66,30 @@ def test_prefill_shapes(pkg, dev, lens, h, hkv, bs):
     _prefill(pkg, dev, pb, seed=1)
 
 
+@pytest.mark.parametrize("kind", ["permuted", "gapped", "reversed"])
+def test_prefill_noncontiguous_positions(pkg, dev, kind):
+    """Positions that are not contiguous inside a sequence.  kv index j of
+    sequence b is visible to row i iff j + positions[cu[b]] <= positions[i]
+    (prefill_paged_attention.py:79-82,108-115), so the rows of one q tile have
+    different kv limits and most tiles straddle them.  The first row keeps the
+    smallest position, so every row sees at least kv index 0."""
+    pb = wl.make_prefill([300, 97, 64, 1], num_heads=32, num_kv_heads=8, page_size=64,
+                         rng=np.random.default_rng(7))
+    rng = np.random.default_rng(11)
+    cu = pb.cu_seqlens_q
+    for b in range(len(cu) - 1):
+        q0, n = int(cu[b]), int(cu[b + 1] - cu[b])
+        p0 = int(pb.input_positions[q0])
+        if kind == "permuted":
+            rel = np.concatenate([[0], 1 + rng.permutation(n - 1)])
+        elif kind == "gapped":
+            rel = 2 * np.arange(n)
+        else:
+            rel = np.concatenate([[0], np.arange(n - 1, 0, -1)])
+        pb.input_positions[q0:q0 + n] = p0 + rel
+    _prefill(pkg, dev, pb, seed=5, use_seam=False)
+
+
 def test_prefill_engine_padding(pkg, dev):
     """Engine layout: tokens padded to a power of two (slot -1), batch padded with repeated cu_seqlens."""
     pb = wl.make_prefill([100, 23, 7], num_heads=16, num_kv_heads=8, page_size=16, num_pages=20,
