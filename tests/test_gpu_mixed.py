@@ -86,6 +86,24 @@ def test_mixed_matches_oracle(pkg, dev, dec, pre_q, pre_p, h, hkv, bs, pad):
     assert not got[zero].any()
 
 
+def test_mixed_prefill_noncontiguous_positions(pkg, dev):
+    """Prefill rows of the mixed launch with permuted positions inside their
+    sequences (the first row keeps the smallest): every row has its own kv
+    limit, so the prefill items' masked tiles vary row by row."""
+    rng = np.random.default_rng(21)
+    q, kc, vc, bt, cu, kv, pos = _case(rng, [300, 1000, 5], [200, 70, 129], [0, 90, 300], 32, 8, 64)
+    nd = 3
+    pos = pos.copy()
+    for b in range(nd, len(kv)):
+        q0, n = int(cu[b]), int(cu[b + 1] - cu[b])
+        pos[q0 + 1:q0 + n] = pos[q0] + 1 + rng.permutation(n - 1)
+    got = _run(pkg, dev, q, kc, vc, bt, cu, kv, pos, nd, 200)
+    want = ora.mixed_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, kv, pos, nd)
+    err = np.abs(ora.bf16_to_f32(got) - ora.bf16_to_f32(want)).max()
+    print(f"mixed max-abs err {err:.3e}")
+    assert err <= TOL
+
+
 def test_mixed_soft_cap_and_empty_decode_row(pkg, dev):
     """A decode sequence without a q row writes nothing (its cu_seqlens entry
     is the next sequence's row)."""
