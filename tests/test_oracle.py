@@ -202,6 +202,47 @@ def test_prefill_first_row_returns_v0_exactly():
             assert np.array_equal(got[row, hh], vc[bt[b, 0], 0, hh // 2])
 
 
+def test_prefill_rows_at_the_first_position_see_only_kv0():
+    """Every row of a sequence at the first row's position: kv j is visible
+    iff j + pos0 <= pos_i, so each row sees kv 0 alone and returns V[0]
+    exactly (prefill_paged_attention.py:79-82,108-115)."""
+    rng = np.random.default_rng(8)
+    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, [9, 30], 4, 2, 16)
+    pos = pos.copy()
+    for b in range(2):
+        pos[cu[b]:cu[b + 1]] = 100 + 7 * b
+    got = ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, pos)
+    for b in range(2):
+        for row in range(cu[b], cu[b + 1]):
+            for hh in range(4):
+                assert np.array_equal(got[row, hh], vc[bt[b, 0], 0, hh // 2])
+
+
+def test_prefill_rows_past_the_end_see_the_whole_sequence():
+    """Rows after the first at position pos0 + L - 1 see every kv token of
+    their sequence: non-causal attention, computed here in float64 from the
+    gathered K/V (q pre-scaled in bf16 as prefill_paged_attention.py:60)."""
+    rng = np.random.default_rng(9)
+    lens = [13, 40]
+    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, lens, 4, 2, 16)
+    pos = pos.copy()
+    for b, n in enumerate(lens):
+        pos[cu[b] + 1:cu[b + 1]] = pos[cu[b]] + n - 1
+    got = ora.bf16_to_f32(ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3),
+                                                bt, cu, pos))
+    kctx = ora.bf16_to_f32(ora.gather_kv(kc, bt, kvl)).astype(np.float64)
+    vctx = ora.bf16_to_f32(ora.gather_kv(vc, bt, kvl)).astype(np.float64)
+    sc = float(ora.round_bf16(np.float32(1 / math.sqrt(128))).reshape(-1)[0])
+    qs = ora.round_bf16(ora.bf16_to_f32(q) * np.float32(sc)).astype(np.float64)
+    for b, n in enumerate(lens):
+        for row in range(cu[b] + 1, cu[b + 1]):
+            for hh in range(4):
+                logits = kctx[b, :n, hh // 2] @ qs[row, hh]
+                w = np.exp(logits - logits.max())
+                want = (w / w.sum()) @ vctx[b, :n, hh // 2]
+                assert np.abs(got[row, hh] - want).max() <= BRUTE_TOL
+
+
 def test_equal_keys_give_mean_of_values():
     rng = np.random.default_rng(6)
     kc, vc = _pool(rng, 2, 64, 1)
