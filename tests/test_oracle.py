@@ -224,12 +224,16 @@ def test_prefill_rows_past_the_end_see_the_whole_sequence():
     gathered K/V (q pre-scaled in bf16 as prefill_paged_attention.py:60)."""
     rng = np.random.default_rng(9)
     lens = [13, 40]
-    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, lens, 4, 2, 16)
-    pos = pos.copy()
+    q, kc, vc, bt, cu, cuk, pos_rows, kvl = _prefill_case(rng, lens, 4, 2, 16)
+    pos = pos_rows.copy()
     for b, n in enumerate(lens):
         pos[cu[b] + 1:cu[b + 1]] = pos[cu[b]] + n - 1
     got = ora.bf16_to_f32(ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3),
                                                 bt, cu, pos))
+    # planted mistake: masking by row index (the contiguous positions) instead
+    bad = ora.bf16_to_f32(ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3),
+                                                bt, cu, pos_rows))
+    bad_err = 0.0
     kctx = ora.bf16_to_f32(ora.gather_kv(kc, bt, kvl)).astype(np.float64)
     vctx = ora.bf16_to_f32(ora.gather_kv(vc, bt, kvl)).astype(np.float64)
     sc = float(ora.round_bf16(np.float32(1 / math.sqrt(128))).reshape(-1)[0])
@@ -241,6 +245,8 @@ def test_prefill_rows_past_the_end_see_the_whole_sequence():
                 w = np.exp(logits - logits.max())
                 want = (w / w.sum()) @ vctx[b, :n, hh // 2]
                 assert np.abs(got[row, hh] - want).max() <= BRUTE_TOL
+                bad_err = max(bad_err, float(np.abs(bad[row, hh] - want).max()))
+    assert bad_err > 0.05
 
 
 def test_equal_keys_give_mean_of_values():
