@@ -139,6 +139,12 @@ __device__ __forceinline__ void dma16(const void* gptr, uint32_t lds_block) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_block) : "memory", "m0");
 }
 
+// The same from a scalar base: lane l loads the 16 bytes at sbase + voff.
+__device__ __forceinline__ void dma16s(uint32_t voff, const void* sbase, uint32_t lds_block) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_block)
+               : "memory", "m0");
+}
+
 // s_waitcnt with vmcnt = N (N < 16), lgkmcnt = 0, expcnt untouched (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vm_lgkm0() {
@@ -333,7 +339,10 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   // of them, so the loads can be spread through other work.  In the aligned
   // case the tile's page id comes in raw (read ahead of time by the caller).
   struct TileAddrs {
-    const uint16_t* g[2 * kBlk];
+    const char* kb;         // (aligned) scalar K and V bases of the tile
+    const char* vb;
+    uint32_t vo[kBlk];      // (aligned) this lane's byte offsets from them
+    const uint16_t* g[2 * kBlk];  // (unaligned) this lane's pointers
   };
   // Aligned pages hold tpp whole tiles: tile j0 = 64 (tpp lp + r) is tile r
   // of table entry lp.  The loop walks (lp, r) incrementally, so no division
@@ -350,21 +359,20 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     if constexpr (kAligned) {
       // page_size % 64 == 0: the whole tile lies in one page
       const int32_t page = raw < 0 ? 0 : (raw >= p.num_pages ? p.num_pages - 1 : raw);
+      // One scalar base per tile and a per-lane offset: no per-lane 64-bit
+      // address arithmetic on the softmax wave's path.
       const int64_t pbase = (int64_t)page * p.page_stride + rin * tile_stride + head_off;
+      a.kb = (const char*)(p.k_cache + pbase);
+      a.vb = (const char*)(p.v_cache + pbase);
       if (j0 + kTileN <= lk) {
 #pragma unroll
-        for (int i = 0; i < kBlk; ++i) {
-          a.g[2 * i] = p.k_cache + pbase + ld_off[i];
-          a.g[2 * i + 1] = p.v_cache + pbase + ld_off[i];
-        }
+        for (int i = 0; i < kBlk; ++i) a.vo[i] = 2u * ld_off[i];
       } else {
         const int last = lk - 1 - j0;  // clamp onto a valid token: masked, never stale
 #pragma unroll
         for (int i = 0; i < kBlk; ++i) {
           const int r = 4 * (kBlk * wave + i) + ld_r;
-          const int64_t o = pbase + (int64_t)min(r, last) * p.slot_stride + 8 * swz(r, ld_p);
-          a.g[2 * i] = p.k_cache + o;
-          a.g[2 * i + 1] = p.v_cache + o;
+          a.vo[i] = 2u * (uint32_t)(min(r, last) * (int32_t)p.slot_stride + 8 * swz(r, ld_p));
         }
       }
     } else {
@@ -390,8 +398,9 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   const uint32_t k_lds0 = (uint32_t)(uintptr_t)(lds_void_ptr)(&k_lds[0][0]);
   const uint32_t v_lds0 = (uint32_t)(uintptr_t)(lds_void_ptr)(&v_lds[0][0]);
   auto dma_issue = [&](const TileAddrs& a, int i, int stage) __attribute__((always_inline)) {
-    const uint32_t base = (i & 1) ? v_lds0 : k_lds0;
-    dma16(a.g[i], base + (uint32_t)(stage * kTileElems * 2 + (kBlk * wave + (i >> 1)) * 1024));
+    const uint32_t lds = ((i & 1) ? v_lds0 : k_lds0) + (uint32_t)(stage * kTileElems * 2 + (kBlk * wave + (i >> 1)) * 1024);
+    if constexpr (kAligned) dma16s(a.vo[i >> 1], (i & 1) ? a.vb : a.kb, lds);
+    else dma16(a.g[i], lds);
   };
   auto issue_tile_raw = [&](int j0, int32_t raw, int stage) __attribute__((always_inline)) {
     const TileAddrs a = tile_addrs(j0, raw, (j0 / kTileN) % tpp);
