@@ -21,6 +21,10 @@ workload, inputs resident in HBM:
   4096] + 32 prefill sequences L ~ U[64, 2048], seed 1) as one unpadded
   ``pa_mixed`` launch against the separate decode and prefill launches
   (timed in its own loop): reported under ``"mixed"``.
+* The Qwen3-0.6B single-layer prefill (4 sequences [17, 128, 300, 511], the
+  configuration the reference runs on its CPU path): GPU step time next to
+  the CPU oracle over the same whole configuration, under
+  ``"qwen3_06b_prefill"``.
 * The fused q/k RMSNorm + RoPE + KV store over the prefill workload's tokens
   (timed in its own loop after the step): reported under ``"qk_norm_rope"``
   in GB/s of algorithmic HBM traffic, (2 H + 4 Hkv) * 256 + 8 bytes a token.
@@ -178,6 +182,7 @@ def run_gpu(args):
     d_gbs_kernel = rate(d_bytes, float(d_attn.mean()), 1e9)
 
     rope = run_rope(args, torch, pkg, pb, pt, kv_p) if run_r else None
+    c1 = run_c1(args, torch, pkg, wl, dev, cpu=not args.no_cpu_baseline) if args.only is None else None
     mixed = run_mixed(args, torch, pkg, wl, dev) if run_m else None
     prefix = run_prefix(args, torch, pkg, wl, dev) if run_x else None
     if prefix is not None:
@@ -250,7 +255,10 @@ def run_gpu(args):
         rope["roofline"]["traffic"] = traffic.get("qk_norm_rope_store_kernel")
         res["qk_norm_rope"] = rope
     if mixed is not None:
+        mixed["roofline"]["traffic"] = traffic.get("mixed_kernel")
         res["mixed"] = mixed
+    if c1 is not None:
+        res["qwen3_06b_prefill"] = c1
     if prefix is not None:
         res["prefix_prefill"] = prefix
     if dec8 is not None:
@@ -390,13 +398,82 @@ def run_mixed(args, torch, pkg, wl, dev):
 
     ms_one, ms_two = timed(one), timed(two)
     flops, dbytes = pre.flops(), dec.hbm_bytes()
+    # The step is a prefill half bound by the matrix cores and a decode half
+    # bound by HBM; the serial roof is the time of each half at its own peak,
+    # added (a kernel that overlapped the halves perfectly could beat it).
+    roof_ms = (flops / (MFMA_BF16_PEAK_TFLOPS * 1e12) + dbytes / (HBM_PEAK_GBS * 1e9)) * 1e3
     return {
         "metric": "mixed step ms (one launch vs decode + prefill launches)",
         "decode_seqs": int(nd), "prefill_seqs": int(pre.batch), "tokens": int(mb.num_tokens),
         "prefill_gflop": round(flops / 1e9, 3), "decode_gb": round(dbytes / 1e9, 4),
         "one_launch_ms": round(ms_one, 4), "two_launches_ms": round(ms_two, 4),
         "speedup": round(ms_two / ms_one, 3) if ms_one > 0 else None,
+        "roofline": {"kernel": "mixed_kernel", "bound": "mfma+hbm (serial: prefill flops at the bf16 MFMA peak "
+                     "plus decode bytes at the HBM peak)", "achieved": round(ms_one, 4),
+                     "peak": round(roof_ms, 4), "unit": "ms", "frac": round(roof_ms / ms_one, 4) if ms_one > 0 else None,
+                     "traffic": None},
     }
+
+
+def run_c1(args, torch, pkg, wl, dev, cpu):
+    """The Qwen3-0.6B single-layer prefill, the configuration the reference
+    can run on its CPU path: 4 sequences [17, 128, 300, 511], 16 q / 8 kv
+    heads, a 64 x 256-token pool, seed 0.  One step = KV store of the 956 new
+    tokens + the causal prefill, on the GPU (median of the timed steps) and in
+    the CPU oracle (median of 5 runs of the same full step)."""
+    pb = wl.qwen3_06b_prefill()
+    t = wl.materialize_prefill(pb, seed=0, device=dev)
+    kv = t["kv_cache"]
+    kp, vp = kv[0].permute(2, 0, 1, 3), kv[1].permute(2, 0, 1, 3)
+    out = torch.empty_like(t["q"])
+
+    def step():
+        pkg.update_kv_cache(kv, t["slot_mapping"], t["k"], t["v"])
+        pkg.prefill_paged_attention(t["q"], kp, vp, t["block_tables"], t["cu_seqlens_q"], t["slot_mapping"],
+                                    t["input_positions"], max_seqlen_bucket=pb.max_seqlen_bucket, out=out)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    n = max(args.steps, 20)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+    for e in ev:
+        e[0].record(); step(); e[1].record()
+    torch.cuda.synchronize()
+    gpu_ms = float(np.median([e[0].elapsed_time(e[1]) for e in ev]))
+    flops = pb.flops()
+    res = {"metric": "Qwen3-0.6B single-layer prefill step (KV store + attention) TFLOP/s",
+           "q_lens": [int(x) for x in pb.q_lens], "algorithmic_gflop": round(flops / 1e9, 4),
+           "gpu_step_ms": round(gpu_ms, 4), "gpu_tflops": round(flops / (gpu_ms * 1e-3) / 1e12, 3)}
+    if cpu:
+        from oracle import paged_attention_oracle as ora
+        u16 = lambda x: x.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+        kc0, vc0 = u16(kv[0]), u16(kv[1])
+        qh, kh, vh = u16(t["q"]), u16(t["k"]), u16(t["v"])
+        times = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            kc, vc = ora.kv_store(kc0, vc0, kh, vh, pb.slot_mapping)
+            ora.prefill_attention(qh, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), pb.block_tables,
+                                  pb.cu_seqlens_q, pb.input_positions)
+            times.append(time.perf_counter() - t0)
+        cpu_s = float(np.median(times))
+        threads = _blas_threads()
+        res["cpu_baseline"] = {"value": round(flops / cpu_s / 1e12, 6), "unit": "TFLOP/s", "cores": threads,
+                               "kind": "port", "step_ms": round(cpu_s * 1e3, 2),
+                               "sample": f"the whole configuration: CPU oracle (numpy, {threads} BLAS threads of "
+                                         f"{os.cpu_count()} host CPUs) KV store + prefill, median of 5 runs "
+                                         f"({', '.join(f'{x * 1e3:.0f}' for x in times)} ms)"}
+        res["gpu_over_cpu"] = round(cpu_s * 1e3 / gpu_ms, 1)
+    return res
+
+
+def _blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+        return int(max([i.get("num_threads", 1) for i in threadpool_info()] or [1]))
+    except Exception:  # pragma: no cover
+        return 1
 
 
 def run_rope(args, torch, pkg, pb, pt, kv):
@@ -436,15 +513,15 @@ def run_rope(args, torch, pkg, pb, pt, kv):
 
 
 def cpu_baseline(pb, pt, db, dt_, budget_s):
-    """Time the CPU oracle on bounded samples of the two workloads (host cores)."""
+    """Time the CPU oracle on bounded samples of the two workloads (host
+    cores).  Each sample is sized so that one run takes about a sixth of the
+    budget, then run 3 times; the median is reported."""
     import torch
     from oracle import paged_attention_oracle as ora
-    try:
-        from threadpoolctl import threadpool_info
-        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        threads = 1
+    threads = _blas_threads()
     u16 = lambda x: x.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+    runs = 3
+    per_run = budget_s / (2 * runs)
 
     # prefill sample: the last R q rows of the shortest sequence, against its whole context
     b = int(np.argmin(pb.q_lens))
@@ -458,24 +535,29 @@ def cpu_baseline(pb, pt, db, dt_, budget_s):
     bt = np.arange(n_pages, dtype=np.int32)[None]
     cu = np.array([0, q1 - q0], np.int32)
     pos = pb.input_positions[q0:q1]
-    rows_n, spent, flops = 8, 0.0, 0
+    rows_n = 8
     while True:
         rows = np.arange(q1 - q0 - rows_n, q1 - q0)
         t0 = time.perf_counter()
         ora.prefill_attention(qh, kp, vp, bt, cu, pos, rows=rows)
         dt = time.perf_counter() - t0
-        if dt * 2.2 > budget_s / 2 or rows_n >= 4096:
-            spent, flops, used_rows = dt, 4 * pb.head_dim * pb.num_heads * int((pos[rows] + 1).sum()), rows_n
+        if dt * 2.2 > per_run or rows_n >= 4096:
             break
         rows_n *= 2
+    times = [dt]
+    for _ in range(runs - 1):
+        t0 = time.perf_counter()
+        ora.prefill_attention(qh, kp, vp, bt, cu, pos, rows=rows)
+        times.append(time.perf_counter() - t0)
+    spent = float(np.median(times))
+    flops = 4 * pb.head_dim * pb.num_heads * int((pos[rows] + 1).sum())
     p_val = flops / spent / 1e12
 
     # decode sample: the first S sequences
-    s_n, d_spent, d_bytes = 2, 0.0, 0
+    s_n = 2
     kvd = dt_["kv_cache"]
     qd = dt_["q"]
     while True:
-        seqs = np.arange(s_n)
         used = sorted(set(int(x) for x in db.block_tables[:s_n].ravel() if x >= 0))
         remap = {blk: i for i, blk in enumerate(used)}
         bt_s = np.array([[remap.get(int(x), 0) if x >= 0 else -1 for x in row] for row in db.block_tables[:s_n]],
@@ -487,20 +569,27 @@ def cpu_baseline(pb, pt, db, dt_, budget_s):
         t0 = time.perf_counter()
         ora.decode_attention(qs, kp_s, vp_s, bt_s, db.context_lens[:s_n])
         dt = time.perf_counter() - t0
-        if dt * 2.2 > budget_s / 2 or s_n >= db.batch:
-            d_spent = dt
-            d_bytes = int(db.context_lens[:s_n].sum()) * 2 * db.num_kv_heads * db.head_dim * 2
+        if dt * 2.2 > per_run or s_n >= db.batch:
             break
         s_n = min(s_n * 2, db.batch)
+    d_times = [dt]
+    for _ in range(runs - 1):
+        t0 = time.perf_counter()
+        ora.decode_attention(qs, kp_s, vp_s, bt_s, db.context_lens[:s_n])
+        d_times.append(time.perf_counter() - t0)
+    d_spent = float(np.median(d_times))
+    d_bytes = int(db.context_lens[:s_n].sum()) * 2 * db.num_kv_heads * db.head_dim * 2
     d_val = d_bytes / d_spent / 1e9
     ncpu = os.cpu_count()
+    fmt = lambda ts: ", ".join(f"{x:.2f}" for x in ts)
     return (
         {"value": round(p_val, 6), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
          "sample": f"CPU oracle (numpy, {threads} BLAS threads of {ncpu} host CPUs): prefill of the last "
-                   f"{used_rows} q rows of the {q1 - q0}-token sequence against its whole causal context, "
-                   f"{flops / 1e9:.1f} GFLOP in {spent:.1f} s"},
+                   f"{rows_n} q rows of the {q1 - q0}-token sequence against its whole causal context, "
+                   f"{flops / 1e9:.1f} GFLOP, median of {runs} runs ({fmt(times)} s)"},
         {"value": round(d_val, 4), "unit": "GB/s", "cores": int(threads), "kind": "port",
-         "sample": f"CPU oracle decode of the first {s_n} sequences ({d_bytes / 1e9:.3f} GB KV) in {d_spent:.1f} s"},
+         "sample": f"CPU oracle decode of the first {s_n} sequences ({d_bytes / 1e9:.3f} GB KV), median of "
+                   f"{runs} runs ({fmt(d_times)} s)"},
     )
 
 

@@ -264,7 +264,15 @@ def prefill_attention(q, k_pages, v_pages, block_tables, cu_seqlens,
         ``pos0_b = input_positions[cu[b]]`` and is visible to row i iff
         ``j < L_b`` and ``j + pos0_b <= input_positions[i]``;
       * GQA: q head h reads kv head ``h // G`` (prefill...:209-211);
-      * rows outside every sequence are 0.
+      * rows outside every sequence are 0;
+      * a row of a sequence that sees no kv index (its position precedes the
+        sequence's first kv position) is 0, the value the reference's dense
+        definition gives it (prefill...:502, qwen3.py:166).  The Pallas
+        kernel differs there: its finite ``mask_value`` with ``m`` starting
+        at ``f32.min`` (prefill...:62-64,109-117) weighs every token of the
+        loaded compute blocks equally, a mean of V that includes tokens past
+        the sequence.  The engine never builds such a row (positions run
+        0, 1, 2, ... per sequence, model_runner.py:228).
 
     ``cu_seqlens_k`` (optional) extends the reference to a cached prefix: the
     kv length becomes ``Lk_b = cu_k[b+1]-cu_k[b]`` and kv index j has position
@@ -339,6 +347,7 @@ def prefill_attention(q, k_pages, v_pages, block_tables, cu_seqlens,
                 page_size=bs, used_tokens=lk, soft_cap=soft_cap,
                 mask_value=mask_value, k_scale=k_sc, v_scale=v_sc)
             res = _merge_splits(o_p, l_p, m_p)
+            res = np.where(vmask.any(axis=1)[:, None], res, np.float32(0))  # rows with no visible key
             out[sel, kh * g:(kh + 1) * g] = res.reshape(sel.size, g, d)
     return f32_to_bf16(out)
 

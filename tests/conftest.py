@@ -57,3 +57,37 @@ def u16(t):
 def from_u16(a, device):
     import torch
     return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).to(device)
+
+
+def boundary_rows(cu_seqlens, prefix_lens, rng, *, tile_tokens, page_size=256, kv_tile=64, per_seq=10):
+    """q rows to check at full size, spread over every sequence.
+
+    For each sequence (q rows cu[b] .. cu[b+1]-1, kv position of row i is
+    prefix_b + i): its first, second, middle and last row; the rows on both
+    sides of a q-tile edge (offsets k*tile_tokens - 1 and k*tile_tokens) and
+    of a kv page edge and a 64-token kv tile edge (position % page_size and
+    % kv_tile in {size - 1, 0}), a few of each picked at random; and random
+    interior rows, up to ``per_seq`` rows per sequence in total."""
+    cu = np.asarray(cu_seqlens, np.int64)
+    out = []
+    for b in range(len(cu) - 1):
+        q0, n = int(cu[b]), int(cu[b + 1] - cu[b])
+        if n <= 0:
+            continue
+        p = int(prefix_lens[b]) if prefix_lens is not None else 0
+        fixed = {0, min(1, n - 1), n // 2, n - 1}
+        cand = set()
+        for step, base in ((tile_tokens, 0), (page_size, p), (kv_tile, p)):
+            # offsets o with (base + o) % step in {step - 1, 0}
+            first = (-base) % step
+            edges = np.arange(first, n, step)
+            edges = np.concatenate([edges, edges - 1])
+            edges = edges[(edges >= 0) & (edges < n)]
+            if edges.size:
+                cand.update(int(x) for x in rng.choice(edges, size=min(2, edges.size), replace=False))
+        rows = sorted(fixed | cand)
+        extra = max(0, per_seq - len(rows))
+        if extra and n > len(rows):
+            rows = sorted(set(rows) | set(int(x) for x in rng.integers(0, n, extra)))
+        out.extend(q0 + r for r in rows)
+    return np.unique(np.asarray(out, np.int64))

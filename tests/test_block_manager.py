@@ -199,3 +199,46 @@ def test_fork_then_decode_copies_the_shared_tail():
     m.deallocate(parent)
     m.deallocate(child)
     assert m.num_free_blocks == 10
+
+
+def test_refused_prefill_after_prefix_hit_changes_nothing():
+    # Sequence 2 would take two cached blocks and then needs more free blocks
+    # than there are: the refusal must leave tables, reference counts and the
+    # free queue as they were, and a later retry must find the prefix again.
+    bs = 4
+    m = KVCacheManager(5, bs, enable_prefix_caching=True)
+    p = list(range(100, 109))                              # 9 tokens: 2 full blocks + 1 partial
+    a = Req(p)
+    m.allocate_slots(a, True)
+    ta = m.block_ids(a)
+    assert [m.ref_count(x) for x in range(5)] == [1, 1, 1, 0, 0] and m.num_free_blocks == 2
+    big = Req(p[:8] + list(range(500, 509)))               # 17 tokens: 2 hits + 3 new > 2 free
+    assert not m.can_allocate(big, True)
+    with pytest.raises(IndexError):
+        m.allocate_slots(big, True)
+    assert m.block_ids(big) == [] and m.num_free_blocks == 2
+    assert [m.ref_count(x) for x in range(5)] == [1, 1, 1, 0, 0]
+    m.deallocate(a)
+    assert m.num_free_blocks == 5 and [m.ref_count(x) for x in range(5)] == [0] * 5
+    # the retry fits now and still finds the two cached blocks
+    assert m.can_allocate(big, True)
+    m.allocate_slots(big, True)
+    assert m.block_ids(big)[:2] == ta[:2] and m.num_cached_tokens(big) == 8
+
+
+def test_refused_decode_with_copy_on_write_changes_nothing():
+    # A forked sequence whose next token both falls into a shared block and
+    # opens a new one needs two free blocks; with one free the call must fail
+    # before the copy-on-write moves anything.
+    bs = 4
+    m = KVCacheManager(3, bs)
+    parent = Req(range(7))                                 # blocks [0, 1], block 1 holds 3 tokens
+    m.allocate_slots(parent, True)
+    child = Req(range(7))
+    m.fork(parent, child)
+    child.token_ids.append(1)                              # 8 tokens: writes block 1 (shared), 8 % 4 == 0
+    assert not m.can_allocate(child, False)
+    with pytest.raises(IndexError):
+        m.allocate_slots(child, False)
+    assert m.block_ids(child) == [0, 1] and m.take_block_copies() == ([], [])
+    assert [m.ref_count(x) for x in range(3)] == [2, 2, 0] and m.num_free_blocks == 1

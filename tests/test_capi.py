@@ -146,6 +146,38 @@ def test_mixed_workspace_size():
     assert lib.pa_mixed_workspace_size(5, 3, 300, 16, 8, 128, 40, 256) == part + 256 + 32 * 16
     assert lib.pa_mixed_workspace_size(5, 6, 300, 16, 8, 128, 40, 256) == 0   # more decodes than sequences
     assert lib.pa_mixed_workspace_size(5, 3, 300, 15, 8, 128, 40, 256) == 0   # heads not a multiple of kv heads
+    # pages above 4096 tokens: 4096-token chunks inside one page (2 per 8192-token page)
+    part = r256(2 * 16 * 2 * (128 + 2) * 4)
+    assert lib.pa_mixed_workspace_size(4, 2, 100, 16, 8, 128, 1, 8192) == part + 256 + 32 * 8
+    assert lib.pa_mixed_workspace_size(4, 2, 100, 16, 8, 128, 1, 4096) == 256 + 32 * 8
+    # more than 16 q heads per kv head is refused (pa_mixed refuses it too)
+    assert lib.pa_mixed_workspace_size(4, 2, 100, 512, 1, 128, 8, 256) == 0
+    assert lib.pa_mixed_workspace_size(4, 2, 100, 32, 1, 128, 8, 256) == 0
+
+
+def test_large_slot_stride_is_refused_by_the_aligned_tile_loads():
+    # The aligned prefill tile loads use 32-bit per-lane offsets of up to
+    # 63 * slot_stride + 127 elements: a larger stride (e.g. a [BS, NB, Hkv, d]
+    # pool view with NB >= 32768) must be refused, not wrapped.
+    lib = PKG._lib.load()
+    fake = 1 << 20
+    big = 0x7fffffff // 63 + 8          # first multiple-of-8 stride past the limit
+    big -= big % 8
+    ok = (0x7fffffff - 127) // 63 // 8 * 8
+    def prefill(ss, page_size=256):
+        args = [fake, 2048, 128, fake, fake, 16, page_size, 262144, ss, 128, fake, 4, 4, fake, None, fake,
+                2, 100, 64, 16, 8, 128, 0.088, 0.0, fake, 2048, 128, None, 0, None]
+        return lib.pa_prefill(*args)
+    assert prefill(big) == -2
+    assert "slot stride" in lib.pa_last_error().decode()
+    assert prefill(-8) == -2
+    def mixed(ss):
+        return lib.pa_mixed(fake, 2048, 128, fake, fake, 16, 256, 262144, ss, 128, fake, 4, 4, fake, fake, fake,
+                            3, 1, 100, 64, 16, 8, 128, 0.088, 1.0, 0.0, fake, 2048, 128, fake, 0, None)
+    assert mixed(big) == -2
+    assert "slot stride" in lib.pa_last_error().decode()
+    # the largest stride that fits passes this check and stops at the next one (workspace)
+    assert mixed(ok) == -3
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

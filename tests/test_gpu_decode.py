@@ -106,11 +106,9 @@ def test_decode_reference_layout_and_no_lengths(pkg, dev):
 
 
 def test_decode_qwen3_8b_full(pkg, dev):
-    """Full Qwen3-8B decode workload (256 seqs, ctx U[512,8192]); oracle on a sample of sequences."""
+    """Full Qwen3-8B decode workload (256 seqs, ctx U[512,8192]); every sequence against the oracle."""
     db = wl.qwen3_8b_decode()
-    order = np.argsort(db.context_lens)
-    seqs = np.unique(np.concatenate([order[:3], order[-3:], [0, 100, 200]]))
-    _run_and_check(pkg, dev, db, seed=2, seqs=seqs)
+    _run_and_check(pkg, dev, db, seed=2)
 
 
 def test_decode_through_attention_seam(pkg, dev):

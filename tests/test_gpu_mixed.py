@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import vllm_jax_amd.workloads as wl
-from conftest import from_u16, u16
+from conftest import boundary_rows, from_u16, u16
 from oracle import paged_attention_oracle as ora
 
 pytestmark = pytest.mark.gpu
@@ -149,16 +149,18 @@ def test_mixed_qwen3_06b_step_through_seam(pkg, dev):
     kc, vc = u16(kv_cache[0]), u16(kv_cache[1])
     qh = u16(t["q"])
     nd = mb.num_decodes
-    dseq = [0, 1, int(np.argmax(dec.context_lens)), int(np.argmin(dec.context_lens)), nd - 1]
-    ps = nd + int(np.argmax(pre.q_lens))
-    pr = [int(mb.cu_seqlens_q[nd]), int(mb.cu_seqlens_q[ps]), int(mb.cu_seqlens_q[ps + 1]) - 1,
-          int(mb.cu_seqlens_q[-1]) - 1]
+    # every decode row, and >= 256 prefill rows: each prefill sequence's first,
+    # last and middle rows and rows on q-tile / kv-tile / page edges
+    dseq = np.arange(nd)
+    pr = boundary_rows(mb.cu_seqlens_q[nd:], None, np.random.default_rng(1),
+                       tile_tokens=256 // (pre.num_heads // pre.num_kv_heads), per_seq=10)
+    assert pr.size >= 256
     want = ora.mixed_attention(qh, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), mb.block_tables,
                                mb.cu_seqlens_q, mb.kv_lens, mb.input_positions, nd, prefill_rows=pr,
                                decode_seqs=dseq)
     rows = np.concatenate([mb.cu_seqlens_q[dseq], pr])
     err = np.abs(ora.bf16_to_f32(got[rows]) - ora.bf16_to_f32(want[rows])).max()
-    print(f"mixed step max-abs err {err:.3e} over {len(rows)} sampled rows")
+    print(f"mixed step max-abs err {err:.3e} over {nd} decode rows and {pr.size} prefill rows", flush=True)
     assert err <= TOL
     # against the separate decode and prefill entries on the whole step
     kp, vp = kv_cache[0].permute(2, 0, 1, 3), kv_cache[1].permute(2, 0, 1, 3)

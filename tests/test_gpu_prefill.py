@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 
 import vllm_jax_amd.workloads as wl
-from conftest import u16
+from conftest import boundary_rows, u16
 from oracle import paged_attention_oracle as ora
 
 pytestmark = pytest.mark.gpu
@@ -90,6 +90,27 @@ def test_prefill_noncontiguous_positions(pkg, dev, kind):
     _prefill(pkg, dev, pb, seed=5, use_seam=False)
 
 
+def test_prefill_rows_before_the_first_kv_position_are_zero(pkg, dev):
+    """Rows whose position precedes their sequence's first kv position see no
+    key and are written as zeros (the contract of the reference's dense
+    definition, prefill_paged_attention.py:502); every other row matches the
+    oracle.  Covers q tiles where such rows sit next to rows that see keys."""
+    pb = wl.make_prefill([300, 97, 40], num_heads=32, num_kv_heads=8, page_size=64,
+                         rng=np.random.default_rng(13))
+    cu = pb.cu_seqlens_q
+    blind = []
+    for b in range(len(cu) - 1):
+        q0, n = int(cu[b]), int(cu[b + 1] - cu[b])
+        p0 = 1000 * (b + 1)
+        pb.input_positions[q0:q0 + n] = p0 + np.arange(n)
+        lo = q0 + n // 3
+        hi = lo + max(1, n // 5)
+        pb.input_positions[lo:hi] = p0 - 1 - np.arange(hi - lo)   # before kv position p0
+        blind.extend(range(lo, hi))
+    got, _ = _prefill(pkg, dev, pb, seed=6, use_seam=False)
+    assert not got[np.asarray(blind)].any()
+
+
 def test_prefill_engine_padding(pkg, dev):
     """Engine layout: tokens padded to a power of two (slot -1), batch padded with repeated cu_seqlens."""
     pb = wl.make_prefill([100, 23, 7], num_heads=16, num_kv_heads=8, page_size=16, num_pages=20,
@@ -112,32 +133,47 @@ def test_prefill_prefix_cached_small(pkg, dev):
 
 
 def test_prefill_qwen3_8b_prefix_workload(pkg, dev):
-    """Full Qwen3-8B prefix-cached workload; oracle on sampled rows (incl. every sequence's last row)."""
+    """Full Qwen3-8B prefix-cached workload (64 sequences, cached prefixes
+    U[0, 4096], new chunks U[128, 1024]); oracle on the first and last new row
+    of every sequence plus rows on q-tile, kv-tile and page edges."""
     pb = wl.qwen3_8b_prefix_prefill()
     rng = np.random.default_rng(0)
-    rows = np.unique(np.concatenate([pb.cu_seqlens_q[1:] - 1, rng.integers(0, pb.num_tokens, 32)]))
+    prefix = np.diff(pb.cu_seqlens_k) - np.diff(pb.cu_seqlens_q)
+    rows = boundary_rows(pb.cu_seqlens_q, prefix, rng, tile_tokens=256 // (pb.num_heads // pb.num_kv_heads),
+                         per_seq=6)
+    cu = pb.cu_seqlens_q
+    assert set(cu[:-1]) <= set(rows) and set(cu[1:] - 1) <= set(rows)
+    print(f"qwen3-8b prefix-cached: {rows.size} rows over {pb.batch} sequences", flush=True)
     _prefill(pkg, dev, pb, seed=3, rows=rows)
 
 
 def test_prefill_qwen3_06b_mixed_prefill_half(pkg, dev):
+    """The 32 prefill sequences of the Qwen3-0.6B mixed step: first, last and
+    edge rows of every sequence (>= 256 rows)."""
     pre, _ = wl.qwen3_06b_mixed()
     rng = np.random.default_rng(1)
-    rows = np.unique(np.concatenate([pre.cu_seqlens_q[1:] - 1, pre.cu_seqlens_q[:-1], rng.integers(0, pre.num_tokens, 64)]))
+    rows = boundary_rows(pre.cu_seqlens_q, None, rng, tile_tokens=256 // (pre.num_heads // pre.num_kv_heads),
+                         per_seq=10)
+    assert rows.size >= 256
     _prefill(pkg, dev, pre, seed=1, rows=rows)
 
 
 def test_prefill_qwen3_32b_long(pkg, dev):
     """Full Qwen3-32B long-context workload (8 seqs of 8k-32k tokens).
 
-    Oracle on sampled rows of two sequences, plus a full-size property: the
-    last row of every sequence must equal a decode over that sequence's
-    whole context with the same q (both on the GPU).
+    Oracle on 10 rows of every sequence (first, second, middle, last, rows on
+    both sides of 32-token q-tile, 64-token kv-tile and 256-token page edges,
+    random interior rows), plus a full-size property: the last row of every
+    sequence must equal a decode over that sequence's whole context with the
+    same q (both on the GPU).
     """
     import torch
     pb = wl.qwen3_32b_long_prefill()
     cu = pb.cu_seqlens_q
-    b_small = int(np.argmin(pb.q_lens))
-    rows = np.array([cu[b_small], cu[b_small] + 1, cu[b_small] + 700, cu[b_small + 1] - 1, cu[1] - 1])
+    rows = boundary_rows(cu, None, np.random.default_rng(4), tile_tokens=256 // (pb.num_heads // pb.num_kv_heads),
+                         per_seq=10)
+    assert rows.size >= 64
+    print(f"qwen3-32b long prefill: {rows.size} rows over {pb.batch} sequences", flush=True)
     got, t = _prefill(pkg, dev, pb, seed=4, rows=rows)
     kv = t["kv_cache"]
     last = torch.as_tensor(cu[1:] - 1, dtype=torch.long, device=dev)

@@ -249,6 +249,35 @@ def test_prefill_rows_past_the_end_see_the_whole_sequence():
     assert bad_err > 0.05
 
 
+def test_prefill_rows_before_the_first_kv_position_are_zero():
+    """A row whose position precedes its sequence's first kv position sees no
+    key.  Contract: the row is 0, as the reference's dense definition gives it
+    (prefill_paged_attention.py:502, qwen3.py:166); the Pallas kernel's finite
+    mask_value (prefill...:62-64,109-117) would give a mean of V over its
+    loaded blocks instead.  Both oracle forms must agree on 0, and the other
+    rows must still match float64 attention."""
+    rng = np.random.default_rng(12)
+    lens = [20, 9]
+    q, kc, vc, bt, cu, cuk, pos, kvl = _prefill_case(rng, lens, 4, 2, 16)
+    pos = pos.copy()
+    # sequence 0: row 0 keeps position 50; rows 5..9 drop below it (no key)
+    pos[cu[0]:cu[1]] = 50 + np.arange(20)
+    pos[cu[0] + 5:cu[0] + 10] = 40 + np.arange(5)
+    blind = np.arange(cu[0] + 5, cu[0] + 10)
+    got = ora.prefill_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, pos)
+    assert not got[blind].any()
+    kctx, vctx = ora.gather_kv(kc, bt, kvl), ora.gather_kv(vc, bt, kvl)
+    sc = float(ora.round_bf16(np.float32(1 / math.sqrt(128))).reshape(-1)[0])
+    qs = ora.f32_to_bf16(ora.round_bf16(ora.bf16_to_f32(q) * np.float32(sc)))
+    want = ora.dense_prefill_f64(qs, kctx, vctx, cu, pos, scale=1.0)
+    assert not want[blind].any()
+    assert np.abs(ora.bf16_to_f32(got) - want).max() <= BRUTE_TOL
+    # the kernel-faithful alternative (finite mask value, no zeroing) is
+    # what the contract rules out: it gives a nonzero mean of V there
+    mean_v = ora.bf16_to_f32(vc[bt[0, :2]].reshape(32, 2, 128))[:20].mean(axis=0)
+    assert np.abs(mean_v).max() > 0.05
+
+
 def test_equal_keys_give_mean_of_values():
     rng = np.random.default_rng(6)
     kc, vc = _pool(rng, 2, 64, 1)

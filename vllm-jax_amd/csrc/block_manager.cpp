@@ -201,23 +201,23 @@ extern "C" int pa_bm_allocate(pa_block_manager* h, int64_t seq_id, const int32_t
   const int32_t bs = m.block_size;
   if (is_prefill) {
     // :46-51, with cached leading blocks taken first
+    // Every check comes before the first change of state: a refused
+    // allocation leaves the table, the reference counts and the queue as
+    // they were (as pa_bm_can_allocate counts it).
     const int64_t needed = ((int64_t)num_tokens + bs - 1) / bs;
-    if (s.table.empty()) {
-      std::vector<int32_t> hits;
-      m.prefix_hits(token_ids, num_tokens, &hits);
-      for (int32_t c : hits) {
-        if (m.in_free[c]) m.unlink(c);
-        ++m.ref[c];
-        s.table.push_back(c);
-      }
-      s.cached_tokens = (int32_t)hits.size() * bs;
-    } else {
-      s.cached_tokens = 0;
-    }
-    int64_t from_free = needed - (int64_t)s.table.size();
+    std::vector<int32_t> hits;
+    if (s.table.empty()) m.prefix_hits(token_ids, num_tokens, &hits);
+    int64_t from_free = needed - (int64_t)s.table.size() - (int64_t)hits.size();
+    for (int32_t c : hits) from_free += m.in_free[c];  // a free cached block leaves the queue too
     if (from_free > m.nfree)
       return fail(PA_ERR_INVALID_ARGUMENT, "pa_bm_allocate: %lld blocks needed, %d free", (long long)from_free,
                   m.nfree);
+    for (int32_t c : hits) {
+      if (m.in_free[c]) m.unlink(c);
+      ++m.ref[c];
+      s.table.push_back(c);
+    }
+    s.cached_tokens = (int32_t)hits.size() * bs;
     while ((int64_t)s.table.size() < needed) {
       const int32_t b = m.pop_front();
       ++m.ref[b];
@@ -239,8 +239,12 @@ extern "C" int pa_bm_allocate(pa_block_manager* h, int64_t seq_id, const int32_t
   if (s.table.empty())
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_bm_allocate: decode of sequence %lld without blocks", (long long)seq_id);
   const int64_t idx = ((int64_t)num_tokens - 1) / bs;
-  if (num_tokens > 0 && idx < (int64_t)s.table.size() && m.ref[s.table[idx]] > 1) {
-    if (m.nfree == 0) return fail(PA_ERR_INVALID_ARGUMENT, "pa_bm_allocate: no free block for copy-on-write");
+  const bool cow = num_tokens > 0 && idx < (int64_t)s.table.size() && m.ref[s.table[idx]] > 1;
+  const int32_t want = (cow ? 1 : 0) + (num_tokens % bs == 0 ? 1 : 0);
+  if (want > m.nfree)
+    return fail(PA_ERR_INVALID_ARGUMENT, "pa_bm_allocate: %d blocks needed (copy-on-write %d), %d free", want,
+                cow ? 1 : 0, m.nfree);
+  if (cow) {
     const int32_t old = s.table[idx];
     const int32_t b = m.pop_front();
     ++m.ref[b];
@@ -250,7 +254,6 @@ extern "C" int pa_bm_allocate(pa_block_manager* h, int64_t seq_id, const int32_t
     m.copy_dst.push_back(b);
   }
   if (num_tokens % bs == 0) {
-    if (m.nfree == 0) return fail(PA_ERR_INVALID_ARGUMENT, "pa_bm_allocate: no free block");
     const int32_t b = m.pop_front();
     ++m.ref[b];
     s.table.push_back(b);

@@ -243,9 +243,11 @@ static_assert(sizeof(float) * kMixedDecodeWaves * 16 * kPHeadDim <= sizeof(uint1
 // Tokens per decode item (a multiple of the 16-token step): eight waves take
 // up to twice the chunk of the four-wave decode kernel.  With 16-aligned pages
 // the chunk is whole pages, at most 64 of them (one page id per lane).
+// Pages above 4096 tokens get 4096-token chunks inside one page (the
+// aligned decode item walks a chunk that starts inside a page).
 static int mixed_decode_chunk(int page_size) {
   constexpr int kMax = 4096;
-  if (page_size % kDecodeStep != 0) return kMax;
+  if (page_size % kDecodeStep != 0 || page_size >= kMax) return kMax;
   return 64 * page_size <= kMax ? 64 * page_size : (kMax / page_size) * page_size;
 }
 
@@ -282,7 +284,8 @@ extern "C" size_t pa_mixed_workspace_size(int32_t batch, int32_t num_decodes, in
                                           int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                           int32_t pages_per_seq, int32_t page_size) {
   if (batch < 0 || num_decodes < 0 || num_decodes > batch || max_seqlen_q < 0 || num_heads <= 0 ||
-      num_kv_heads <= 0 || num_heads % num_kv_heads || head_dim <= 0 || pages_per_seq < 0 || page_size <= 0)
+      num_kv_heads <= 0 || num_heads % num_kv_heads || num_heads / num_kv_heads > 16 || head_dim <= 0 ||
+      pages_per_seq < 0 || page_size <= 0)
     return 0;
   const int chunks = pages_per_seq > 0 ? mixed_decode_chunks(pages_per_seq, page_size) : 0;
   const int64_t pairs = mixed_pairs(batch, num_decodes, max_seqlen_q, num_heads, num_kv_heads, pages_per_seq,
@@ -328,6 +331,9 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
     return fail(PA_ERR_UNSUPPORTED, "pa_mixed: operands must be 16-byte aligned with strides multiple of 8");
   if ((int64_t)pages_per_seq * page_size > 0x7fffffffLL)
     return fail(PA_ERR_UNSUPPORTED, "pa_mixed: block table spans more than 2^31 tokens");
+  if (page_size % kTileN == 0 && !prefill_offsets_fit(slot_stride))
+    return fail(PA_ERR_UNSUPPORTED, "pa_mixed: slot stride %lld too large for 32-bit tile offsets (max %lld)",
+                (long long)slot_stride, (long long)((0x7fffffffLL - (kPHeadDim - 1)) / (kTileN - 1)));
   const int n_chunks = pages_per_seq > 0 ? mixed_decode_chunks(pages_per_seq, page_size) : 0;
   const size_t need = pa_mixed_workspace_size(batch, num_decodes, max_seqlen_q, num_heads, num_kv_heads, head_dim,
                                               pages_per_seq, page_size);

@@ -205,6 +205,9 @@ static int prefill_launch(const char* name, const uint16_t* q, int64_t q_tok_str
   if ((align_bits & 15u) || (q_tok_stride | q_head_stride | page_stride | slot_stride | head_stride |
                              out_tok_stride | out_head_stride) % 8)
     return fail(PA_ERR_UNSUPPORTED, "%s: operands must be 16-byte aligned with strides multiple of 8", name);
+  if (page_size % kTileN == 0 && !prefill_offsets_fit(slot_stride))
+    return fail(PA_ERR_UNSUPPORTED, "%s: slot stride %lld too large for 32-bit tile offsets (max %lld)", name,
+                (long long)slot_stride, (long long)((0x7fffffffLL - (kPHeadDim - 1)) / (kTileN - 1)));
   if (workspace) {
     const size_t need = pa_prefill_workspace_size(batch, max_seqlen_q, num_heads, num_kv_heads);
     if (workspace_bytes < need || ((uintptr_t)workspace & 255u))

@@ -161,6 +161,14 @@ static __shared__ __attribute__((aligned(1024))) uint16_t k_lds[kStages][kTileEl
 static __shared__ __attribute__((aligned(1024))) uint16_t v_lds[kStages][kTileElems];
 static __shared__ int red_max[kWaves], red_min[kWaves];
 
+// The aligned tile loads address a K/V row as a 32-bit per-lane offset from
+// a scalar page base: tile row r (< 64) plus a 16-byte chunk (< 128 elements)
+// is r * slot_stride + 8 * chunk elements, 2x that in bytes.  True when that
+// fits int32 for every row (so the byte offset fits uint32 as well).
+inline bool prefill_offsets_fit(int64_t slot_stride) {
+  return slot_stride >= 0 && (kTileN - 1) * slot_stride + kPHeadDim - 1 <= (int64_t)0x7fffffff;
+}
+
 // Row range and kv geometry of prefill sequence b, as prefill_resolve
 // derives them without a work list: g = (q0, lq_rows, lk, kv_pos_off), and
 // lag = lk - lq (kv index of the first q row when positions are contiguous).
@@ -328,7 +336,10 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   const int ld_r = lane >> 4;            // row within a 1 KiB block
   const int ld_p = lane & 15;            // physical chunk
   const int64_t head_off = (int64_t)kvh * p.head_stride;
-  uint32_t ld_off[kBlk];                 // per-lane element offset of the row within a page
+  // per-lane element offset of the row within a page; the host guarantees
+  // 63 * slot_stride + 127 <= INT32_MAX (prefill_offsets_fit), so neither
+  // this nor the byte offset 2 * ld_off below wraps
+  uint32_t ld_off[kBlk];
 #pragma unroll
   for (int i = 0; i < kBlk; ++i) {
     const int r = 4 * (kBlk * wave + i) + ld_r;
@@ -351,7 +362,9 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   const int64_t tile_stride = (int64_t)kTileN * p.slot_stride;
   auto page_raw_at = [&](int lp) __attribute__((always_inline)) {
     const __attribute__((address_space(4))) int32_t* c = (const __attribute__((address_space(4))) int32_t*)bt_row;
-    return c[min(lp, p.pages_per_seq - 1)];  // stays inside the table row
+    // stays inside the table row; an empty row (pages_per_seq == 0, every
+    // row then sees no key and loads no tile) reads nothing
+    return p.pages_per_seq > 0 ? c[min(lp, p.pages_per_seq - 1)] : 0;
   };
   // rin: (aligned) the tile's index inside its page
   auto tile_addrs = [&](int j0, int32_t raw, int rin) __attribute__((always_inline)) {
