@@ -115,6 +115,33 @@ int pa_decode(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
               void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * pa_decode without a caller workspace and without any allocation: the
+ * split partials and the work list live in a static device array of
+ * pa_decode_noalloc_max_workspace() bytes (64 MiB) that every GPU the library
+ * runs on holds until the process ends.  Arguments, results and errors are
+ * those of pa_decode; a launch whose pa_decode_workspace_size exceeds the
+ * array returns PA_ERR_WORKSPACE before touching the device.  The array's
+ * device address is looked up once per device, on the first call with that
+ * device current (the stream must belong to the current device).  Calls
+ * that overlap on one GPU share the array and race: serialise them (one
+ * stream, or events).  No counterpart in the reference: it exists for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving
+ * loops that forbid hipMalloc).
+ */
+int pa_decode_noalloc(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
+                      const uint16_t* k_cache, const uint16_t* v_cache,
+                      int32_t num_pages, int32_t page_size,
+                      int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                      const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                      const int32_t* lengths, int32_t batch,
+                      int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                      float scale, float soft_cap,
+                      uint16_t* out, int64_t out_batch_stride, int64_t out_head_stride, void* stream);
+
+/* Bytes of pa_decode_noalloc's static scratch (the largest workspace it can serve). */
+size_t pa_decode_noalloc_max_workspace(void);
+
+/*
  * Ragged causal GQA paged prefill.  Sequence b owns q rows
  * [cu_seqlens_q[b], cu_seqlens_q[b+1]) and kv indices [0, Lk_b) with
  * Lk_b = cu_seqlens_k[b+1] - cu_seqlens_k[b] (cu_seqlens_k == NULL: Lk_b is

@@ -49,6 +49,18 @@ SIGNATURES = {
         c_vp, c_i64, c_i64,            # out
         c_vp, c_sz, c_vp,              # workspace, bytes, stream
     ]),
+    "pa_decode_noalloc": (ctypes.c_int, [
+        c_vp, c_i64, c_i64,            # q
+        c_vp, c_vp, c_i32, c_i32,      # caches, num_pages, page_size
+        c_i64, c_i64, c_i64,           # strides
+        c_vp, c_i64, c_i32,            # block_tables, bt_stride, pages_per_seq
+        c_vp, c_i32,                   # lengths, batch
+        c_i32, c_i32, c_i32,           # heads, kv heads, head_dim
+        c_f32, c_f32,                  # scale, soft_cap
+        c_vp, c_i64, c_i64,            # out
+        c_vp,                          # stream (no workspace)
+    ]),
+    "pa_decode_noalloc_max_workspace": (c_sz, []),
     "pa_prefill": (ctypes.c_int, [
         c_vp, c_i64, c_i64,            # q
         c_vp, c_vp, c_i32, c_i32,      # caches, num_pages, page_size

@@ -1,6 +1,8 @@
 // Split-K paged GQA decode for gfx950: the kernel entries and the host
 // launcher.  The work item (one chunk of one sequence and kv head) is
 // decode_item in decode_impl.h.
+#include <mutex>
+
 #include "decode_impl.h"
 
 namespace pa {
@@ -123,6 +125,46 @@ static int decode_chunks(int32_t pages_per_seq, int32_t page_size) {
 }  // namespace pa
 
 using namespace pa;
+
+// ---- pa_decode_noalloc: pa_decode with its workspace in a static device
+// array, for callers that cannot allocate device memory.  Every GPU the
+// library runs on holds its own copy of `scratch` until the process ends;
+// the host refers to it only through the address hipGetSymbolAddress returns
+// for the current device (the symbol's host-side name is not a device
+// address).  The decode workspace needs no clearing (the merge reads only the
+// partials of chunks a launch wrote, and a listed launch rewrites the list),
+// so nothing is zeroed between calls.  Calls that overlap on one GPU share
+// the array and race.
+constexpr size_t kNoAllocScratchBytes = (size_t)64 << 20;
+static __device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];  // per device, set once with that device current
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device).
+int noalloc_scratch(const char* name, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(PA_ERR_LAUNCH, "%s: hipGetDevice failed: %s", name, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(PA_ERR_UNSUPPORTED, "%s: device %d beyond the %d devices the scratch table holds", name, dev,
+                kMaxScratchDevices);
+  std::lock_guard<std::mutex> g(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(PA_ERR_LAUNCH, "%s: hipGetSymbolAddress(scratch) failed on device %d: %s", name, dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return PA_OK;
+}
+}  // namespace
 
 // Partials (o, then max / sum), then at a 256-byte boundary the work list:
 // a header and one int per pair, the pair count rounded up to 8.
@@ -268,6 +310,38 @@ extern "C" int pa_decode(const uint16_t* q, int64_t q_batch_stride, int64_t q_he
                        slot_stride, head_stride, block_tables, bt_stride, pages_per_seq, lengths, batch, num_heads,
                        num_kv_heads, head_dim, scale, soft_cap, out, out_batch_stride, out_head_stride, workspace,
                        workspace_bytes, stream);
+}
+
+extern "C" size_t pa_decode_noalloc_max_workspace(void) { return kNoAllocScratchBytes; }
+
+extern "C" int pa_decode_noalloc(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
+                                 const uint16_t* k_cache, const uint16_t* v_cache,
+                                 int32_t num_pages, int32_t page_size,
+                                 int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                                 const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                                 const int32_t* lengths, int32_t batch,
+                                 int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                 float scale, float soft_cap,
+                                 uint16_t* out, int64_t out_batch_stride, int64_t out_head_stride, void* stream) {
+  // the size limit is checked before the device is touched
+  const size_t need = pa_decode_workspace_size(batch, num_heads, head_dim, pages_per_seq, page_size);
+  if (need > kNoAllocScratchBytes)
+    return fail(PA_ERR_WORKSPACE,
+                "pa_decode_noalloc: this launch needs %zu bytes of workspace, more than the %zu bytes of its static "
+                "scratch (batch=%d, num_heads=%d, pages_per_seq=%d, page_size=%d); use pa_decode with a workspace",
+                need, kNoAllocScratchBytes, batch, num_heads, pages_per_seq, page_size);
+  void* ws = nullptr;
+  if (need > 0 && batch > 0) {
+    int rc = noalloc_scratch("pa_decode_noalloc", &ws);
+    if (rc) return rc;
+  }
+  DecodeParams prm{};
+  prm.k_cache = k_cache;
+  prm.v_cache = v_cache;
+  return decode_common("pa_decode_noalloc", prm, false, q, q_batch_stride, q_head_stride, num_pages, page_size,
+                       page_stride, slot_stride, head_stride, block_tables, bt_stride, pages_per_seq, lengths, batch,
+                       num_heads, num_kv_heads, head_dim, scale, soft_cap, out, out_batch_stride, out_head_stride, ws,
+                       ws ? kNoAllocScratchBytes : 0, stream);
 }
 
 extern "C" int pa_decode_fp8(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
