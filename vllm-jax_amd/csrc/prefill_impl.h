@@ -15,7 +15,11 @@
 //                                       permlane32 swap and rescaling O is
 //                                       lane-local; the reference max only
 //                                       moves when a row max grows by more than
-//                                       2^8, so O is rarely rescaled
+//                                       2^8, so O is rarely rescaled.  Q is
+//                                       scaled by scale*log2 e once per item
+//                                       and the QK accumulators start at
+//                                       -m_ref, so S leaves the MFMAs as the
+//                                       exponent itself (soft cap: raw S)
 //   O^T[d][n] += V^T[d][t] . P^T[t][n]  V^T operand read from the row-major V
 //                                       tile with ds_read_b64_tr_b16 (gfx950's
 //                                       transposing LDS read), P^T straight from
@@ -312,6 +316,18 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   // invisible to the compiler's wait tracking, so nothing it issued may still
   // be in flight when they start (else it would drain them at the loop head).
   wait_vm_lgkm0<0>();
+  if constexpr (!kSoftCap) {
+    // Q^T scaled by scale * log2 e (rounded to bf16), so that S = K Q^T is in
+    // log2 units
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+      const u32x4 w = __builtin_bit_cast(u32x4, qt_op[ks]);
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(bf16_lo(w[e]) * p.logit_scale, bf16_hi(w[e]) * p.logit_scale);
+      qt_op[ks] = as_bf16x8(o);
+    }
+  }
   __syncthreads();
   int qpos_max = red_max[0], qpos_min = red_min[0];
 #pragma unroll
@@ -340,10 +356,12 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   // 63 * slot_stride + 127 <= INT32_MAX (prefill_offsets_fit), so neither
   // this nor the byte offset 2 * ld_off below wraps
   uint32_t ld_off[kBlk];
+  uint32_t ld_sw[kBlk];  // its swizzled chunk part alone
 #pragma unroll
   for (int i = 0; i < kBlk; ++i) {
     const int r = 4 * (kBlk * wave + i) + ld_r;
-    ld_off[i] = (uint32_t)(r * (int32_t)p.slot_stride + 8 * swz(r, ld_p));
+    ld_sw[i] = (uint32_t)(8 * swz(r, ld_p));
+    ld_off[i] = (uint32_t)(r * (int32_t)p.slot_stride) + ld_sw[i];
   }
   // Tile DMA in two steps: tile_addrs() computes this wave's 2*kBlk global
   // addresses (K block 0, V block 0, K block 1, ...), dma_issue() issues one
@@ -362,9 +380,9 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   const int64_t tile_stride = (int64_t)kTileN * p.slot_stride;
   auto page_raw_at = [&](int lp) __attribute__((always_inline)) {
     const __attribute__((address_space(4))) int32_t* c = (const __attribute__((address_space(4))) int32_t*)bt_row;
-    // stays inside the table row; an empty row (pages_per_seq == 0, every
-    // row then sees no key and loads no tile) reads nothing
-    return p.pages_per_seq > 0 ? c[min(lp, p.pages_per_seq - 1)] : 0;
+    // stays inside the table row (only called with n_tiles > 0, so the row
+    // has an entry: lk <= pages_per_seq * page_size)
+    return c[max(min(lp, p.pages_per_seq - 1), 0)];
   };
   // rin: (aligned) the tile's index inside its page
   auto tile_addrs = [&](int j0, int32_t raw, int rin) __attribute__((always_inline)) {
@@ -377,16 +395,15 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
       const int64_t pbase = (int64_t)page * p.page_stride + rin * tile_stride + head_off;
       a.kb = (const char*)(p.k_cache + pbase);
       a.vb = (const char*)(p.v_cache + pbase);
-      if (j0 + kTileN <= lk) {
+      // rows past the kv length read the tile's last valid token (masked,
+      // never stale); a tile wholly past it reads its row 0.  Selects, no
+      // branch.
+      const int last = __builtin_amdgcn_readfirstlane(max(lk - 1 - j0, 0));
+      const uint32_t last_off = (uint32_t)(min(last, kTileN - 1) * (int32_t)p.slot_stride);
 #pragma unroll
-        for (int i = 0; i < kBlk; ++i) a.vo[i] = 2u * ld_off[i];
-      } else {
-        const int last = lk - 1 - j0;  // clamp onto a valid token: masked, never stale
-#pragma unroll
-        for (int i = 0; i < kBlk; ++i) {
-          const int r = 4 * (kBlk * wave + i) + ld_r;
-          a.vo[i] = 2u * (uint32_t)(min(r, last) * (int32_t)p.slot_stride + 8 * swz(r, ld_p));
-        }
+      for (int i = 0; i < kBlk; ++i) {
+        const int r = 4 * (kBlk * wave + i) + ld_r;
+        a.vo[i] = 2u * (r <= last ? ld_off[i] : last_off + ld_sw[i]);
       }
     } else {
       int32_t pages[kBlk];
@@ -442,20 +459,23 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) {
     const int c = 4 * dt + 2 * (tr_gamma & 1) + ((tr_s & 3) >> 1);
-    voff0[dt] = tr_row * 256 + 16 * (c ^ f0) + 8 * (tr_s & 1);
-    voff1[dt] = (tr_row + 8) * 256 + 16 * (c ^ f1) + 8 * (tr_s & 1);
+    voff0[dt] = v_lds0 + tr_row * 256 + 16 * (c ^ f0) + 8 * (tr_s & 1);
+    voff1[dt] = v_lds0 + (tr_row + 8) * 256 + 16 * (c ^ f1) + 8 * (tr_s & 1);
   }
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) asm volatile("" : "+v"(voff0[dt]), "+v"(voff1[dt]));
 
   f32x16 acc_o[4];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc_o[dt][i] = 0.f;
-  float m_ref = -1e30f;  // reference max (log2 units) of the accumulators
-  // running row sums, one per quarter of a tile: four short dot2c chains
-  // instead of one long one
+  float m_ref = kSoftCap ? -1e30f : 0.f;  // reference max (log2 units) of the accumulators
+  f32x16 neg_mref = {};  // -m_ref in every element: the QK accumulators start from it
+  // running row sums, one per quarter of a tile (four short add chains), of
+  // the f32 exponentials: v_dot2c on the packed P would wait for the matrix
+  // core, which the other wave of the SIMD keeps busy
   float l_part[4] = {0.f, 0.f, 0.f, 0.f};
-  const float cs = kSoftCap ? 1.f : p.logit_scale;  // multiplier applied inside the exponent
   f32x16 s_acc[2];  // S^T of the tile between its QK and its softmax
   bf16x8 pt[4];     // P^T of the tile between its softmax and its PV
 
@@ -469,28 +489,24 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   auto qk = [&](auto kst) __attribute__((always_inline)) {
     const lds_cbytes kt = (lds_cbytes)(k_stage(kst));
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s_acc[mt][i] = 0.f;
-#pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt) {
         const bf16x8 a = as_bf16x8(ds_read16(kt + koff[ks] + mt * 8192));
-        s_acc[mt] = mfma32(a, qt_op[ks], s_acc[mt]);
+        // the first k-step starts from -m_ref (zero with the soft cap)
+        s_acc[mt] = mfma32(a, qt_op[ks], ks == 0 ? (kSoftCap ? f32x16{} : neg_mref) : s_acc[mt]);
       }
     }
   };
   auto pv = [&](auto vst) __attribute__((always_inline)) {
-    const lds_cbytes vt = (lds_cbytes)(v_stage(vst));
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       // k-step u: tokens 32(u/2) + 16(u%2) + {4h + r, 8 + 4h + r}
-      const int rb = (32 * (u >> 1) + 16 * (u & 1)) * 256;
+      const int rb = decltype(vst)::value * kTileElems * 2 + (32 * (u >> 1) + 16 * (u & 1)) * 256;
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const s16x4 lo = ds_read_tr16(vt + rb + voff0[dt]);
-        const s16x4 hi = ds_read_tr16(vt + rb + voff1[dt]);
+        const s16x4 lo = ds_read_tr16((lds_cbytes)(uintptr_t)voff0[dt] + rb);
+        const s16x4 hi = ds_read_tr16((lds_cbytes)(uintptr_t)voff1[dt] + rb);
         const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
         const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
         const u32x4 a = {lo2[0], lo2[1], hi2[0], hi2[1]};
@@ -531,10 +547,27 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
       mq[q4] = __builtin_fmaxf(m, s_acc[mt][b0 + 7]);
     }
     float mx = __builtin_fmaxf(__builtin_fmaxf(mq[0], mq[1]), __builtin_fmaxf(mq[2], mq[3]));
-    mx = max_xor32(mx) * cs;
-    // Move the reference max only when this tile's max exceeds it by more
-    // than the slack (any lane in the wave): exponents stay <= 2^slack.
-    if (__any(mx > m_ref + kRescaleSlack)) {
+    mx = max_xor32(mx);  // log2 units: S is computed from the scaled Q (soft cap: capped logits)
+    if constexpr (!kSoftCap) {
+      // S is already relative to m_ref.  The first tile sets m_ref to the row
+      // max (a row that sees no key keeps 0); later the reference moves only
+      // when a row max exceeds it by more than the slack (any lane).
+      if (t == 0 || __any(mx > kRescaleSlack)) {
+        const float d = t == 0 ? (mx == -INFINITY ? 0.f : mx) : fmaxf(mx, 0.f);
+        if (t != 0) {
+          const float corr = fast_exp2(-d);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) l_part[u] *= corr;
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) acc_o[dt] = acc_o[dt] * corr;
+        }
+        m_ref += d;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) neg_mref[i] = -m_ref;
+#pragma unroll
+        for (int mt = 0; mt < 2; ++mt) s_acc[mt] = s_acc[mt] - d;
+      }
+    } else if (__any(mx > m_ref + kRescaleSlack)) {
       const float m_new = fmaxf(m_ref, mx);
       const float corr = fast_exp2(m_ref - m_new);
       m_ref = m_new;
@@ -551,12 +584,11 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
       u32x4 w;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float a = fast_exp2(__builtin_fmaf(s_acc[mt][base + 2 * e], cs, -m_ref));
-        const float c = fast_exp2(__builtin_fmaf(s_acc[mt][base + 2 * e + 1], cs, -m_ref));
+        const float a = fast_exp2(kSoftCap ? s_acc[mt][base + 2 * e] - m_ref : s_acc[mt][base + 2 * e]);
+        const float c = fast_exp2(kSoftCap ? s_acc[mt][base + 2 * e + 1] - m_ref : s_acc[mt][base + 2 * e + 1]);
         w[e] = pack_bf16x2(a, c);
+        l_part[u] += a + c;
       }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) l_part[u] = dot2_bf16_ones(w[e], l_part[u]);
       // Materialise P here: otherwise the compiler sinks the exp work past
       // the barrier into the next MFMA segment, undoing the ping-pong.
       pt[u] = as_bf16x8(w);
@@ -615,12 +647,14 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     }
     wait_vm_lgkm0<15>();  // LDS reads of this segment retired (vmcnt untouched)
     barrier();
+    // Tile t + ahead, also when it is past the last tile (into a stage
+    // nobody reads again): every iteration issues the same loads, so the
+    // softmax has no branch around them and the waits count the same.
     const int ti = t + ahead;
-    const bool dma = ti < n_tiles;
     const int dstage = grp_b ? (s + 3) % kStages : (s + 2) % kStages;
     TileAddrs ta;
-    if (dma) ta = tile_addrs(ti * kTileN, page_next, nx_r);
-    if constexpr (kAligned) {  // for the next iteration: tile ti + 1
+    if constexpr (kPv || kQk) ta = tile_addrs(ti * kTileN, page_next, nx_r);
+    if constexpr (kAligned && (kPv || kQk)) {  // for the next iteration: tile ti + 1
       if (++nx_r == tpp) {
         nx_r = 0;
         ++nx_lp;
@@ -630,7 +664,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     // one DMA before each quarter of the softmax: a burst of them would
     // stall on the address queue
     auto between = [&](int u) __attribute__((always_inline)) {
-      if (dma) dma_issue(ta, u, dstage);
+      if constexpr (kPv || kQk) dma_issue(ta, u, dstage);
     };
     if constexpr (kQk) {
       softmax(t, between);
@@ -640,8 +674,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     }
     // this wave's share of tile t + ahead - 1 has landed: at most the loads of
     // tile t + ahead (issued above) may still be outstanding
-    if (ti < n_tiles) wait_vm_lgkm0<kDmaPerTile>();
-    else wait_vm_lgkm0<0>();
+    wait_vm_lgkm0<kDmaPerTile>();
     barrier();
   };
   using S0 = std::integral_constant<int, 0>;
@@ -652,16 +685,18 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   // Prologue: A issues tiles 0 and 1, B tiles 0, 1 and 2.  Everyone waits for
   // tile 0 before the first barrier; B also waits for tile 1 before its idle
   // barrier (which ends segment 0, i.e. before A's M(1) in segment 2).
-  if (n_tiles > 0) issue_tile_raw(0, raw_pre[0], 0);
-  if (n_tiles > 1) issue_tile_raw(kTileN, raw_pre[1], 1);
-  if (grp_b && n_tiles > 2) issue_tile_raw(2 * kTileN, raw_pre[2], 2);
+  if (n_tiles > 0) {
+    issue_tile_raw(0, raw_pre[0], 0);
+    issue_tile_raw(kTileN, raw_pre[1], 1);
+    if (grp_b) issue_tile_raw(2 * kTileN, raw_pre[2], 2);
+  }
   // raw page id of the first tile the loop loads (tile `ahead`)
   if (kAligned && n_tiles > 0) {
     nx_lp = ahead / tpp;
     nx_r = ahead - nx_lp * tpp;
     page_next = page_raw_at(nx_lp);
   }
-  const int issued = min(n_tiles, grp_b ? 3 : 2);
+  const int issued = n_tiles > 0 ? (grp_b ? 3 : 2) : 0;
   if (issued == 3) wait_vm_lgkm0<2 * kDmaPerTile>();
   else if (issued == 2) wait_vm_lgkm0<kDmaPerTile>();
   else wait_vm_lgkm0<0>();
@@ -696,6 +731,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     }
   }
   if (!grp_b) barrier();
+  wait_vm_lgkm0<0>();  // loads of tiles past the end may still be in flight
 
   // ---- epilogue: row n = (token rtok, head rhead); acc_o[dt][i] holds
   // d = 32dt + 8(i/4) + 4h + i%4.  One permlane32 swap per dword pair gives
