@@ -13,6 +13,10 @@ workload, inputs resident in HBM:
 * The Qwen3-8B prefix-cached prefill (64 sequences, cached prefixes
   U[0, 4096] in shared blocks, new chunks U[128, 1024], 32 q / 8 kv heads,
   seed 3): reported under ``"prefix_prefill"`` in TFLOP/s.
+* The prefix-cached prefill over float8 e4m3 pages (the same pool quantised
+  on the device): each distinct page widened once, then the bf16 prefill;
+  reported under ``"prefill_fp8"`` in TFLOP/s with the widening included,
+  next to the bf16 time of the same batch.
 * The Qwen3-8B decode over float8 e4m3 pages with per-token scales (the same
   pool quantised on the device): reported under ``"decode_fp8"`` in GB/s of
   its own algorithmic bytes (codes + scales), with the bf16 decode time of
@@ -101,7 +105,7 @@ def run_gpu(args):
     # ---------------- prefill: Qwen3-32B long context
     pb = wl.qwen3_32b_long_prefill(seed=4)
     pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False) \
-        if args.only not in ("decode", "mixed", "decode_fp8", "prefix") else None
+        if args.only not in ("decode", "mixed", "decode_fp8", "prefix", "prefill_fp8") else None
     if pt is None:  # decode-only profiling run: keep the prefill half tiny
         pb = wl.make_prefill([64], num_heads=64, num_kv_heads=8, rng=np.random.default_rng(0))
         pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False)
@@ -141,7 +145,7 @@ def run_gpu(args):
     run_r = args.only in (None, "rope")
     run_m = args.only in (None, "mixed")
     run_f = args.only in (None, "decode_fp8")
-    run_x = args.only in (None, "prefix")
+    run_x = args.only in (None, "prefix", "prefill_fp8")
     nop = lambda: None
     if not run_p:
         prefill_step = prefill_attn = nop
@@ -184,7 +188,8 @@ def run_gpu(args):
     rope = run_rope(args, torch, pkg, pb, pt, kv_p) if run_r else None
     c1 = run_c1(args, torch, pkg, wl, dev, cpu=not args.no_cpu_baseline) if args.only is None else None
     mixed = run_mixed(args, torch, pkg, wl, dev) if run_m else None
-    prefix = run_prefix(args, torch, pkg, wl, dev) if run_x else None
+    prefix, pre8 = run_prefix(args, torch, pkg, wl, dev, fp8=args.only in (None, "prefill_fp8")) \
+        if run_x else (None, None)
     if prefix is not None:
         prefix["roofline"]["traffic"] = _load_traffic().get("prefill_kernel_prefix_cached")
     dec8 = run_decode_fp8(args, torch, pkg, db, dt_, ws, dscale, float(d_attn.mean()) if run_d else None) \
@@ -261,6 +266,8 @@ def run_gpu(args):
         res["qwen3_06b_prefill"] = c1
     if prefix is not None:
         res["prefix_prefill"] = prefix
+    if pre8 is not None:
+        res["prefill_fp8"] = pre8
     if dec8 is not None:
         dec8["roofline"]["traffic"] = traffic.get("decode_fp8_split_kernel")
         res["decode_fp8"] = dec8
@@ -310,9 +317,10 @@ def run_decode_fp8(args, torch, pkg, db, dt_, ws, dscale, bf16_ms):
     }
 
 
-def run_prefix(args, torch, pkg, wl, dev):
+def run_prefix(args, torch, pkg, wl, dev, fp8=False):
     """Time the Qwen3-8B prefix-cached prefill: new tokens stored, then the
-    causal prefill over cached + new K/V."""
+    causal prefill over cached + new K/V.  With ``fp8``, also the same batch
+    over float8 pages (``run_prefix_fp8``)."""
     pb = wl.qwen3_8b_prefix_prefill(seed=3)
     t = wl.materialize_prefill(pb, seed=3, device=dev, fill_pool=True)
     kv = t["kv_cache"]
@@ -340,6 +348,7 @@ def run_prefix(args, torch, pkg, wl, dev):
     at = float(np.mean([e[1].elapsed_time(e[2]) for e in ev]))
     flops = pb.flops()
     tf = flops / (at * 1e-3) / 1e12
+    pre8 = run_prefix_fp8(args, torch, pkg, pb, t, at) if fp8 else None
     return {
         "metric": "prefix-cached prefill attn TFLOP/s",
         "seqs": int(pb.batch), "new_tokens": int(pb.num_tokens),
@@ -347,6 +356,60 @@ def run_prefix(args, torch, pkg, wl, dev):
         "kv_store_ms": round(st, 4), "attn_ms": round(at, 4),
         "attn_tflops": round(tf, 2), "frac_of_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
         "roofline": {"kernel": "prefill_kernel", "bound": "mfma", "achieved": round(tf, 2),
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": None},
+    }, pre8
+
+
+def run_prefix_fp8(args, torch, pkg, pb, t, bf16_ms):
+    """The prefix-cached prefill over float8 e4m3 pages: the bf16 pool
+    quantised on the device, then per call every distinct page in use
+    widened once to bf16 and the bf16 prefill over the remapped table."""
+    kv = t["kv_cache"]
+    nb, bs, hkv, d = kv.shape[1:]
+    codes = torch.empty((2, nb, bs, hkv, d), dtype=torch.float8_e4m3fn, device=kv.device)
+    scales = torch.empty((2, hkv, nb, bs), dtype=torch.float32, device=kv.device)
+    pkg.update_kv_cache_fp8(codes, scales, torch.arange(nb * bs, dtype=torch.int32, device=kv.device),
+                            kv[0].reshape(-1, hkv, d), kv[1].reshape(-1, hkv, d))
+    kp, vp = codes[0].permute(2, 0, 1, 3), codes[1].permute(2, 0, 1, 3)
+    bt = t["block_tables"]
+    lib = pkg._lib.load()
+    need = lib.pa_prefill_fp8_workspace_size(pb.batch, bt.shape[1], bs, hkv, d, int(pb.max_seqlen_bucket),
+                                             pb.num_heads)
+    ws = torch.empty(need, dtype=torch.uint8, device=kv.device)
+    out = torch.empty_like(t["q"])
+
+    def call():
+        pkg.prefill_paged_attention(t["q"], kp, vp, bt, t["cu_seqlens_q"], t["slot_mapping"],
+                                    t["input_positions"], max_seqlen_bucket=pb.max_seqlen_bucket,
+                                    cu_seqlens_k=t["cu_seqlens_k"], k_scales_pages=scales[0],
+                                    v_scales_pages=scales[1], workspace=ws, out=out)
+
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    n = max(args.steps, 10)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    # the widening leaves its page count after the widened pages, the
+    # remapped table and the pages' owner entries
+    entries = pb.batch * bt.shape[1]
+    at = 2 * entries * bs * hkv * d * 2 + 2 * entries * 4
+    widened = int(ws[at:at + 4].cpu().numpy().view(np.int32)[0])
+    kv_lens = (pb.prefix_lens + pb.q_lens).astype(np.int64)
+    in_use = int(np.sum(-(-kv_lens // bs)))
+    tf = pb.flops() / (ms * 1e-3) / 1e12
+    return {
+        "metric": "prefix-cached prefill attn TFLOP/s over float8 e4m3 pages (widening included)",
+        "attn_ms": round(ms, 4), "bf16_attn_ms": round(bf16_ms, 4),
+        "widened_pages": widened, "table_entries_in_use": in_use,
+        "attn_tflops": round(tf, 2), "frac_of_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+        "roofline": {"kernel": "fp8_pages_widen_kernel + prefill_kernel", "bound": "mfma", "achieved": round(tf, 2),
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
                      "traffic": None},
     }
@@ -600,7 +663,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU oracle work (total)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["prefill", "decode", "rope", "mixed", "decode_fp8", "prefix", "copy"],
+    ap.add_argument("--only", choices=["prefill", "decode", "rope", "mixed", "decode_fp8", "prefix", "prefill_fp8",
+                                       "copy"],
                     default=None,
                     help="profiling aid: run one kernel family only (the JSON line then covers that part)")
     args = ap.parse_args()

@@ -246,8 +246,9 @@ int pa_decode_fp8(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stri
                   uint16_t* out, int64_t out_batch_stride, int64_t out_head_stride,
                   void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes pa_prefill_fp8 needs: two bf16 pages per block-table
- * entry (K and V), one int32 per entry, then pa_prefill's work list. */
+/* Workspace bytes pa_prefill_fp8 needs: room for two bf16 pages per
+ * block-table entry (K and V), two int32 per entry and a count, then
+ * pa_prefill's work list. */
 size_t pa_prefill_fp8_workspace_size(int32_t batch, int32_t pages_per_seq, int32_t page_size,
                                      int32_t num_kv_heads, int32_t head_dim, int32_t max_seqlen_q,
                                      int32_t num_heads);
@@ -255,9 +256,10 @@ size_t pa_prefill_fp8_workspace_size(int32_t batch, int32_t pages_per_seq, int32
 /*
  * pa_prefill over float8 e4m3fn pages with per-token scales
  * (prefill_paged_attention.py:169-170,255-266, in-kernel :84-92,120-123).
- * Every page a sequence uses is first widened into the workspace as bf16
- * (code * token scale, one rounding); the bf16 prefill then runs on those
- * pages.  The reference scales the logits and P instead of K and V; the two
+ * Every distinct physical page the sequences use is first widened once into
+ * the workspace as bf16 (code * token scale, one rounding), so pages shared
+ * between sequences (cached prefixes) are widened once; the bf16 prefill then
+ * runs on those pages through a remapped table.  The reference scales the logits and P instead of K and V; the two
  * differ by that one bf16 rounding.  Strides and scales as in pa_decode_fp8;
  * the workspace (256-byte aligned) is caller-owned.
  */

@@ -105,7 +105,7 @@ def test_prefill_workspace_size():
     assert lib.pa_prefill_workspace_size(0, 1024, 64, 8) == 256
     assert lib.pa_prefill_workspace_size(2, 300, 15, 8) == 0   # heads not a multiple of kv heads
     fp8 = lib.pa_prefill_fp8_workspace_size(2, 4, 256, 8, 128, 300, 16)
-    widened = 2 * 8 * 256 * 8 * 128 * 2 + 8 * 4
+    widened = 2 * 8 * 256 * 8 * 128 * 2 + (2 * 8 + 1) * 4   # pages, then table, owners, count
     assert fp8 == (widened + 255) // 256 * 256 + 256 + 32 * 6
 
 

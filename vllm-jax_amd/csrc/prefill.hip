@@ -117,31 +117,110 @@ prefill_prep_kernel(PrefillParams p, int32_t* __restrict__ plan) {
   }
 }
 
-// Float8 pages for the prefill: every page a sequence uses (block-table
-// entry lp with lp * page_size < its kv length) is widened into a bf16
-// workspace pool, entry (b, lp) to workspace page b * P + lp, each element
-// bf16(code * scale of its token) (one rounding), and the new table points
-// there (-1 for unused entries, which the prefill never reads).  One
-// workgroup per table entry, 16 codes per thread and step.
-__global__ void __launch_bounds__(256)
-prefill_dequant_pages_kernel(const uint8_t* __restrict__ k8, const uint8_t* __restrict__ v8,
-                             const float* __restrict__ ks, const float* __restrict__ vs, int32_t num_pages,
-                             int32_t page_size, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
-                             int64_t sc_page_stride, int64_t sc_head_stride, const int32_t* __restrict__ bt,
-                             int64_t bt_stride, int32_t pages_per_seq, const int32_t* __restrict__ cu_q,
-                             const int32_t* __restrict__ cu_k, int32_t num_kv_heads, uint16_t* __restrict__ wk,
-                             uint16_t* __restrict__ wv, int32_t* __restrict__ bt_out) {
-  const int64_t e = blockIdx.x;  // table entry (b, lp)
+// Float8 pages for the prefill.  A block-table entry (b, lp) is in use when
+// lp * page_size < the sequence's kv length.  Every distinct physical page
+// in use is widened once into a compact bf16 pool (slot i of the pool holds
+// the i-th distinct page), each element bf16(code * scale of its token), one
+// rounding; the remapped table points there (-1 for unused entries, which
+// the prefill never reads).  Pages shared between sequences (cached
+// prefixes) are widened once.
+//
+// fp8_pages_plan_kernel (one workgroup) finds the distinct pages with an
+// open-addressing hash in LDS: keys are physical page ids, and the thread
+// whose atomicCAS claims a key takes the next slot from an LDS counter and
+// records its entry as the slot's owner.  Tables with more entries than the
+// hash holds (hbits == 0) get one slot per used entry.
+constexpr int kFp8HashBits = 14;  // LDS hash of 2^14 slots: tables of up to 2^13 entries
+
+// Physical page of table entry e, or -1 when the entry is not in use.
+__device__ __forceinline__ int32_t fp8_entry_page(const int32_t* __restrict__ bt, int64_t bt_stride,
+                                                  int32_t pages_per_seq, int32_t page_size, int32_t num_pages,
+                                                  const int32_t* __restrict__ cu_q, const int32_t* __restrict__ cu_k,
+                                                  int64_t e) {
   const int b = (int)(e / pages_per_seq);
   const int lp = (int)(e - (int64_t)b * pages_per_seq);
   const int lk = cu_k ? cu_k[b + 1] - cu_k[b] : cu_q[b + 1] - cu_q[b];
-  const bool used = (int64_t)lp * page_size < lk;
-  if (threadIdx.x == 0) bt_out[e] = used ? (int32_t)e : -1;
-  if (!used) return;
+  if ((int64_t)lp * page_size >= lk) return -1;
   const int32_t raw = bt[(int64_t)b * bt_stride + lp];
-  const int64_t page = raw < 0 ? 0 : (raw >= num_pages ? num_pages - 1 : raw);
+  return raw < 0 ? 0 : (raw >= num_pages ? num_pages - 1 : raw);
+}
+
+__device__ __forceinline__ uint32_t fp8_page_hash(int32_t page, int hbits) {
+  return ((uint32_t)page * 0x9E3779B1u) >> (32 - hbits);
+}
+
+__global__ void __launch_bounds__(1024)
+fp8_pages_plan_kernel(const int32_t* __restrict__ bt, int64_t bt_stride, int32_t pages_per_seq, int32_t batch,
+                      int32_t page_size, int32_t num_pages, const int32_t* __restrict__ cu_q,
+                      const int32_t* __restrict__ cu_k, int32_t hbits, int32_t* __restrict__ bt_out,
+                      int32_t* __restrict__ owner, int32_t* __restrict__ count) {
+  __shared__ int32_t keys[1 << kFp8HashBits];
+  __shared__ int32_t slots[1 << kFp8HashBits];
+  __shared__ int32_t n_slots;
+  const int tid = threadIdx.x;
+  const int64_t entries = (int64_t)batch * pages_per_seq;
+  const uint32_t hmask = hbits ? (1u << hbits) - 1u : 0u;
+  if (hbits)
+    for (uint32_t h = tid; h <= hmask; h += blockDim.x) keys[h] = -1;
+  if (tid == 0) n_slots = 0;
+  __syncthreads();
+  for (int64_t e = tid; e < entries; e += blockDim.x) {
+    const int32_t page = fp8_entry_page(bt, bt_stride, pages_per_seq, page_size, num_pages, cu_q, cu_k, e);
+    if (page < 0) continue;
+    if (!hbits) {  // no hash: every used entry is its own slot
+      owner[atomicAdd(&n_slots, 1)] = (int32_t)e;
+      continue;
+    }
+    // the hash has at least twice as many slots as there are entries, so a
+    // free key is always found within the probe
+    uint32_t h = fp8_page_hash(page, hbits);
+    for (;;) {
+      const int32_t prev = atomicCAS(&keys[h], -1, page);
+      if (prev == -1) {
+        const int32_t sl = atomicAdd(&n_slots, 1);
+        slots[h] = sl;
+        owner[sl] = (int32_t)e;
+        break;
+      }
+      if (prev == page) break;
+      h = (h + 1) & hmask;
+    }
+  }
+  __syncthreads();
+  for (int64_t e = tid; e < entries; e += blockDim.x) {
+    const int32_t page = fp8_entry_page(bt, bt_stride, pages_per_seq, page_size, num_pages, cu_q, cu_k, e);
+    int32_t sl = -1;
+    if (page >= 0 && hbits) {
+      uint32_t h = fp8_page_hash(page, hbits);
+      while (keys[h] != page) h = (h + 1) & hmask;  // claimed above, so present
+      sl = slots[h];
+    }
+    bt_out[e] = sl;
+  }
+  if (!hbits) {  // one slot per used entry: the slot order is the claim order
+    __syncthreads();
+    for (int32_t sl = tid; sl < n_slots; sl += blockDim.x) bt_out[owner[sl]] = sl;
+  }
+  if (tid == 0) *count = n_slots;
+}
+
+// Slot i of the compact pool: the page of entry owner[i], widened.  One
+// workgroup per possible slot (the table's entry count); those past the
+// number of distinct pages return at once.  16 codes per thread and step.
+__global__ void __launch_bounds__(256)
+fp8_pages_widen_kernel(const uint8_t* __restrict__ k8, const uint8_t* __restrict__ v8,
+                       const float* __restrict__ ks, const float* __restrict__ vs, int32_t num_pages,
+                       int32_t page_size, int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                       int64_t sc_page_stride, int64_t sc_head_stride, const int32_t* __restrict__ bt,
+                       int64_t bt_stride, int32_t pages_per_seq, const int32_t* __restrict__ cu_q,
+                       const int32_t* __restrict__ cu_k, int32_t num_kv_heads, const int32_t* __restrict__ owner,
+                       const int32_t* __restrict__ count, uint16_t* __restrict__ wk, uint16_t* __restrict__ wv) {
+  const int32_t sl = blockIdx.x;
+  if (sl >= *count) return;
+  const int64_t page =
+      fp8_entry_page(bt, bt_stride, pages_per_seq, page_size, num_pages, cu_q, cu_k, owner[sl]);  // in use
   const int rows = page_size * num_kv_heads;  // (slot, head) rows of 128 codes
-  const int64_t wbase = e * (int64_t)rows * kPHeadDim;
+  const int64_t wbase = (int64_t)sl * rows * kPHeadDim;
   for (int c = threadIdx.x; c < rows * 8; c += 256) {
     const int r = c >> 3, part = c & 7;  // 16 codes of row r
     const int slot = r / num_kv_heads, h = r - slot * num_kv_heads;
@@ -302,13 +381,14 @@ extern "C" int pa_prefill(const uint16_t* q, int64_t q_tok_stride, int64_t q_hea
                         stream);
 }
 
-// Widened K and V pages, their block table, then (256-byte aligned) the
-// prefill's work list.
+// Widened K and V pages (one per table entry at most), the remapped block
+// table, the slots' owner entries and the slot count, then (256-byte
+// aligned) the prefill's work list.
 static size_t fp8_widened_bytes(int32_t batch, int32_t pages_per_seq, int32_t page_size, int32_t num_kv_heads,
                                 int32_t head_dim) {
   const size_t entries = (size_t)batch * pages_per_seq;
   const size_t page_elems = (size_t)page_size * num_kv_heads * head_dim;
-  return (2 * entries * page_elems * sizeof(uint16_t) + entries * sizeof(int32_t) + 255) / 256 * 256;
+  return (2 * entries * page_elems * sizeof(uint16_t) + (2 * entries + 1) * sizeof(int32_t) + 255) / 256 * 256;
 }
 
 extern "C" size_t pa_prefill_fp8_workspace_size(int32_t batch, int32_t pages_per_seq, int32_t page_size,
@@ -370,11 +450,22 @@ extern "C" int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q
   uint16_t* wv = wk + entries * page_elems;
   int32_t* bt2 = reinterpret_cast<int32_t*>(wv + entries * page_elems);
   hipStream_t s = (hipStream_t)stream;
-  prefill_dequant_pages_kernel<<<dim3((unsigned)entries), dim3(256), 0, s>>>(
+  int32_t* owner = bt2 + entries;
+  int32_t* n_slots = owner + entries;
+  // an LDS hash of at least twice the entries finds the distinct pages
+  int hbits = 6;
+  while (hbits <= kFp8HashBits && ((int64_t)1 << hbits) < 2 * entries) ++hbits;
+  if (hbits > kFp8HashBits) hbits = 0;
+  fp8_pages_plan_kernel<<<dim3(1), dim3(1024), 0, s>>>(block_tables, bt_stride, pages_per_seq, batch, page_size,
+                                                       num_pages, cu_seqlens_q, cu_seqlens_k, hbits, bt2, owner,
+                                                       n_slots);
+  int rc = launch_status("pa_prefill_fp8(plan)");
+  if (rc) return rc;
+  fp8_pages_widen_kernel<<<dim3((unsigned)entries), dim3(256), 0, s>>>(
       k_cache, v_cache, k_scales, v_scales, num_pages, page_size, page_stride, slot_stride, head_stride,
       scale_page_stride, scale_head_stride, block_tables, bt_stride, pages_per_seq, cu_seqlens_q, cu_seqlens_k,
-      num_kv_heads, wk, wv, bt2);
-  int rc = launch_status("pa_prefill_fp8(widen)");
+      num_kv_heads, owner, n_slots, wk, wv);
+  rc = launch_status("pa_prefill_fp8(widen)");
   if (rc) return rc;
   return prefill_launch("pa_prefill_fp8", q, q_tok_stride, q_head_stride, wk, wv, (int32_t)std::min<int64_t>(entries, 0x7fffffff),
                         page_size, page_elems, (int64_t)num_kv_heads * head_dim, head_dim, bt2, pages_per_seq,
