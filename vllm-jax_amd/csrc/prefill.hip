@@ -13,7 +13,39 @@ prefill_kernel(PrefillParams p) {
   prefill_body<kSoftCap, kAligned>(p, blockIdx.x);
 }
 
+// The item of workgroup `bid` with the shared pool: every XCD walks the
+// whole list (n items, one kv head of every entry, as prefill_resolve deals
+// them), but only its first n - s items statically (workgroup 8 k + x runs
+// XCD x's k-th item).  The last s items of every XCD, the cheapest, form a
+// pool that the workgroups dispatched after the static ones claim in list
+// order with one atomicAdd.  The 8 XCDs finish identical static work up to
+// 6 % apart (clock and memory differ per XCD); the XCDs that run ahead
+// reach their pool workgroups first and take more of the pool.  -1: nothing
+// left.
+__device__ __forceinline__ int prefill_pooled_item(const PrefillParams& p, int bid) {
+  const int n = p.plan[0] * (p.num_kv_heads >> 3);  // items of one XCD
+  const int s = n >> 2;
+  if (bid < 8 * (n - s)) return bid;
+  // a plain read first: once the pool is exhausted late workgroups leave
+  // without an atomic (the counter only grows, so a stale value errs late)
+  if (__hip_atomic_load(p.pool, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= 8 * s) return -1;
+  const int j = atomicAdd(p.pool, 1);  // pool item j: XCD j % 8's item n - s + j / 8
+  return j < 8 * s ? 8 * (n - s + (j >> 3)) + (j & 7) : -1;
+}
+
+template <bool kSoftCap, bool kAligned>
+__global__ void __launch_bounds__(kThreads, 1)
+prefill_kernel_pooled(PrefillParams p) {
+  __shared__ int32_t s_item;
+  if (threadIdx.x == 0) s_item = prefill_pooled_item(p, blockIdx.x);
+  __syncthreads();
+  const int item = __builtin_amdgcn_readfirstlane(s_item);  // the same in every lane
+  if (item < 0) return;
+  prefill_body<kSoftCap, kAligned>(p, item);
+}
+
 constexpr int kPrepThreads = 1024;
+constexpr int64_t kPoolMinItems = 16384;  // smallest grid that uses prefill_kernel_pooled
 constexpr int kPlanBins = 4096;       // cost classes of the work list (kv tiles + 1, clamped)
 constexpr int kPlanMaxBatch = 2048;   // sequences whose geometry the planner keeps in LDS
 
@@ -73,7 +105,10 @@ __device__ void prefill_plan(const PrefillParams& p, int32_t* __restrict__ plan)
     st16(r, u32x4{(uint32_t)b, (uint32_t)(i - b * nq), (uint32_t)sq.x, (uint32_t)sq.y});
     st16(r + 4, u32x4{(uint32_t)sq.z, (uint32_t)sq.w, 0u, 0u});
   }
-  if (tid == 0) plan[0] = count;
+  if (tid == 0) {
+    plan[0] = count;
+    plan[8] = 0;  // the shared pool's counter (prefill_kernel_pooled)
+  }
 }
 
 // Before the prefill: workgroup 0 builds the work list (when `plan` is
@@ -340,14 +375,29 @@ static int prefill_launch(const char* name, const uint16_t* q, int64_t q_tok_str
   }
   if (batch == 0 || max_seqlen_q == 0) return PA_OK;
   prm.plan = plan;
-  const int64_t blocks = items;  // with a list, items past its count return at once
+  // the pool pays off on long launches (the XCDs' finishing spread grows with
+  // the launch; the extra workgroups cost a dispatch each)
+  prm.pool = plan && num_kv_heads % 8 == 0 && items >= kPoolMinItems ? plan + 8 : nullptr;
+  // with a list, items past its count return at once; with the pool, a
+  // quarter more workgroups than items lets the XCDs that run ahead take up
+  // to twice their share of it
+  const int64_t blocks = prm.pool ? std::min<int64_t>(items + (items + 3) / 4, 0x7fffffff) : items;
   const bool aligned = page_size % kTileN == 0;
-  if (prm.soft_cap > 0.f) {
-    if (aligned) prefill_kernel<true, true><<<dim3((unsigned)blocks), dim3(kThreads), 0, s>>>(prm);
-    else prefill_kernel<true, false><<<dim3((unsigned)blocks), dim3(kThreads), 0, s>>>(prm);
+  const dim3 g((unsigned)blocks), b(kThreads);
+  if (prm.pool) {
+    if (prm.soft_cap > 0.f) {
+      if (aligned) prefill_kernel_pooled<true, true><<<g, b, 0, s>>>(prm);
+      else prefill_kernel_pooled<true, false><<<g, b, 0, s>>>(prm);
+    } else {
+      if (aligned) prefill_kernel_pooled<false, true><<<g, b, 0, s>>>(prm);
+      else prefill_kernel_pooled<false, false><<<g, b, 0, s>>>(prm);
+    }
+  } else if (prm.soft_cap > 0.f) {
+    if (aligned) prefill_kernel<true, true><<<g, b, 0, s>>>(prm);
+    else prefill_kernel<true, false><<<g, b, 0, s>>>(prm);
   } else {
-    if (aligned) prefill_kernel<false, true><<<dim3((unsigned)blocks), dim3(kThreads), 0, s>>>(prm);
-    else prefill_kernel<false, false><<<dim3((unsigned)blocks), dim3(kThreads), 0, s>>>(prm);
+    if (aligned) prefill_kernel<false, true><<<g, b, 0, s>>>(prm);
+    else prefill_kernel<false, false><<<g, b, 0, s>>>(prm);
   }
   return launch_status(name);
 }
