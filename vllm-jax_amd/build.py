@@ -3,6 +3,10 @@
 Compiles every HIP/C++ source under ``csrc/`` with hipcc into one shared
 library next to this file.  Run ``python vllm-jax_amd/build.py`` or call
 :func:`build`.  hipcc cross-compiles for gfx950 without a GPU present.
+
+It also builds ``libpaged_attention_phases.so``: the prefill entry points
+compiled with ``PA_PREFILL_PHASES``, whose kernel records per-workgroup
+phase timestamps (read by ``prefill_phases.py``).  Nothing else loads it.
 """
 from __future__ import annotations
 
@@ -16,10 +20,12 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libpaged_attention.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+PHASES_LIB_PATH = os.path.join(PKG_DIR, "libpaged_attention_phases.so")
 ARCH = "gfx950"
 
 SOURCES = ["pa_errors.cpp", "block_manager.cpp", "kv_store.hip", "decode.hip", "prefill.hip", "qk_norm_rope.hip",
            "mixed.hip"]
+PHASES_SOURCES = ["pa_errors.cpp", "prefill.hip"]
 
 # Packed-FP32 VALU forms are disabled for every device compile: the build
 # relies on scalar/float2 code only.  Without NaN semantics, fmaxf lowers to a
@@ -38,18 +44,19 @@ def _hipcc() -> str:
 
 
 def build(verbose: bool = False, jobs: int = 4) -> str:
-    """Compile all sources and link ``libpaged_attention.so``; returns its path."""
+    """Compile all sources and link ``libpaged_attention.so`` (and the
+    phase-timestamp build of prefill); returns the product library's path."""
     hipcc = _hipcc()
     with tempfile.TemporaryDirectory(prefix="pa_build_") as tmp:
-        objs, procs = [], []
-        for src in SOURCES:
-            path = os.path.join(CSRC, src)
-            obj = os.path.join(tmp, src + ".o")
-            cmd = [hipcc, *COMMON_FLAGS, "-c", path, "-o", obj]
-            if src.endswith(".hip"):
-                cmd[1:1] = [f"--offload-arch={ARCH}", *DEVICE_FLAGS]
-            objs.append(obj)
-            procs.append((src, cmd))
+        procs = []
+        libs = ((SOURCES, LIB_PATH, []), (PHASES_SOURCES, PHASES_LIB_PATH, ["-DPA_PREFILL_PHASES"]))
+        for i, (sources, _, defines) in enumerate(libs):
+            for src in sources:
+                obj = os.path.join(tmp, f"{i}_{src}.o")
+                cmd = [hipcc, *COMMON_FLAGS, *defines, "-c", os.path.join(CSRC, src), "-o", obj]
+                if src.endswith(".hip"):
+                    cmd[1:1] = [f"--offload-arch={ARCH}", *DEVICE_FLAGS]
+                procs.append((src, cmd))
         running = []
         for src, cmd in procs:
             if verbose:
@@ -59,16 +66,18 @@ def build(verbose: bool = False, jobs: int = 4) -> str:
                 _wait(running.pop(0), verbose)
         for r in running:
             _wait(r, verbose)
-        tmp_lib = os.path.join(tmp, LIB_NAME)
-        link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp_lib, *objs]
-        if verbose:
-            print(" ".join(link), flush=True)
-        res = subprocess.run(link, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
-        if res.returncode != 0:
-            raise RuntimeError("link failed:\n" + res.stdout.decode(errors="replace"))
-        # Replace atomically so a process that has the old library mapped keeps it.
-        shutil.copyfile(tmp_lib, LIB_PATH + ".tmp")
-        os.replace(LIB_PATH + ".tmp", LIB_PATH)
+        for i, (sources, lib_path, _) in enumerate(libs):
+            tmp_lib = os.path.join(tmp, os.path.basename(lib_path))
+            objs = [os.path.join(tmp, f"{i}_{src}.o") for src in sources]
+            link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", "-o", tmp_lib, *objs]
+            if verbose:
+                print(" ".join(link), flush=True)
+            res = subprocess.run(link, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+            if res.returncode != 0:
+                raise RuntimeError("link failed:\n" + res.stdout.decode(errors="replace"))
+            # Replace atomically so a process that has the old library mapped keeps it.
+            shutil.copyfile(tmp_lib, lib_path + ".tmp")
+            os.replace(lib_path + ".tmp", lib_path)
     return LIB_PATH
 
 

@@ -524,3 +524,21 @@ extern "C" int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q
                         (char*)workspace + fp8_widened_bytes(batch, pages_per_seq, page_size, num_kv_heads, head_dim),
                         need - fp8_widened_bytes(batch, pages_per_seq, page_size, num_kv_heads, head_dim), stream);
 }
+
+#ifdef PA_PREFILL_PHASES
+// (phase build only) Copies the first n words of the phase timestamps to
+// host memory / clears them all.
+extern "C" int pa_prefill_phases_read(unsigned long long* out, size_t n) {
+  if (!out || n > (size_t)8 * kPhaseSlots) return fail(PA_ERR_INVALID_ARGUMENT, "pa_prefill_phases_read: bad size");
+  return hipMemcpyFromSymbol(out, HIP_SYMBOL(g_prefill_phases), n * sizeof(unsigned long long)) == hipSuccess
+             ? PA_OK
+             : fail(PA_ERR_LAUNCH, "pa_prefill_phases_read: copy failed");
+}
+extern "C" int pa_prefill_phases_clear(void) {
+  void* g = nullptr;
+  if (hipGetSymbolAddress(&g, HIP_SYMBOL(g_prefill_phases)) != hipSuccess ||
+      hipMemset(g, 0, sizeof(g_prefill_phases)) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+    return fail(PA_ERR_LAUNCH, "pa_prefill_phases_clear: clear failed");
+  return PA_OK;
+}
+#endif

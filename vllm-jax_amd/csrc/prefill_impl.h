@@ -169,6 +169,36 @@ static __shared__ __attribute__((aligned(1024))) uint16_t k_lds[kStages][kTileEl
 static __shared__ __attribute__((aligned(1024))) uint16_t v_lds[kStages][kTileElems];
 static __shared__ int red_max[kWaves], red_min[kWaves];
 
+// Per-workgroup phase timestamps, only in a build with PA_PREFILL_PHASES
+// (libpaged_attention_phases.so; the library proper has none): s_memrealtime
+// (100 MHz) at the item's start, once its kv range is known, once its first
+// tile is in LDS, after the loop and after the stores, then the workgroup's
+// HW_ID | XCC_ID << 32 and its tile count, 8 words per workgroup id.
+#ifdef PA_PREFILL_PHASES
+constexpr int kPhaseSlots = 1 << 17;
+__device__ unsigned long long g_prefill_phases[8 * kPhaseSlots];
+#define PA_PHASE(t) const unsigned long long t = __builtin_amdgcn_s_memrealtime()
+__device__ __forceinline__ void prefill_phases_store(unsigned long long t0, unsigned long long t1,
+                                                     unsigned long long t2, unsigned long long t3,
+                                                     unsigned long long t4, int n_tiles) {
+  if (threadIdx.x != 0 || blockIdx.x >= kPhaseSlots) return;
+  unsigned long long* g = g_prefill_phases + 8 * (unsigned long long)blockIdx.x;
+  g[0] = t0;
+  g[1] = t1;
+  g[2] = t2;
+  g[3] = t3;
+  g[4] = t4;
+  const unsigned hw = __builtin_amdgcn_s_getreg((4) | (0 << 6) | (31 << 11));   // HW_ID
+  const unsigned xcc = __builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11));  // XCC_ID
+  g[5] = (unsigned long long)hw | ((unsigned long long)xcc << 32);
+  g[6] = (unsigned long long)n_tiles;
+}
+#else
+#define PA_PHASE(t) \
+  do {              \
+  } while (0)
+#endif
+
 // The aligned tile loads address a K/V row as a 32-bit per-lane offset from
 // a scalar page base: tile row r (< 64) plus a 16-byte chunk (< 128 elements)
 // is r * slot_stride + 8 * chunk elements, 2x that in bytes.  True when that
@@ -262,6 +292,7 @@ __device__ __forceinline__ bool prefill_resolve(const PrefillParams& p, int bid,
 // One prefill work item, run by a whole 512-thread workgroup.
 template <bool kSoftCap, bool kAligned>
 __device__ __forceinline__ void prefill_run(const PrefillParams& p, const PrefillWork& w) {
+  PA_PHASE(ph0);
   auto k_stage = [&](auto c) __attribute__((always_inline)) -> uint16_t* { return k_lds[decltype(c)::value]; };
   auto v_stage = [&](auto c) __attribute__((always_inline)) -> uint16_t* { return v_lds[decltype(c)::value]; };
 
@@ -343,6 +374,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   const int64_t kv_hi64 = min((int64_t)lk, (int64_t)qpos_max - kv_pos_off + 1);
   const int kv_hi = kv_hi64 < 0 ? 0 : (int)kv_hi64;
   const int n_tiles = (kv_hi + kTileN - 1) / kTileN;
+  PA_PHASE(ph1);
   // tiles [0, n_free) need no mask: every token is < lk and visible to every row
   const int64_t free_hi = min((int64_t)lk, (int64_t)qpos_min - kv_pos_off + 1);
   const int n_free = free_hi < 0 ? 0 : (int)(free_hi / kTileN);
@@ -710,6 +742,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     else wait_vm_lgkm0<0>();
     barrier();
   }
+  PA_PHASE(ph2);
 
   // iterations t = 0 .. n_tiles: QK(0) alone, then PV(t-1) + QK(t), then
   // PV(n_tiles-1) alone.  Tile t sits in stage t % 4.
@@ -736,6 +769,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   }
   if (!grp_b) barrier();
   wait_vm_lgkm0<0>();  // loads of tiles past the end may still be in flight
+  PA_PHASE(ph3);
 
   // ---- epilogue: row n = (token rtok, head rhead); acc_o[dt][i] holds
   // d = 32dt + 8(i/4) + 4h + i%4.  One permlane32 swap per dword pair gives
@@ -764,6 +798,10 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
 #pragma unroll
       for (int pr = 0; pr < 2; ++pr) st16(orow + 32 * dt + 16 * pr, ow[dt][pr]);
   }
+#ifdef PA_PREFILL_PHASES
+  PA_PHASE(ph4);
+  prefill_phases_store(ph0, ph1, ph2, ph3, ph4, n_tiles);
+#endif
 }
 
 // The work item numbered `bid`, resolved and run.
