@@ -29,7 +29,9 @@
 // XOR-swizzled per row so that both the K reads and the transposing V reads
 // are bank-conflict free.  KV tiles entirely above the causal diagonal of the
 // q tile are never loaded; the mask is evaluated only on tiles that straddle
-// it or the kv length.  Workgroups take their items from a work list sorted
+// it or the kv length.  The Q tile comes in and the O tile goes out through
+// each wave's own LDS blocks, four whole 256-byte rows per load or store.
+// Workgroups take their items from a work list sorted
 // by cost (prefill_plan in prefill.hip), longest first; without a list, from
 // the last q tile down.
 #pragma once
@@ -307,7 +309,6 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   const int h = lane >> 5;
   const int row = wave * 32 + n;
   const int rtok = tok0 + row / p.group;
-  const int rhead = row % p.group;
   const bool row_ok = row < p.tile_tokens * p.group && rtok < lq_rows;
   // Loads are unconditional from a clamped row (lq_rows >= 1 here): a load
   // under a branch makes the compiler wait for it at the branch join.  A lane
@@ -316,13 +317,34 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   const int ltok = min(rtok, lq_rows - 1);
   const int qpos_ld = p.positions[q0 + ltok];
 
-  // Q^T operand (B of S^T): k-step ks covers d = 16ks + 8h .. +8.  Issued
-  // before the position reduction below so that their latencies overlap.
+  // Wave w stages its Q rows and, at the end, its O rows in its own LDS:
+  // 1 KiB blocks 2w and 2w+1 of K and of V in every stage, the only blocks
+  // its own tile loads write (so no other wave's loads or reads can touch
+  // them at those times).  Piece j of stage pair st holds rows 8j .. 8j+7 of
+  // the wave, 256 bytes per row, with 16-byte chunk c of row r stored at
+  // chunk c ^ (r & 15) (conflict-free reads of one chunk from 16 rows).
+  auto piece = [&](int st, int j) __attribute__((always_inline)) -> uint32_t {
+    return (uint32_t)(uintptr_t)(lds_void_ptr)((j & 1) ? &v_lds[st + (j >> 1)][0] : &k_lds[st + (j >> 1)][0]) +
+           (uint32_t)(2048 * wave);
+  };
+  // row / group for rows < 256 as (row * gm) >> 24 (exact for group <= 256)
+  const uint32_t gm = (0x1000000u + (uint32_t)p.group - 1u) / (uint32_t)p.group;
+
+  // Q tile rows into stages 2 and 3 (free until tile 2 is issued, after the
+  // barrier below), four whole 256-byte rows per load: full cache lines, where
+  // a lane-per-row load would touch 32 lines a quarter each.  Issued before
+  // the position reduction below so that their latencies overlap.
   bf16x8 qt_op[8];
-  {
-    const uint16_t* qrow = p.q + (int64_t)(q0 + ltok) * p.q_ts + (int64_t)(kvh * p.group + rhead) * p.q_hs + 8 * h;
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) qt_op[ks] = as_bf16x8(ld16(qrow + 16 * ks));
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * i + (lane >> 4);
+    const int rw = wave * 32 + r;
+    const int tk = (int)(((uint32_t)rw * gm) >> 24);
+    const int hd = rw - tk * p.group;
+    const int lt = min(tok0 + tk, lq_rows - 1);
+    const int c = (lane & 15) ^ (r & 15);
+    dma16(p.q + (int64_t)(q0 + lt) * p.q_ts + (int64_t)(kvh * p.group + hd) * p.q_hs + 8 * c,
+          piece(2, i >> 1) + 1024 * (i & 1));
   }
   const int qpos = row_ok ? qpos_ld : 0;
   // raw page ids of the first three kv tiles, read while the loads above fly
@@ -347,9 +369,20 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     }
   }
 
-  // Retire every compiler-visible vector load here: the tile DMAs below are
-  // invisible to the compiler's wait tracking, so nothing it issued may still
-  // be in flight when they start (else it would drain them at the loop head).
+  // Retire every vector load here: the Q rows are in LDS, and the tile DMAs
+  // below are invisible to the compiler's wait tracking, so nothing it
+  // issued may still be in flight when they start (else it would drain them
+  // at the loop head).
+  wait_vm_lgkm0<0>();
+  asm volatile("" ::: "memory");  // the Q reads stay after the wait
+  // Q^T operand (B of S^T): lane (n, h)'s k-step ks is row n, d = 16ks + 8h
+  // .. +8, i.e. chunk 2ks + h
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks)
+    qt_op[ks] = as_bf16x8(
+        ds_read16((lds_cbytes)(uintptr_t)(piece(2, n >> 3) + 256 * (n & 7) + 16 * ((2 * ks + h) ^ (n & 15)))));
+  // read before any wave passes the barrier below (then tile 2 may overwrite
+  // stage 2)
   wait_vm_lgkm0<0>();
   if constexpr (!kSoftCap) {
     // Q^T scaled by scale * log2 e (rounded to bf16), so that S = K Q^T is in
@@ -771,32 +804,38 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   wait_vm_lgkm0<0>();  // loads of tiles past the end may still be in flight
   PA_PHASE(ph3);
 
-  // ---- epilogue: row n = (token rtok, head rhead); acc_o[dt][i] holds
-  // d = 32dt + 8(i/4) + 4h + i%4.  One permlane32 swap per dword pair gives
-  // lane (n, 0) d = 32dt + 16pr + 0..7 and lane (n, 1) d = 32dt + 16pr + 8..15,
-  // so every lane stores whole 16-byte pieces.  The swaps run on all lanes
-  // (lanes n and n + 32 share a row, hence row_ok).
+  // ---- epilogue.  acc_o[dt][i] of lane (n, h) holds row n, d = 32dt +
+  // 8(i/4) + 4h + i%4: four consecutive d per i/4, i.e. the h-th half of
+  // 16-byte chunk 4dt + i/4.  The normalised bf16 rows go to the wave's own
+  // blocks of stages 0 and 1 (every LDS read ended at the loop's last
+  // barrier, and this wave's own tile loads have landed), then out four
+  // whole 256-byte rows per store.
   const float l_run = sum_xor32((l_part[0] + l_part[1]) + (l_part[2] + l_part[3]));
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-  u32x4 ow[4][2];
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int pr = 0; pr < 2; ++pr) {
+    for (int q4 = 0; q4 < 4; ++q4) {
       const f32x16& a = acc_o[dt];
-      const int i = 8 * pr;
-      const uint32_t x0 = pack_bf16x2(a[i] * inv, a[i + 1] * inv), x1 = pack_bf16x2(a[i + 2] * inv, a[i + 3] * inv);
-      const uint32_t y0 = pack_bf16x2(a[i + 4] * inv, a[i + 5] * inv), y1 = pack_bf16x2(a[i + 6] * inv, a[i + 7] * inv);
-      const auto s0 = __builtin_amdgcn_permlane32_swap(x0, y0, false, false);
-      const auto s1 = __builtin_amdgcn_permlane32_swap(x1, y1, false, false);
-      ow[dt][pr] = u32x4{s0[0], s1[0], s0[1], s1[1]};
+      const int i = 4 * q4;
+      const u32x2 v = {pack_bf16x2(a[i] * inv, a[i + 1] * inv), pack_bf16x2(a[i + 2] * inv, a[i + 3] * inv)};
+      *reinterpret_cast<u32x2 __attribute__((address_space(3)))*>(
+          (uintptr_t)(piece(0, n >> 3) + 256 * (n & 7) + 16 * ((4 * dt + q4) ^ (n & 15)) + 8 * h)) = v;
     }
-  if (row_ok) {
-    uint16_t* orow = p.out + (int64_t)(q0 + rtok) * p.o_ts + (int64_t)(kvh * p.group + rhead) * p.o_hs + 8 * h;
+  // A fresh lane index: the row arithmetic below repeats the Q loads'
+  // expressions, which the compiler would otherwise carry through the loop.
+  int lane_e = lane;
+  asm volatile("" : "+v"(lane_e));
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int pr = 0; pr < 2; ++pr) st16(orow + 32 * dt + 16 * pr, ow[dt][pr]);
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * i + (lane_e >> 4);
+    const u32x4 v = ds_read16((lds_cbytes)(uintptr_t)(piece(0, r >> 3) + 256 * (r & 7) + 16 * (lane_e & 15)));
+    const int rw = wave * 32 + r;
+    const int tk = (int)(((uint32_t)rw * gm) >> 24);
+    const int hd = rw - tk * p.group;
+    const int c = (lane_e & 15) ^ (r & 15);
+    if (rw < p.tile_tokens * p.group && tok0 + tk < lq_rows)
+      st16(p.out + (int64_t)(q0 + tok0 + tk) * p.o_ts + (int64_t)(kvh * p.group + hd) * p.o_hs + 8 * c, v);
   }
 #ifdef PA_PREFILL_PHASES
   PA_PHASE(ph4);
