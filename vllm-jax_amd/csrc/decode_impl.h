@@ -16,11 +16,13 @@
 //   O^T[d][q] += V^T[d][t] . P^T[t][q]      8 x v_mfma_f32_16x16x16_bf16
 //
 // The q heads of one kv head sit in the N dimension, so the softmax row of a
-// lane is its accumulator column.  K is read as 64-byte row pieces in the MFMA
-// A layout; V as 16-byte pieces where each 16-lane group reads one whole
-// 256-byte token row, transposed in registers with v_perm_b32.  The M (d)
+// lane is its accumulator column.  K and V are read as 16-byte pieces where
+// each 16-lane group reads one whole 256-byte token row (full cache lines,
+// non-temporal).  V is transposed in registers with v_perm_b32: the M (d)
 // dimension of the PV MFMA is permuted so that M-tile j row m holds
-// d = 8m + j: a lane then owns the 8 contiguous d values of its V load.
+// d = 8m + j, and a lane then owns the 8 contiguous d values of its V load.
+// K goes through the wave's LDS into the row-per-lane MFMA A layout (pages
+// whose size is not a multiple of 16 read K in that layout directly).
 //
 // Workgroups are dealt round-robin to the 8 XCDs; the grid is renumbered so
 // that each XCD runs a contiguous range of (sequence, chunk, kv head) items.
@@ -104,9 +106,9 @@ __device__ __forceinline__ bool decode_has_row(const DecodeParams& p, int b) {
   return r0 >= 0 && r0 < p.row_limit && p.rows[b + 1] > r0;
 }
 
-// V rows are read exactly once and as whole 256-byte rows: stream them past
-// the caches.  K rows are read 64 bytes per row per instruction, so their
-// 128-byte lines stay cacheable for the instruction that reads the other half.
+// K and V rows are read exactly once and as whole rows: stream them past the
+// caches.  (Half-row K reads, 64 bytes per row per instruction, must stay
+// cacheable for the instruction that reads the other half.)
 __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
@@ -259,9 +261,11 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
         ksp = p.k_scales + sbase;
         vsp = p.v_scales + sbase;
       }
-      const int64_t krow = (int64_t)min(n, lim) * rs;
+      // K rows whole (128 bytes of codes, eight lanes a row), streamed: load r
+      // gives lane l row 8r + l / 8, 16-byte chunk l % 8
 #pragma unroll
-      for (int r = 0; r < kKLoads; ++r) kd[r] = ld16(kbase + krow + 64 * r + 16 * g);  // chunks kchunk(2r), kchunk(2r+1)
+      for (int r = 0; r < kKLoads; ++r)
+        kd[r] = ld16_stream(kbase + (int64_t)min(8 * r + (lane >> 3), lim) * rs + 16 * (lane & 7));
 #pragma unroll
       for (int i = 0; i < 4; ++i) vd[i] = ld8_stream(vbase + (int64_t)min(4 * g + i, lim) * rs + 8 * n);
       sb[j][0] = ld16(ksp);
@@ -279,9 +283,10 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
         vbase = p.v_cache + base;
         rs = p.slot_stride;
       }
-      const int64_t krow = (int64_t)min(n, lim) * rs;
+      // K rows whole (one 256-byte row per 16-lane group), streamed like V:
+      // load i gives lane (n, g) row 4i + g, chunk n
 #pragma unroll
-      for (int s = 0; s < 4; ++s) kd[s] = ld16(kbase + krow + 8 * (4 * s + g));
+      for (int i = 0; i < 4; ++i) kd[i] = ld16_stream(kbase + (int64_t)min(4 * i + g, lim) * rs + 8 * n);
 #pragma unroll
       for (int i = 0; i < 4; ++i) vd[i] = ld16_stream(vbase + (int64_t)min(4 * g + i, lim) * rs + 8 * n);
     } else {
@@ -310,16 +315,46 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
     const VBuf(&vdr)[4] = vb[j];
     const int t0 = t_begin + kDecodeStep * (kWaves * ks + wave);
     f32x4 sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      u32x4 kk;
+    if constexpr (kAligned) {
+      // The K A operand wants row n per lane (chunks kchunk(s)); the loads
+      // delivered whole rows across lanes.  The wave turns them round
+      // through its own slice of red_o (free until the combine), with chunk c
+      // of row r stored at c ^ (r mod rows-per-bank-cycle): conflict-free
+      // 16-byte writes and reads.
+      typedef u32x4 __attribute__((address_space(3))) * lds_u32x4;
+      const uint32_t kst = (uint32_t)(uintptr_t)(float __attribute__((address_space(3)))*)(red_o) +
+                           (uint32_t)(wave * 16 * kHeadDim * 4);
       if constexpr (kFp8) {
-        const u32x4& w = kd[s >> 1];
-        kk = fp8x8_to_bf16x8((s & 1) ? u32x2{w[2], w[3]} : u32x2{w[0], w[1]});
+#pragma unroll
+        for (int r = 0; r < kKLoads; ++r) {
+          const int row = 8 * r + (lane >> 3);
+          *(lds_u32x4)(uintptr_t)(kst + 128 * row + 16 * ((lane & 7) ^ (row & 7))) = kd[r];
+        }
+        u32x4 kr[kKLoads];
+#pragma unroll
+        for (int r = 0; r < kKLoads; ++r)  // row n, chunk 4r + g: the codes of k-steps 2r, 2r + 1
+          kr[r] = *(lds_u32x4)(uintptr_t)(kst + 128 * n + 16 * ((4 * r + g) ^ (n & 7)));
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const u32x4& w = kr[s >> 1];
+          const u32x4 kk = fp8x8_to_bf16x8((s & 1) ? u32x2{w[2], w[3]} : u32x2{w[0], w[1]});
+          sc = mfma16(as_bf16x8(kk), qt[s], sc);
+        }
       } else {
-        kk = kd[s];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * i + g;
+          *(lds_u32x4)(uintptr_t)(kst + 256 * r + 16 * (n ^ (r & 15))) = kd[i];
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const u32x4 kk = *(lds_u32x4)(uintptr_t)(kst + 256 * n + 16 * ((4 * s + g) ^ (n & 15)));
+          sc = mfma16(as_bf16x8(kk), qt[s], sc);
+        }
       }
-      sc = mfma16(as_bf16x8(kk), qt[s], sc);
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) sc = mfma16(as_bf16x8(kd[s]), qt[s], sc);
     }
     // lane holds S[q = n][token t0 + 4g + r]
     float x[4];
