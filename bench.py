@@ -228,7 +228,7 @@ def run_gpu(args):
             "frac_of_mfma_peak": round(p_tflops_kernel / MFMA_BF16_PEAK_TFLOPS, 4),
         },
         "roofline": {
-            "kernel": "prefill_kernel",
+            "kernel": "prefill_kernel_pooled",
             "bound": "mfma",
             "achieved": round(p_tflops_kernel, 2),
             "peak": MFMA_BF16_PEAK_TFLOPS,
