@@ -44,6 +44,9 @@ def _run_and_check(pkg, dev, db, seed, *, seqs=None, soft_cap=None):
     ([1100, 2049, 64, 1024], 8, 2, 16),                     # 16-token pages: 64 page ids per chunk
     ([5, 40, 1500, 2100], 8, 2, 24),                        # page size not a multiple of 16
     ([2048, 2049, 4097, 6000], 32, 8, 256),                 # chunk boundaries
+    ([1, 70, 2049, 300], 40, 2, 256),                       # G = 20: two blocks of q heads, the second partial
+    ([17, 1100, 2050], 32, 1, 16),                          # G = 32, 16-token pages, several chunks
+    ([0, 5, 600], 17, 1, 24),                               # G = 17, unaligned pages, length 0
 ])
 def test_decode_small(pkg, dev, lens, h, hkv, bs):
     # power-of-two table width: the oracle keeps the reference's split divisibility rules
@@ -143,4 +146,18 @@ def test_decode_work_list_all_sequences(pkg, dev):
     db = wl.make_decode(lens.tolist(), num_heads=32, num_kv_heads=8, page_size=256, rng=rng, table_width=width)
     print(f"decode work list: {db.batch} sequences, table width {width}", flush=True)
     out, _ = _run_and_check(pkg, dev, db, seed=31)
+    assert not u16(out)[0].any()
+
+
+def test_decode_work_list_many_q_heads_per_kv_head(pkg, dev):
+    """G = 64 (blocks of 16 q heads as separate work items) on a launch large
+    enough for the work list (64 sequences, 131 (sequence, chunk) pairs x 4 kv
+    heads x 4 blocks = 2096 items); every sequence against the oracle."""
+    rng = np.random.default_rng(57)
+    lens = rng.integers(1, 6000, 64)
+    lens[:4] = [0, 1, 2048, 4097]
+    width = 1 << (int(-(-6000 // 256)) - 1).bit_length()
+    db = wl.make_decode(lens.tolist(), num_heads=256, num_kv_heads=4, page_size=256, rng=rng, table_width=width)
+    print(f"decode G=64: {db.batch} sequences, table width {width}", flush=True)
+    out, _ = _run_and_check(pkg, dev, db, seed=57)
     assert not u16(out)[0].any()

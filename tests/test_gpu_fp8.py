@@ -72,6 +72,7 @@ def _run_fp8(pkg, dev, q, kq, vq, ks, vs, bt, lens, scale=1.0, soft_cap=None):
     ([1000, 2049, 64], 32, 8, 256, None),            # Qwen3-8B heads, two chunks
     ([5, 40, 1500, 2100], 16, 1, 32, None),          # G = 16
     ([700, 33], 8, 8, 64, 30.0),                     # MHA, soft cap
+    ([900, 2100, 3], 48, 2, 32, None),               # G = 24: two blocks of q heads
 ])
 def test_decode_fp8_matches_oracle(pkg, dev, lens, h, hkv, bs, cap):
     rng = np.random.default_rng(sum(lens) + h)

@@ -59,10 +59,10 @@ decode_split_kernel(DecodeParams p) {
   int item;
   if (p.plan) {
     // XCD x = bid % 8 takes ranks x, x + 8, x + 16, ... of the list, all
-    // kv heads of a rank in a row: the XCDs get near-equal token counts,
-    // and the kv heads of a token row (adjacent slices of one pool row) are
-    // read by one XCD at nearly the same time.
-    const int hkv = p.num_kv_heads;
+    // kv heads (and their q-head blocks) of a rank in a row: the XCDs get
+    // near-equal token counts, and the kv heads of a token row (adjacent
+    // slices of one pool row) are read by one XCD at nearly the same time.
+    const int hkv = p.num_kv_heads * p.hblocks;
     const int k = blockIdx.x >> 3;
     const int kr = k / hkv;
     const int r = 8 * kr + (blockIdx.x & 7);
@@ -203,8 +203,6 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
   if (head_dim != kHeadDim)
     return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported (only %d)", name, head_dim, kHeadDim);
   const int group = num_heads / num_kv_heads;
-  if (group > 16)
-    return fail(PA_ERR_UNSUPPORTED, "%s: %d q heads per kv head not supported (max 16)", name, group);
   if (fp8 && page_size % kDecodeStep != 0)
     return fail(PA_ERR_UNSUPPORTED, "%s: float8 pages need page_size %% %d == 0 (got %d)", name, kDecodeStep,
                 page_size);
@@ -246,6 +244,7 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
   prm.num_heads = num_heads;
   prm.num_kv_heads = num_kv_heads;
   prm.group = group;
+  prm.hblocks = (group + 15) / 16;
   prm.chunk = decode_chunk_tokens(page_size);
   prm.n_chunks = pages_per_seq > 0 ? decode_chunks(pages_per_seq, page_size) : 0;
   prm.soft_cap = soft_cap > 0.f ? soft_cap : 0.f;
@@ -262,10 +261,11 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
 
   hipStream_t s = (hipStream_t)stream;
   const int64_t pairs = (int64_t)batch * prm.n_chunks;
+  const int64_t vheads = (int64_t)num_kv_heads * prm.hblocks;  // work items per (sequence, chunk)
   // The work list pays for its launch once the grid is several waves of
   // workgroups deep (two per CU, 256 CUs).
-  const bool planned = pairs > 0 && pairs * num_kv_heads >= kDecodePlanMinItems;
-  const int64_t blocks = planned ? (pairs + 7) / 8 * 8 * num_kv_heads : pairs * num_kv_heads;
+  const bool planned = pairs > 0 && pairs * vheads >= kDecodePlanMinItems;
+  const int64_t blocks = planned ? (pairs + 7) / 8 * 8 * vheads : pairs * vheads;
   if (blocks > 0x7fffffff)
     return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)blocks);
   if (planned) {

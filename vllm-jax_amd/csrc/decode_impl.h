@@ -69,6 +69,10 @@ struct DecodeParams {
   int32_t pages_per_seq;
   const int32_t* lengths;
   int32_t batch, num_heads, num_kv_heads, group;
+  // q heads of a kv head are taken 16 at a time (the MFMA's N columns): a
+  // work item is one of hblocks = ceil(group / 16) blocks of them, and reads
+  // its kv head's K/V itself
+  int32_t hblocks;
   int32_t chunk;     // tokens per workgroup
   int32_t n_chunks;  // chunks of the widest block-table row
   float logit_scale;  // scale * log2(e) when soft_cap is off, else scale
@@ -164,8 +168,12 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int hkv = p.num_kv_heads;
-  const int kvh = item % hkv;
-  const int rest = item / hkv;
+  const int vheads = hkv * p.hblocks;  // (kv head, block of 16 q heads) pairs
+  const int vh = item % vheads;
+  const int rest = item / vheads;
+  const int kvh = vh / p.hblocks;
+  const int qc0 = 16 * (vh - kvh * p.hblocks);  // first q column (head within the group) of this item
+  const int g_end = min(p.group, qc0 + 16);
   const int chunk = rest % p.n_chunks;
   const int b = rest / p.n_chunks;
   // lengths past the block table's span are clamped to it (no read beyond the table row)
@@ -176,8 +184,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
     if (chunk == 0 && p.zero_empty) {
       // length 0: the G output rows of this kv head are zero
       const int64_t orow = decode_row(p, b) * p.out_bs;
-      for (int c = threadIdx.x; c < p.group * (kHeadDim / 8); c += 64 * kWaves)
-        st16(p.out + orow + (int64_t)(kvh * p.group + c / (kHeadDim / 8)) * p.out_hs + 8 * (c % (kHeadDim / 8)),
+      for (int c = threadIdx.x; c < (g_end - qc0) * (kHeadDim / 8); c += 64 * kWaves)
+        st16(p.out + orow + (int64_t)(kvh * p.group + qc0 + c / (kHeadDim / 8)) * p.out_hs + 8 * (c % (kHeadDim / 8)),
              u32x4{0, 0, 0, 0});
     }
     return;
@@ -209,8 +217,8 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
   };
   bf16x8 qt[4];
   {
-    const bool live = n < p.group;
-    const uint16_t* qrow = p.q + decode_row(p, b) * p.q_bs + (int64_t)(kvh * p.group + (live ? n : 0)) * p.q_hs;
+    const bool live = qc0 + n < g_end;
+    const uint16_t* qrow = p.q + decode_row(p, b) * p.q_bs + (int64_t)(kvh * p.group + qc0 + (live ? n : 0)) * p.q_hs;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       u32x4 v = live ? ld16(qrow + 8 * kchunk(s)) : u32x4{0, 0, 0, 0};
@@ -458,10 +466,10 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
       for (int i = 0; i < 4; ++i) o[4 * i4 + i] += sw * a[i];
     }
   }
-  if (n >= p.group) return;
+  if (qc0 + n >= g_end) return;
   if (n_chunks_b == 1) {
     const float inv = 1.f / ll;  // ll >= 1: the chunk holds a visible token
-    uint16_t* dst = p.out + decode_row(p, b) * p.out_bs + (int64_t)(kvh * p.group + n) * p.out_hs + d0;
+    uint16_t* dst = p.out + decode_row(p, b) * p.out_bs + (int64_t)(kvh * p.group + qc0 + n) * p.out_hs + d0;
     if constexpr (kDPerLane == 8) {
       u32x4 w;
 #pragma unroll
@@ -474,7 +482,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
       *reinterpret_cast<u32x2*>(dst) = w;
     }
   } else {
-    const int64_t part = (((int64_t)b * hkv + kvh) * p.n_chunks + chunk) * p.group + n;
+    const int64_t part = (((int64_t)b * hkv + kvh) * p.n_chunks + chunk) * p.group + qc0 + n;
     float* dst = p.ws_o + part * kHeadDim + d0;
 #pragma unroll
     for (int i4 = 0; i4 < kDPerLane / 4; ++i4)

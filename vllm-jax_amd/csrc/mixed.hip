@@ -397,6 +397,7 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
   dp.num_heads = num_heads;
   dp.num_kv_heads = num_kv_heads;
   dp.group = group;
+  dp.hblocks = 1;  // group <= 16 here
   dp.chunk = mixed_decode_chunk(page_size);
   dp.n_chunks = n_chunks;
   dp.soft_cap = cap;
