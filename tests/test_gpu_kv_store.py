@@ -96,3 +96,23 @@ def test_gather_bit_exact(pkg, dev):
     out = pkg.gather_kv(cache, torch.as_tensor(bt, device=dev), torch.as_tensor(lens, device=dev))
     torch.cuda.synchronize()
     assert np.array_equal(u16(out), ora.gather_kv(u16(cache), bt, lens))
+
+
+def test_kv_store_duplicate_slot_check(pkg, dev, monkeypatch):
+    """With PA_CHECK_SLOTS=1 the stores refuse a slot mapping that writes one
+    slot twice, before any device write; without it the store runs (the
+    winner of the duplicated slot is unspecified, as in the reference)."""
+    import torch
+    cache = torch.zeros((2, 4, 16, 2, 128), dtype=torch.bfloat16, device=dev)
+    k = torch.ones((3, 2, 128), dtype=torch.bfloat16, device=dev)
+    v = torch.ones_like(k)
+    sm = torch.tensor([5, 9, 5], dtype=torch.int32, device=dev)
+    monkeypatch.setenv("PA_CHECK_SLOTS", "1")
+    with pytest.raises(ValueError, match="slot 5 from tokens"):
+        pkg.update_kv_cache(cache, sm, k, v)
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(cache)) == 0
+    pkg.update_kv_cache(cache, torch.tensor([5, 9, 6], dtype=torch.int32, device=dev), k, v)
+    monkeypatch.delenv("PA_CHECK_SLOTS")
+    pkg.update_kv_cache(cache, sm, k, v)
+    torch.cuda.synchronize()

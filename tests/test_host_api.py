@@ -109,3 +109,17 @@ def test_bf16_scale_constants():
     from vllm_jax_amd.kernels._common import inv_sqrt_head_dim_bf16, bf16_round
     assert inv_sqrt_head_dim_bf16(128) == 0.08837890625        # bf16(1/sqrt(128))
     assert bf16_round(128 ** 0.5) == 11.3125                    # bf16(sqrt(128)), qwen3.py:207
+
+
+def test_check_slot_mapping_finds_duplicates():
+    """The debug check of the store's contract (qwen3.py:109-110 leaves the
+    winner of a duplicated slot unspecified): slots outside the pool are
+    ignored, a slot written twice is named with its tokens."""
+    from vllm_jax_amd.attention import check_slot_mapping
+    check_slot_mapping(torch.tensor([3, 1, -1, -1, 7, 100], dtype=torch.int32), 64)  # -1 twice, 100 outside
+    check_slot_mapping(torch.tensor([], dtype=torch.int32), 64)
+    with pytest.raises(ValueError, match=r"1 slot\(s\) more than once: slot 5 from tokens \[1, 4\]"):
+        check_slot_mapping(torch.tensor([0, 5, 6, 7, 5], dtype=torch.int32), 64)
+    with pytest.raises(ValueError, match="2 slot"):
+        check_slot_mapping(torch.tensor([9, 9, 2, 2, 63], dtype=torch.int32), 64)
+    check_slot_mapping(torch.tensor([9, 9, 64, 64], dtype=torch.int32)[2:], 64)  # both past the pool

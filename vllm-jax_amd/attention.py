@@ -21,6 +21,7 @@ prefill or decode kernel.  Differences from the reference, all deliberate:
 """
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass, field
 from typing import Optional, Tuple, Union
 
@@ -78,6 +79,34 @@ class MixedAttentionMetadata:
 AttentionMetadata = Union[DecodeAttentionMetadata, PrefillAttentionMetadata, MixedAttentionMetadata]
 
 
+def check_slot_mapping(slot_mapping: torch.Tensor, num_slots: int) -> None:
+    """Debug check of the store's contract: no two tokens may write one slot.
+
+    The reference's scatter (``.at[slot].set(..., mode="drop")``,
+    qwen3.py:109-110) leaves the winner of a duplicated slot unspecified, and
+    so do the store kernels here (the tokens' rows race).  Slots outside
+    ``[0, num_slots)`` are skipped by the store and ignored here.  Raises
+    ``ValueError`` naming the first duplicated slot.  It synchronises the
+    device, so the stores run it only when the environment sets
+    ``PA_CHECK_SLOTS=1``.
+    """
+    s = slot_mapping.reshape(-1).to(torch.int64)
+    s = s[(s >= 0) & (s < num_slots)]
+    if s.numel() < 2:
+        return
+    u, counts = torch.unique(s, return_counts=True)
+    dup = u[counts > 1]
+    if dup.numel():
+        first = int(dup[0])
+        tokens = torch.nonzero(slot_mapping.reshape(-1).to(torch.int64) == first).reshape(-1)[:4].tolist()
+        raise ValueError(f"slot_mapping writes {dup.numel()} slot(s) more than once: slot {first} "
+                         f"from tokens {tokens}")
+
+
+def _checking_slots() -> bool:
+    return os.environ.get("PA_CHECK_SLOTS", "") == "1"
+
+
 def update_kv_cache(kv_cache: torch.Tensor, slot_mapping: torch.Tensor, k: torch.Tensor,
                     v: torch.Tensor) -> torch.Tensor:
     """In-place KV store: ``kv_cache[0].flat[slot[t]] = k[t]``, same for v.
@@ -98,6 +127,8 @@ def update_kv_cache(kv_cache: torch.Tensor, slot_mapping: torch.Tensor, k: torch
         raise ValueError(f"k/v must be [T, {hkv}, {d}], got {tuple(k.shape)} and {tuple(v.shape)}")
     if slot_mapping.dtype != torch.int32 or tuple(slot_mapping.shape) != (k.shape[0],):
         raise ValueError("slot_mapping must be int32 of shape [T]")
+    if _checking_slots():
+        check_slot_mapping(slot_mapping, nb * bs)
     kc, vc = kv_cache[0], kv_cache[1]
     sm = slot_mapping if slot_mapping.is_contiguous() else slot_mapping.contiguous()
     _lib.call(
@@ -150,6 +181,8 @@ def qk_norm_rope_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm
     factor = 1.0
     if rope_scaling is not None and rope_scaling.get("type") in {"linear", "dynamic"}:
         factor = float(rope_scaling.get("factor", 1.0))
+    if _checking_slots():
+        check_slot_mapping(slot_mapping, nb * bs)
     if out is None:
         out = torch.empty_like(q)
     kc, vc = kv_cache[0], kv_cache[1]
@@ -193,6 +226,8 @@ def update_kv_cache_fp8(kv_codes: torch.Tensor, kv_scales: torch.Tensor, slot_ma
     t_count = k.shape[0]
     if slot_mapping.dtype != torch.int32 or tuple(slot_mapping.shape) != (t_count,):
         raise ValueError("slot_mapping must be int32 of shape [T]")
+    if _checking_slots():
+        check_slot_mapping(slot_mapping, nb * bs)
     kc, vc = kv_codes[0], kv_codes[1]
     ks, vs = kv_scales[0], kv_scales[1]
     sm = slot_mapping.contiguous()
