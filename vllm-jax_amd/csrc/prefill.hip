@@ -239,9 +239,13 @@ fp8_pages_plan_kernel(const int32_t* __restrict__ bt, int64_t bt_stride, int32_t
   if (tid == 0) *count = n_slots;
 }
 
-// Slot i of the compact pool: the page of entry owner[i], widened.  One
-// workgroup per possible slot (the table's entry count); those past the
-// number of distinct pages return at once.  16 codes per thread and step.
+// Slot i of the compact pool: the page of entry owner[i], widened.
+// kWidenSplit workgroups per possible slot (the table's entry count), each
+// taking a kWidenSplit-th of the page's (slot, head) rows: with one
+// workgroup per page too few loads were in flight (a distinct page is
+// 1 MiB of codes); those past the number of distinct pages return at once.
+// 16 codes per thread and step.
+constexpr int kWidenSplit = 16;
 __global__ void __launch_bounds__(256)
 fp8_pages_widen_kernel(const uint8_t* __restrict__ k8, const uint8_t* __restrict__ v8,
                        const float* __restrict__ ks, const float* __restrict__ vs, int32_t num_pages,
@@ -250,13 +254,17 @@ fp8_pages_widen_kernel(const uint8_t* __restrict__ k8, const uint8_t* __restrict
                        int64_t bt_stride, int32_t pages_per_seq, const int32_t* __restrict__ cu_q,
                        const int32_t* __restrict__ cu_k, int32_t num_kv_heads, const int32_t* __restrict__ owner,
                        const int32_t* __restrict__ count, uint16_t* __restrict__ wk, uint16_t* __restrict__ wv) {
-  const int32_t sl = blockIdx.x;
+  const int32_t sl = blockIdx.x / kWidenSplit;
+  const int part_w = blockIdx.x - sl * kWidenSplit;
   if (sl >= *count) return;
   const int64_t page =
       fp8_entry_page(bt, bt_stride, pages_per_seq, page_size, num_pages, cu_q, cu_k, owner[sl]);  // in use
   const int rows = page_size * num_kv_heads;  // (slot, head) rows of 128 codes
   const int64_t wbase = (int64_t)sl * rows * kPHeadDim;
-  for (int c = threadIdx.x; c < rows * 8; c += 256) {
+  const int c_lo = (int)((int64_t)rows * 8 * part_w / kWidenSplit);
+  const int c_hi = (int)((int64_t)rows * 8 * (part_w + 1) / kWidenSplit);
+#pragma unroll 4
+  for (int c = c_lo + threadIdx.x; c < c_hi; c += 256) {
     const int r = c >> 3, part = c & 7;  // 16 codes of row r
     const int slot = r / num_kv_heads, h = r - slot * num_kv_heads;
     const int64_t src = page * page_stride + (int64_t)slot * slot_stride + (int64_t)h * head_stride + 16 * part;
@@ -493,7 +501,7 @@ extern "C" int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q
     return fail(PA_ERR_WORKSPACE, "pa_prefill_fp8: 256-byte aligned workspace of %zu bytes needed, %zu given", need,
                 workspace_bytes);
   const int64_t entries = (int64_t)batch * pages_per_seq;
-  if (entries > 0x7fffffff)
+  if (entries > 0x7fffffff / kWidenSplit)
     return fail(PA_ERR_UNSUPPORTED, "pa_prefill_fp8: %lld table entries", (long long)entries);
   const int64_t page_elems = (int64_t)page_size * num_kv_heads * head_dim;
   uint16_t* wk = reinterpret_cast<uint16_t*>(workspace);
@@ -511,7 +519,7 @@ extern "C" int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q
                                                        n_slots);
   int rc = launch_status("pa_prefill_fp8(plan)");
   if (rc) return rc;
-  fp8_pages_widen_kernel<<<dim3((unsigned)entries), dim3(256), 0, s>>>(
+  fp8_pages_widen_kernel<<<dim3((unsigned)(entries * kWidenSplit)), dim3(256), 0, s>>>(
       k_cache, v_cache, k_scales, v_scales, num_pages, page_size, page_stride, slot_stride, head_stride,
       scale_page_stride, scale_head_stride, block_tables, bt_stride, pages_per_seq, cu_seqlens_q, cu_seqlens_k,
       num_kv_heads, owner, n_slots, wk, wv);
