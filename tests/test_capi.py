@@ -33,6 +33,20 @@ def test_library_exports_every_declared_symbol():
     assert set(declared) <= set(PKG._lib.SIGNATURES)
 
 
+def test_phase_timestamp_build_exports_its_readers():
+    """The prefill build with per-workgroup phase stamps (a measurement
+    library, never loaded by the package) carries the prefill entry points
+    and the stamp readers; the library proper has no stamps."""
+    path = os.path.join(ROOT, "vllm-jax_amd", "libpaged_attention_phases.so")
+    assert os.path.exists(path), "build the libraries first (__graft_entry__.build())"
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (pa_\w+)$", out, re.M))
+    assert {"pa_prefill", "pa_prefill_workspace_size", "pa_prefill_phases_read", "pa_prefill_phases_clear"} <= exported
+    proper = subprocess.run(["nm", "-D", "--defined-only", PKG._lib.lib_path()], capture_output=True, text=True,
+                            check=True).stdout
+    assert "pa_prefill_phases" not in proper
+
+
 def test_error_codes_match_header():
     text = open(HEADER).read()
     codes = dict(re.findall(r"#define (PA_\w+) \(?(-?\d+)\)?", text))
@@ -60,7 +74,10 @@ def test_decode_rejects_bad_arguments_without_a_device():
     assert "divisible" in lib.pa_last_error().decode()
     assert lib.pa_decode(*_decode_args(head_dim=64)) == -2
     assert "head_dim" in lib.pa_last_error().decode()
-    assert lib.pa_decode(*_decode_args(heads=64, kv_heads=2)) == -2   # 32 q heads per kv head
+    # 32 q heads per kv head are accepted (two blocks of 16 per work item):
+    # these arguments then fail only on their null pointers
+    assert lib.pa_decode(*_decode_args(heads=64, kv_heads=2)) == -1
+    assert "null pointer" in lib.pa_last_error().decode()
     assert lib.pa_decode(*_decode_args(batch=0)) == 0                  # nothing to do
     assert lib.pa_decode(*_decode_args(page_size=0)) == -1
 
