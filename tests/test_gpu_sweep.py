@@ -1,13 +1,16 @@
 """Seeded random sweep of the device entries against the oracle.
 
 Every case draws its shape from one seed: the q heads per kv head
-(G in 1, 2, 4, 8, 16), the kv heads, the page size (aligned and unaligned
+(G in 1, 2, 4, 8, 16; decode also 20 and 32), the kv heads, the page size (aligned and unaligned
 to the 64-token prefill tile and the 16-token decode step), the batch, q
 lengths including 0 and 1, cached prefixes and the soft cap.  The prefill
 cases run through the kernel entry, hence with the work list.  Bar as in the
 per-entry tests: max-abs 2e-2 on bf16 outputs, zero rows exactly zero.
+PA_SWEEP_SEEDS=n runs n seeds per sweep instead of the default counts.
 """
 from __future__ import annotations
+
+import os
 
 import numpy as np
 import pytest
@@ -21,10 +24,15 @@ TOL = 2e-2
 PAGE_SIZES = [16, 24, 32, 48, 64, 128, 256]
 
 
-def _heads(rng, max_g=16):
-    g = int(rng.choice([g for g in (1, 2, 4, 8, 16) if g <= max_g]))
+def _heads(rng, max_g=16, groups=(1, 2, 4, 8, 16)):
+    g = int(rng.choice([g for g in groups if g <= max_g]))
     hkv = int(rng.choice([1, 2, 4, 8] if g <= 8 else [1, 2, 4]))
     return g * hkv, hkv
+
+
+def _seeds(default):
+    n = os.environ.get("PA_SWEEP_SEEDS")
+    return range(int(n) if n else default)
 
 
 def _prefill_case(seed):
@@ -43,7 +51,7 @@ def _prefill_case(seed):
 
 def _decode_case(seed):
     rng = np.random.default_rng(2000 + seed)
-    h, hkv = _heads(rng)
+    h, hkv = _heads(rng, max_g=32, groups=(1, 2, 4, 8, 16, 20, 32))
     bs = int(rng.choice(PAGE_SIZES))
     batch = int(rng.integers(1, 17))
     lens = rng.integers(1, 5000, batch)
@@ -53,7 +61,7 @@ def _decode_case(seed):
     return h, hkv, bs, lens.tolist(), cap
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", _seeds(16))
 def test_prefill_sweep(pkg, dev, seed):
     import torch
     h, hkv, bs, new, prefix, cap = _prefill_case(seed)
@@ -79,7 +87,7 @@ def test_prefill_sweep(pkg, dev, seed):
     assert err <= TOL and np.isfinite(got).all()
 
 
-@pytest.mark.parametrize("seed", range(16))
+@pytest.mark.parametrize("seed", _seeds(16))
 def test_decode_sweep(pkg, dev, seed):
     import torch
     h, hkv, bs, lens, cap = _decode_case(seed)
@@ -105,7 +113,7 @@ def test_decode_sweep(pkg, dev, seed):
     assert not got[np.asarray(lens) == 0].any()
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", _seeds(8))
 def test_mixed_sweep(pkg, dev, seed):
     import torch
     from test_gpu_mixed import _case, _run
@@ -137,7 +145,7 @@ def test_mixed_sweep(pkg, dev, seed):
     assert not got[zero].any()
 
 
-@pytest.mark.parametrize("seed", range(6))
+@pytest.mark.parametrize("seed", _seeds(6))
 def test_fp8_sweep(pkg, dev, seed):
     """Quantized decode and prefill over the same random float8 pool."""
     import torch
