@@ -217,7 +217,8 @@ def _raw_prefill(pkg, t, pb, workspace, max_seqlen=None):
 
 def _expected_list(pb, num_tokens, max_seqlen):
     """Per (sequence, q tile) pair with rows: its geometry and kv-tile cost
-    (contiguous-position estimate), as the work list must hold them."""
+    class (contiguous-position estimate, classes of 16 kv tiles), as the
+    work list must hold them."""
     g = pb.num_heads // pb.num_kv_heads
     tt = 256 // g
     nq = -(-max_seqlen // tt)
@@ -234,7 +235,7 @@ def _expected_list(pb, num_tokens, max_seqlen):
                 continue
             off = int(pb.input_positions[q0]) - (lk - lq)
             hi = min(lk, lk - lq + min(qt * tt + tt, rows))
-            cost = min((-(-hi // 64) if hi > 0 else 0) + 1, 4095)
+            cost = min((-(-hi // 64) if hi > 0 else 0) // 16 + 1, 4095)
             want[(b, qt)] = (q0, rows, lk, off, cost)
     return want
 
@@ -242,8 +243,9 @@ def _expected_list(pb, num_tokens, max_seqlen):
 @pytest.mark.parametrize("case", ["prefix", "many", "padded"])
 def test_prefill_work_list(pkg, dev, case):
     """The work list (caller workspace) holds every (sequence, q tile) pair
-    with rows once, with its geometry, in non-increasing cost; and the
-    output with the list is bit-identical to the grid-order output without."""
+    with rows once, with its geometry, in non-increasing cost class, a
+    sequence's q tiles of one class in descending order; and the output with
+    the list is bit-identical to the grid-order output without."""
     import torch
     if case == "prefix":
         pb = wl.make_prefix_prefill([0, 300, 512, 40, 1500, 3], [130, 64, 200, 1, 700, 260], num_heads=32,
@@ -278,7 +280,13 @@ def test_prefill_work_list(pkg, dev, case):
         q0, rows, lk, off, cost = want[key]
         assert tuple(int(x) for x in r[2:6]) == (q0, rows, lk, off), (key, r)
         costs.append(cost)
-    assert all(a >= b for a, b in zip(costs, costs[1:])), "work list not in non-increasing cost"
+    assert all(a >= b for a, b in zip(costs, costs[1:])), "work list not in non-increasing cost class"
+    # inside a class, a sequence's q tiles appear costliest (last) first
+    last_qt = {}
+    for r, c in zip(rec, costs):
+        key = (c, int(r[0]))
+        assert int(r[1]) < last_qt.get(key, 1 << 30), (key, int(r[1]))
+        last_qt[key] = int(r[1])
 
 
 def test_prefill_more_sequences_than_the_planner_holds(pkg, dev):

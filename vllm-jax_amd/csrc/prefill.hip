@@ -46,16 +46,22 @@ prefill_kernel_pooled(PrefillParams p) {
 
 constexpr int kPrepThreads = 1024;
 constexpr int64_t kPoolMinItems = 16384;  // smallest grid that uses prefill_kernel_pooled
-constexpr int kPlanBins = 4096;       // cost classes of the work list (kv tiles + 1, clamped)
+constexpr int kPlanBins = 4096;       // cost classes of the work list (class + 1, clamped)
+constexpr int kPlanClassTiles = 16;   // kv tiles per cost class
 constexpr int kPlanMaxBatch = 2048;   // sequences whose geometry the planner keeps in LDS
 
 // Work list of the prefill (run by one workgroup).  A pair (sequence b,
 // q tile qt) is listed when the tile has rows; its cost is the number of kv
 // tiles its last row sees, estimated as if positions were contiguous (the
 // list orders the work and changes no result).  Pairs are counting-sorted by
-// cost, largest first, so the longest items start first and no long item is
-// left for the end.  Per sequence, q0 / lq_rows / lk / kv_pos_off are derived
-// exactly as prefill_resolve derives them without a list.
+// cost in classes of kPlanClassTiles kv tiles, largest first, so the longest
+// items start first and no long item is left for the end.  Inside a class a
+// sequence's q tiles stay together (costliest first), in runs of up to 64
+// pairs: the workgroups an XCD runs at one time then stream the K/V of a few
+// sequences, which its L2 holds (Qwen3-32B long prefill -2.7 %, prefix-cached
+// -2.2 % against a list sorted by exact cost with the sequences interleaved).
+// Per sequence, q0 / lq_rows / lk / kv_pos_off are derived exactly as
+// prefill_resolve derives them without a list.
 __device__ void prefill_plan(const PrefillParams& p, int32_t* __restrict__ plan) {
   __shared__ int32_t hist[kPlanBins];
   __shared__ int4 seqs[kPlanMaxBatch];  // q0, lq_rows, lk, kv_pos_off
@@ -67,10 +73,12 @@ __device__ void prefill_plan(const PrefillParams& p, int32_t* __restrict__ plan)
   __syncthreads();
   const int nq = p.n_qtiles;
   const int pairs = p.batch * nq;
+  // pair i: sequence i / nq, q tile nq - 1 - i % nq (a sequence's tiles in a
+  // row, costliest first); bin: its cost class
   auto bin_of = [&](int i) -> int {  // 0: no rows
     const int b = i / nq;
-    const int tiles = prefill_pair_tiles(seqs[b], lag[b], i - b * nq, p.tile_tokens);
-    return tiles < 0 ? 0 : min(tiles + 1, kPlanBins - 1);
+    const int tiles = prefill_pair_tiles(seqs[b], lag[b], nq - 1 - (i - b * nq), p.tile_tokens);
+    return tiles < 0 ? 0 : min(tiles / kPlanClassTiles + 1, kPlanBins - 1);
   };
   for (int64_t ii = tid; ii < pairs; ii += kPrepThreads) {
     const int i = (int)ii;
@@ -94,15 +102,28 @@ __device__ void prefill_plan(const PrefillParams& p, int32_t* __restrict__ plan)
     run += cnt[j];
   }
   __syncthreads();
-  for (int64_t ii = tid; ii < pairs; ii += kPrepThreads) {
-    const int i = (int)ii;
-    const int c = bin_of(i);
+  const int lane = tid & 63;
+  for (int64_t i0 = tid - lane; i0 < pairs; i0 += kPrepThreads) {  // whole waves (uniform trip count)
+    const int i = (int)i0 + lane;
+    const int c = i < pairs ? bin_of(i) : 0;
+    // ranks for this wave's 64 consecutive pairs, class by class, in lane order
+    uint64_t todo = __ballot(c != 0);
+    int rank = 0;
+    while (todo) {
+      const int lead = __ffsll((unsigned long long)todo) - 1;
+      const int cc = __shfl(c, lead);
+      const uint64_t m = __ballot(c == cc);
+      int base = 0;
+      if (lane == lead) base = atomicAdd(&hist[cc], __popcll(m));
+      base = __shfl(base, lead);
+      if (c == cc) rank = base + __popcll(m & ((1ull << lane) - 1));
+      todo &= ~m;
+    }
     if (!c) continue;
-    const int rank = atomicAdd(&hist[c], 1);
     const int b = i / nq;
     const int4 sq = seqs[b];
     int32_t* r = plan + kPlanHeader + 8 * rank;
-    st16(r, u32x4{(uint32_t)b, (uint32_t)(i - b * nq), (uint32_t)sq.x, (uint32_t)sq.y});
+    st16(r, u32x4{(uint32_t)b, (uint32_t)(nq - 1 - (i - b * nq)), (uint32_t)sq.x, (uint32_t)sq.y});
     st16(r + 4, u32x4{(uint32_t)sq.z, (uint32_t)sq.w, 0u, 0u});
   }
   if (tid == 0) {
