@@ -13,24 +13,30 @@ prefill_kernel(PrefillParams p) {
   prefill_body<kSoftCap, kAligned>(p, blockIdx.x);
 }
 
-// The item of workgroup `bid` with the shared pool: every XCD walks the
-// whole list (n items, one kv head of every entry, as prefill_resolve deals
-// them), but only its first n - s items statically (workgroup 8 k + x runs
-// XCD x's k-th item).  The last s items of every XCD, the cheapest, form a
-// pool that the workgroups dispatched after the static ones claim in list
-// order with one atomicAdd.  The 8 XCDs finish identical static work up to
-// 6 % apart (clock and memory differ per XCD); the XCDs that run ahead
-// reach their pool workgroups first and take more of the pool.  -1: nothing
-// left.
+// The item of workgroup `bid` with the pools: every XCD walks the whole list
+// (n items, one kv head of every entry, as prefill_resolve deals them), but
+// only its first n - s items statically (workgroup 8 k + x runs XCD x's k-th
+// item).  The last s items of every XCD, the cheapest, form that XCD's pool,
+// claimed in list order with one atomicAdd on its counter by the workgroups
+// dispatched after the static ones.  A workgroup takes from its own XCD's
+// pool first (its items' K/V is in that XCD's L2) and steals from the next
+// XCDs' pools once it is empty.  The 8 XCDs finish identical static work up
+// to 6 % apart (clock and memory differ per XCD); the XCDs that run ahead
+// reach their pool workgroups first and take more.  -1: nothing left.
 __device__ __forceinline__ int prefill_pooled_item(const PrefillParams& p, int bid) {
   const int n = p.plan[0] * (p.num_kv_heads >> 3);  // items of one XCD
   const int s = n >> 2;
   if (bid < 8 * (n - s)) return bid;
-  // a plain read first: once the pool is exhausted late workgroups leave
-  // without an atomic (the counter only grows, so a stale value errs late)
-  if (__hip_atomic_load(p.pool, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= 8 * s) return -1;
-  const int j = atomicAdd(p.pool, 1);  // pool item j: XCD j % 8's item n - s + j / 8
-  return j < 8 * s ? 8 * (n - s + (j >> 3)) + (j & 7) : -1;
+  const int x = bid & 7;
+  for (int i = 0; i < 8; ++i) {
+    const int y = (x + i) & 7;
+    // a plain read first: a spent pool is passed without an atomic (the
+    // counter only grows, so a stale value errs late)
+    if (__hip_atomic_load(p.pool + y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= s) continue;
+    const int j = atomicAdd(p.pool + y, 1);  // XCD y's item n - s + j
+    if (j < s) return 8 * (n - s + j) + y;
+  }
+  return -1;
 }
 
 template <bool kSoftCap, bool kAligned>
@@ -128,7 +134,7 @@ __device__ void prefill_plan(const PrefillParams& p, int32_t* __restrict__ plan)
   }
   if (tid == 0) {
     plan[0] = count;
-    plan[8] = 0;  // the shared pool's counter (prefill_kernel_pooled)
+    for (int i = 8; i < 16; ++i) plan[i] = 0;  // the pools' counters (prefill_kernel_pooled)
   }
 }
 

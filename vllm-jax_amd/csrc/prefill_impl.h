@@ -80,9 +80,9 @@ struct PrefillParams {
   // Work list (may be null): plan[0] = number of (sequence, q tile) pairs with
   // rows, PrefillPair records from int kPlanHeader on, most kv tiles first.
   const int32_t* plan;
-  // With the work list and num_kv_heads % 8 == 0: the counter of its shared
-  // pool (plan + 8, zeroed by the list builder), see prefill_kernel_pooled;
-  // null otherwise.
+  // With the work list and num_kv_heads % 8 == 0: the counters of the eight
+  // XCDs' pools (plan + 8 .. plan + 15, zeroed by the list builder), see
+  // prefill_kernel_pooled; null otherwise.
   int32_t* pool;
 };
 
