@@ -167,9 +167,11 @@ def test_mixed_workspace_size():
     part = r256(2 * 16 * 2 * (128 + 2) * 4)
     assert lib.pa_mixed_workspace_size(4, 2, 100, 16, 8, 128, 1, 8192) == part + 256 + 32 * 8
     assert lib.pa_mixed_workspace_size(4, 2, 100, 16, 8, 128, 1, 4096) == 256 + 32 * 8
-    # more than 16 q heads per kv head is refused (pa_mixed refuses it too)
+    # G = 32: two decode pairs per (sequence, chunk), one per block of 16 q heads;
+    # 8-token q tiles (13 per prefill sequence)
+    assert lib.pa_mixed_workspace_size(4, 2, 100, 32, 1, 128, 8, 256) == 256 + 32 * 32
+    # more q heads per kv head than the 256 rows of a prefill item is refused
     assert lib.pa_mixed_workspace_size(4, 2, 100, 512, 1, 128, 8, 256) == 0
-    assert lib.pa_mixed_workspace_size(4, 2, 100, 32, 1, 128, 8, 256) == 0
 
 
 def test_large_slot_stride_is_refused_by_the_aligned_tile_loads():

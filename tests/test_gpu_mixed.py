@@ -67,6 +67,8 @@ def _run(pkg, dev, q, kc, vc, bt, cu, kv, pos, nd, max_q, soft_cap=None):
     ([3000, 5000, 100], [90], [0], 8, 2, 48, 0),                           # 48-token pages, 3072-token chunks
     ([], [17, 128, 300], [0, 0, 0], 16, 8, 256, 0),                        # no decode sequence
     ([10, 600, 4096], [], [], 16, 8, 256, 1),                              # no prefill sequence
+    ([700, 30, 0], [100, 7], [0, 20], 40, 2, 64, 0),                       # G = 20: a 16 + 4 head split
+    ([5000, 300], [90, 1], [0, 0], 32, 1, 256, 0),                         # G = 32 (one kv head), 2 chunks
 ])
 def test_mixed_matches_oracle(pkg, dev, dec, pre_q, pre_p, h, hkv, bs, pad):
     rng = np.random.default_rng(len(dec) * 100 + h + bs)
@@ -84,6 +86,24 @@ def test_mixed_matches_oracle(pkg, dev, dec, pre_q, pre_p, h, hkv, bs, pad):
         zero[cu[b]:cu[b + 1]] = False
     zero[cu[:nd][kv[:nd] == 0]] = True      # empty decode context
     assert not got[zero].any()
+
+
+def test_mixed_work_list_many_q_heads_per_kv_head(pkg, dev):
+    """1100 decode sequences with 32 q heads on one kv head and three prefill
+    sequences: 2 200 decode items of 16 q heads (two per sequence) put the
+    launch on the work-list path, which lists each block of 16 q heads as
+    its own entry."""
+    rng = np.random.default_rng(77)
+    dec = rng.integers(0, 400, 1100).tolist()
+    pre_q, pre_p = [150, 9, 260], [0, 40, 300]
+    q, kc, vc, bt, cu, kv, pos = _case(rng, dec, pre_q, pre_p, 32, 1, 32)
+    nd = len(dec)
+    got = _run(pkg, dev, q, kc, vc, bt, cu, kv, pos, nd, max(pre_q))
+    want = ora.mixed_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, kv, pos, nd)
+    err = np.abs(ora.bf16_to_f32(got) - ora.bf16_to_f32(want)).max()
+    print(f"mixed (work list, G = 32) max-abs err {err:.3e}")
+    assert err <= TOL
+    assert not got[cu[:nd][kv[:nd] == 0]].any()
 
 
 def test_mixed_prefill_noncontiguous_positions(pkg, dev):

@@ -58,6 +58,9 @@ def test_prefill_qwen3_06b_config(pkg, dev):
     ([150, 300], 64, 8, 256),                  # G = 8 (Qwen3-32B heads)
     ([100, 33], 8, 8, 32),                     # MHA
     ([257, 40], 16, 1, 64),                    # G = 16
+    ([300, 41], 40, 2, 64),                    # G = 20: 12-token q tiles, rows 240-255 idle
+    ([200, 77], 32, 1, 256),                   # G = 32 (one kv head)
+    ([90, 3], 64, 1, 16),                      # G = 64: 4-token q tiles
     ([129], 4, 4, 256),
 ])
 def test_prefill_shapes(pkg, dev, lens, h, hkv, bs):

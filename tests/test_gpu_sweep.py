@@ -1,7 +1,7 @@
 """Seeded random sweep of the device entries against the oracle.
 
 Every case draws its shape from one seed: the q heads per kv head
-(G in 1, 2, 4, 8, 16; decode also 20 and 32), the kv heads, the page size (aligned and unaligned
+(G in 1, 2, 4, 8, 16, 20, 32), the kv heads, the page size (aligned and unaligned
 to the 64-token prefill tile and the 16-token decode step), the batch, q
 lengths including 0 and 1, cached prefixes and the soft cap.  The prefill
 cases run through the kernel entry, hence with the work list.  Bar as in the
@@ -24,7 +24,7 @@ TOL = 2e-2
 PAGE_SIZES = [16, 24, 32, 48, 64, 128, 256]
 
 
-def _heads(rng, max_g=16, groups=(1, 2, 4, 8, 16)):
+def _heads(rng, max_g=32, groups=(1, 2, 4, 8, 16, 20, 32)):
     g = int(rng.choice([g for g in groups if g <= max_g]))
     hkv = int(rng.choice([1, 2, 4, 8] if g <= 8 else [1, 2, 4]))
     return g * hkv, hkv
@@ -51,7 +51,7 @@ def _prefill_case(seed):
 
 def _decode_case(seed):
     rng = np.random.default_rng(2000 + seed)
-    h, hkv = _heads(rng, max_g=32, groups=(1, 2, 4, 8, 16, 20, 32))
+    h, hkv = _heads(rng)
     bs = int(rng.choice(PAGE_SIZES))
     batch = int(rng.integers(1, 17))
     lens = rng.integers(1, 5000, batch)

@@ -60,7 +60,8 @@ struct MixedParams {
   DecodeParams dec;   // the decode sequences (entries 0 .. num_decodes-1)
   // Work list (may be null): plan[0] = entries, records of 8 ints from
   // kPlanHeader on, costliest first: {0, b, qt, q0, lq_rows, lk, kv_pos_off}
-  // for a prefill q tile, {1, b, chunk} for a decode chunk.  With a list,
+  // for a prefill q tile, {1, b, chunk, hb} for block hb of 16 q heads (of
+  // every kv head) of a decode chunk.  With a list,
   // [0, r3) are list items and [r3, r4) the zero pass.
   const int32_t* plan;
   int32_t r1, r2, r3, r4;
@@ -124,14 +125,14 @@ mixed_plan_kernel(MixedParams m, int32_t* __restrict__ plan) {
   for (int i = tid; i < kMixedPlanBins; i += kMixedPlanThreads) hist[i] = 0;
   for (int b = tid; b < pp.batch; b += kMixedPlanThreads) prefill_seq_geometry(pp, b, seqs[b], lag[b]);
   __syncthreads();
-  const int nc = dp.n_chunks, nq = pp.n_qtiles;
-  const int dec_pairs = dp.batch * nc;
+  const int nc = dp.n_chunks, nq = pp.n_qtiles, hb = dp.hblocks;
+  const int dec_pairs = dp.batch * nc * hb;
   const int pairs = dec_pairs + pp.batch * nq;
   const int span = dp.pages_per_seq * dp.page_size;
   auto bin_of = [&](int i) -> int {  // 0: nothing to do
     int cost;
     if (i < dec_pairs) {
-      const int b = i / nc, c = i - b * nc;
+      const int bc = i / hb, b = bc / nc, c = bc - b * nc;
       const int t0 = c * dp.chunk;
       const int len = min(dp.lengths[b], span);
       if (t0 >= len && c > 0) return 0;
@@ -172,8 +173,8 @@ mixed_plan_kernel(MixedParams m, int32_t* __restrict__ plan) {
     if (!c) continue;
     int32_t* r = plan + kPlanHeader + 8 * atomicAdd(&hist[c], 1);
     if (i < dec_pairs) {
-      const int b = i / nc;
-      st16(r, u32x4{1u, (uint32_t)b, (uint32_t)(i - b * nc), 0u});
+      const int bc = i / hb, b = bc / nc;
+      st16(r, u32x4{1u, (uint32_t)b, (uint32_t)(bc - b * nc), (uint32_t)(i - bc * hb)});
       st16(r + 4, u32x4{0u, 0u, 0u, 0u});
     } else {
       const int j = i - dec_pairs, b = j / nq;
@@ -213,7 +214,7 @@ mixed_kernel(MixedParams m) {
     const int kind = e[0], b = e[1], sub = e[2];
     if (r >= count) return;  // uniform over the workgroup
     if (kind) {
-      dec = (b * m.dec.n_chunks + sub) * hkv + h;
+      dec = ((b * m.dec.n_chunks + sub) * hkv + h) * m.dec.hblocks + e[3];
     } else {
       w = PrefillWork{b, sub, h, e[3], e[4], e[5], e[6]};
       pre = true;
@@ -271,20 +272,23 @@ static size_t mixed_partials_bytes(int32_t num_decodes, int32_t num_heads, int32
   return ((size_t)num_decodes * num_heads * chunks * ((size_t)head_dim + 2) * sizeof(float) + 255) / 256 * 256;
 }
 
+// Decode pairs (sequence, chunk, block of 16 q heads) and prefill pairs
+// (sequence, q tile) of the work list; each pair is one item per kv head.
 static int64_t mixed_pairs(int32_t batch, int32_t num_decodes, int32_t max_seqlen_q, int32_t num_heads,
                            int32_t num_kv_heads, int32_t pages_per_seq, int32_t page_size) {
   const int chunks = pages_per_seq > 0 ? mixed_decode_chunks(pages_per_seq, page_size) : 0;
-  const int64_t tile_tokens = kRows / (num_heads / num_kv_heads);
+  const int group = num_heads / num_kv_heads;
+  const int64_t tile_tokens = kRows / group;
   const int64_t n_pre = batch - num_decodes;
   const int64_t n_qtiles = n_pre > 0 ? (max_seqlen_q + tile_tokens - 1) / tile_tokens : 0;
-  return (int64_t)num_decodes * chunks + n_pre * n_qtiles;
+  return (int64_t)num_decodes * chunks * ((group + 15) / 16) + n_pre * n_qtiles;
 }
 
 extern "C" size_t pa_mixed_workspace_size(int32_t batch, int32_t num_decodes, int32_t max_seqlen_q,
                                           int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                           int32_t pages_per_seq, int32_t page_size) {
   if (batch < 0 || num_decodes < 0 || num_decodes > batch || max_seqlen_q < 0 || num_heads <= 0 ||
-      num_kv_heads <= 0 || num_heads % num_kv_heads || num_heads / num_kv_heads > 16 || head_dim <= 0 ||
+      num_kv_heads <= 0 || num_heads % num_kv_heads || num_heads / num_kv_heads > kRows || head_dim <= 0 ||
       pages_per_seq < 0 || page_size <= 0)
     return 0;
   const int chunks = pages_per_seq > 0 ? mixed_decode_chunks(pages_per_seq, page_size) : 0;
@@ -319,8 +323,8 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
   if (head_dim != kPHeadDim)
     return fail(PA_ERR_UNSUPPORTED, "pa_mixed: head_dim %d not supported (only %d)", head_dim, kPHeadDim);
   const int group = num_heads / num_kv_heads;
-  if (group > 16)
-    return fail(PA_ERR_UNSUPPORTED, "pa_mixed: %d q heads per kv head not supported (max 16)", group);
+  if (group > kRows)
+    return fail(PA_ERR_UNSUPPORTED, "pa_mixed: %d q heads per kv head not supported (max %d)", group, kRows);
   if (num_tokens == 0) return PA_OK;
   if (!q || !out || !cu_seqlens_q || !input_positions ||
       (batch > 0 && (!k_cache || !v_cache || !block_tables || !kv_lens)))
@@ -397,7 +401,7 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
   dp.num_heads = num_heads;
   dp.num_kv_heads = num_kv_heads;
   dp.group = group;
-  dp.hblocks = 1;  // group <= 16 here
+  dp.hblocks = (group + 15) / 16;  // a decode item covers 16 q heads of one kv head
   dp.chunk = mixed_decode_chunk(page_size);
   dp.n_chunks = n_chunks;
   dp.soft_cap = cap;
@@ -433,7 +437,7 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
   if (num_decodes == 0) head_levels = pp.n_qtiles;
   const int64_t pre_items = (int64_t)pp.n_qtiles * pairs;
   const int64_t pre_head = (int64_t)head_levels * pairs;
-  const int64_t dec_items = (int64_t)num_decodes * n_chunks * num_kv_heads;
+  const int64_t dec_items = (int64_t)num_decodes * n_chunks * num_kv_heads * dp.hblocks;
   const int64_t r1 = round8(pre_head);
   const int64_t r2 = r1 + round8(dec_items);
   const int64_t r3 = r2 + (pre_items - pre_head);
