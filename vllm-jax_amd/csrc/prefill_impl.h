@@ -175,14 +175,16 @@ static __shared__ int red_max[kWaves], red_min[kWaves];
 // (libpaged_attention_phases.so; the library proper has none): s_memrealtime
 // (100 MHz) at the item's start, once its kv range is known, once its first
 // tile is in LDS, after the loop and after the stores, then the workgroup's
-// HW_ID | XCC_ID << 32 and its tile count, 8 words per workgroup id.
+// HW_ID | XCC_ID << 32, its tile count and its item (sequence | q tile << 24
+// | kv head << 48), 8 words per workgroup id.
 #ifdef PA_PREFILL_PHASES
 constexpr int kPhaseSlots = 1 << 17;
 __device__ unsigned long long g_prefill_phases[8 * kPhaseSlots];
 #define PA_PHASE(t) const unsigned long long t = __builtin_amdgcn_s_memrealtime()
 __device__ __forceinline__ void prefill_phases_store(unsigned long long t0, unsigned long long t1,
                                                      unsigned long long t2, unsigned long long t3,
-                                                     unsigned long long t4, int n_tiles) {
+                                                     unsigned long long t4, int n_tiles, int b, int qt,
+                                                     int kvh) {
   if (threadIdx.x != 0 || blockIdx.x >= kPhaseSlots) return;
   unsigned long long* g = g_prefill_phases + 8 * (unsigned long long)blockIdx.x;
   g[0] = t0;
@@ -194,6 +196,7 @@ __device__ __forceinline__ void prefill_phases_store(unsigned long long t0, unsi
   const unsigned xcc = __builtin_amdgcn_s_getreg((20) | (0 << 6) | (3 << 11));  // XCC_ID
   g[5] = (unsigned long long)hw | ((unsigned long long)xcc << 32);
   g[6] = (unsigned long long)n_tiles;
+  g[7] = (unsigned long long)b | ((unsigned long long)qt << 24) | ((unsigned long long)kvh << 48);
 }
 #else
 #define PA_PHASE(t) \
@@ -839,7 +842,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   }
 #ifdef PA_PREFILL_PHASES
   PA_PHASE(ph4);
-  prefill_phases_store(ph0, ph1, ph2, ph3, ph4, n_tiles);
+  prefill_phases_store(ph0, ph1, ph2, ph3, ph4, n_tiles, b, qt, kvh);
 #endif
 }
 

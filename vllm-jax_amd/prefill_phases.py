@@ -8,18 +8,24 @@ kernel stamps ``s_memrealtime`` (100 MHz) at five points of every item:
     T0 item start          T1 kv range and tile count known
     T2 first tile in LDS   T3 loop done (all tiles)   T4 output stored
 
-and records the workgroup's CU (HW_ID, XCC_ID) and tile count.  From these
+and records the workgroup's CU (HW_ID, XCC_ID), tile count and item.  From these
 the script reports the mean / median / p90 of each phase, the gap between one
 workgroup's T4 and the next workgroup's T0 on the same CU (one 8-wave
 workgroup fills a CU), each CU's first start and last end, the last end per
 XCD, and the share of CU time that is not tile work (phases T0-T2 and
-T3-T4 plus the gaps).
+T3-T4 plus the gaps).  A table per XCD gives the workgroups and kv tiles it
+ran, its loop time per tile and its CUs' last ends.
 
 Usage (one GPU)::
 
     python3 vllm-jax_amd/prefill_phases.py long     # Qwen3-32B, 8 x ~26.7k tokens
     python3 vllm-jax_amd/prefill_phases.py prefix   # Qwen3-8B prefix-cached
     python3 vllm-jax_amd/prefill_phases.py short    # 64 x 1024 tokens, 16/8 heads
+    python3 vllm-jax_amd/prefill_phases.py prefix --dump stamps.npy
+
+``--dump FILE`` also saves the raw records (one row of 8 uint64 per
+workgroup that ran an item: T0..T4, HW_ID | XCC_ID << 32, tiles,
+sequence | q tile << 24 | kv head << 48) with numpy.save.
 
 The instrumented kernel is timed too; the stamps add a few stores per
 workgroup and the run is within a percent of the library proper.
@@ -81,6 +87,13 @@ def main(argv):
     lib = _load(pkg)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    dump = None
+    if "--dump" in argv:
+        i = argv.index("--dump")
+        if i + 1 >= len(argv):
+            raise SystemExit("--dump needs a file name")
+        dump = argv[i + 1]
+        argv = argv[:i] + argv[i + 2:]
     title, pb, seed = _workload(wl, argv[0] if argv else "prefix")
     t = wl.materialize_prefill(pb, seed=seed, device=dev, fill_pool=True)
     kv = t["kv_cache"]
@@ -122,6 +135,8 @@ def main(argv):
         raise RuntimeError(lib.pa_last_error().decode(errors="replace"))
     g = buf.reshape(-1, 8)
     g = g[g[:, 0] > 0]
+    if dump:
+        np.save(dump, g)
     T = (g[:, :5].astype(np.float64) - float(g[:, 0].min())) / 100.0  # microseconds from the first start
     ph = np.diff(T, axis=1)
     tiles = g[:, 6].astype(np.float64)
@@ -170,8 +185,14 @@ def main(argv):
           f"{(fixed + gaps.sum()) / total * 100:.1f} % of CU time between first start and last end")
     print(f"- CU first start: max {max(firsts):.1f} us; CU last end: min {min(lasts):.1f}, "
           f"p50 {np.median(lasts):.1f}, max {max(lasts):.1f} us; CU busy mean {np.mean(busy):.1f} us of {span:.1f}")
-    print("- last end per XCD (us, min / max over its CUs): "
-          + ", ".join(f"{x}: {min(v):.0f} / {max(v):.0f}" for x, v in sorted(xcd_last.items())))
+    print()
+    print("| XCD | workgroups | kv tiles | loop us per tile | last end us (min / max over its CUs) |")
+    print("|---|---|---|---|---|")
+    for x, v in sorted(xcd_last.items()):
+        sel = xcc == x
+        nt = max(float(tiles[sel].sum()), 1.0)
+        print(f"| {x} | {int(sel.sum())} | {int(tiles[sel].sum())} | {ph[sel, 2].sum() / nt:.3f} | "
+              f"{min(v):.0f} / {max(v):.0f} |")
     sys.stdout.flush()
     return 0
 
