@@ -92,6 +92,68 @@ def run_copy(args):
             "ms_per_step": round(ms, 4), "steps": args.steps}
 
 
+def run_head_dims(args):
+    """Prefill and decode at head sizes 64, 96, 128 and 256 on the same
+    shapes: 16 sequences of 2 048 new tokens (32 q / 8 kv heads, 256-token
+    pages) and the Qwen3-8B-shaped decode batch (256 sequences, contexts
+    U[512, 8192], pool sized to the batch).  128 runs the tuned kernels, the
+    other sizes the generic ones.  Attention only (the pages are filled
+    beforehand); HIP events over `steps` launches after `warmup`."""
+    import torch
+    import __graft_entry__ as ge
+    pkg = ge.load_package()
+    import vllm_jax_amd.workloads as wl
+    dev = torch.device("cuda:0")
+    lens_d = np.random.default_rng(2).integers(512, 8193, size=256)
+    pre, dec = [], []
+    for d in (64, 96, 128, 256):
+        pb = wl.make_prefill([2048] * 16, num_heads=32, num_kv_heads=8, head_dim=d, rng=np.random.default_rng(9))
+        t = wl.materialize_prefill(pb, seed=9, device=dev, fill_pool=True)
+        kp, vp = t["kv_cache"][0].permute(2, 0, 1, 3), t["kv_cache"][1].permute(2, 0, 1, 3)
+        out = torch.empty_like(t["q"])
+
+        def attn():
+            pkg.prefill_paged_attention(t["q"], kp, vp, t["block_tables"], t["cu_seqlens_q"], t["slot_mapping"],
+                                        t["input_positions"], max_seqlen_bucket=pb.max_seqlen_bucket,
+                                        cu_seqlens_k=t["cu_seqlens_k"], out=out)
+        ms = _time_ms(torch, attn, args)
+        tf = pb.flops() / (ms * 1e-3) / 1e12
+        pre.append({"head_dim": d, "ms": round(ms, 4), "tflops": round(tf, 1),
+                    "frac_of_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)})
+        del t, kp, vp, out
+        db = wl.make_decode(lens_d, num_heads=32, num_kv_heads=8, head_dim=d, rng=np.random.default_rng(2))
+        dd = wl.materialize_decode(db, seed=2, device=dev)
+        kv = dd["kv_cache"]
+        kpd, vpd = kv[0].permute(2, 0, 1, 3), kv[1].permute(2, 0, 1, 3)
+        outd = torch.empty_like(dd["q"])
+
+        def dec_call():
+            pkg.decode_paged_attention(dd["q"], kpd, vpd, dd["block_tables"], dd["context_lens"], out=outd)
+        ms = _time_ms(torch, dec_call, args)
+        gbs = db.hbm_bytes() / (ms * 1e-3) / 1e9
+        dec.append({"head_dim": d, "ms": round(ms, 4), "gbs": round(gbs, 1),
+                    "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)})
+        del dd, kv, kpd, vpd, outd
+        torch.cuda.empty_cache()
+    return {"metric": "attention at head sizes 64 / 96 / 128 / 256 (128: tuned kernels; others: generic)",
+            "prefill": {"workload": "16 x 2048 new tokens, 32 q / 8 kv heads, causal", "results": pre},
+            "decode": {"workload": "256 sequences, contexts U[512, 8192], 32 q / 8 kv heads", "results": dec},
+            "steps": args.steps, "warmup": args.warmup}
+
+
+def _time_ms(torch, fn, args):
+    for _ in range(args.warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / args.steps
+
+
 def run_gpu(args):
     import torch
     import __graft_entry__ as ge
@@ -664,7 +726,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU oracle work (total)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["prefill", "decode", "rope", "mixed", "decode_fp8", "prefix", "prefill_fp8",
-                                       "copy"],
+                                       "copy", "head_dims"],
                     default=None,
                     help="profiling aid: run one kernel family only (the JSON line then covers that part)")
     args = ap.parse_args()
@@ -675,6 +737,9 @@ def main():
         sys.exit(2)
     if args.only == "copy":
         print(json.dumps(run_copy(args)), flush=True)
+        return
+    if args.only == "head_dims":
+        print(json.dumps(run_head_dims(args)), flush=True)
         return
     res, ctx = run_gpu(args)
     if args.only is not None:

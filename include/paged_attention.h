@@ -25,8 +25,13 @@
  * past the pool are clamped into it, and slots outside [0, pages*page_size)
  * are skipped by the KV store.
  *
- * Supported shapes: head_dim == 128, num_heads % num_kv_heads == 0,
- * num_heads / num_kv_heads <= 16 for decode and <= 256 for prefill.
+ * Supported shapes: num_heads % num_kv_heads == 0, and
+ *   - head_dim 128 in every entry (the tuned kernels); pa_prefill, pa_decode
+ *     and pa_decode_noalloc also take any multiple of 16 from 16 to 256
+ *     (generic kernels, same arithmetic, lower throughput); float8 pages and
+ *     pa_mixed take 128 only;
+ *   - q heads per kv head: any number for decode, up to 256 for prefill and
+ *     pa_mixed (up to 128 for prefill at head sizes other than 128).
  */
 #ifndef VLLM_JAX_AMD_PAGED_ATTENTION_H_
 #define VLLM_JAX_AMD_PAGED_ATTENTION_H_

@@ -72,8 +72,12 @@ def test_decode_rejects_bad_arguments_without_a_device():
     rc = lib.pa_decode(*_decode_args(heads=30))
     assert rc == -1
     assert "divisible" in lib.pa_last_error().decode()
-    assert lib.pa_decode(*_decode_args(head_dim=64)) == -2
+    # head sizes other than 128 go to the generic kernels: multiples of 16 up to 256
+    assert lib.pa_decode(*_decode_args(head_dim=100)) == -2
     assert "head_dim" in lib.pa_last_error().decode()
+    assert lib.pa_decode(*_decode_args(head_dim=272)) == -2
+    assert lib.pa_decode(*_decode_args(head_dim=64)) == -1       # accepted; fails on the null pointers
+    assert "null pointer" in lib.pa_last_error().decode()
     # 32 q heads per kv head are accepted (two blocks of 16 per work item):
     # these arguments then fail only on their null pointers
     assert lib.pa_decode(*_decode_args(heads=64, kv_heads=2)) == -1
@@ -90,8 +94,12 @@ def test_prefill_rejects_bad_arguments_without_a_device():
     bad_div[19] = 15
     assert lib.pa_prefill(*bad_div) == -1
     bad_dim = list(args)
-    bad_dim[21] = 96
+    bad_dim[21] = 100
     assert lib.pa_prefill(*bad_dim) == -2
+    assert "head_dim" in lib.pa_last_error().decode()
+    other_dim = list(args)   # a multiple of 16: accepted, then fails on the null pointers
+    other_dim[21] = 96
+    assert lib.pa_prefill(*other_dim) == -1
     empty = list(args)
     empty[17] = 0   # num_tokens == 0: nothing to write
     assert lib.pa_prefill(*empty) == 0

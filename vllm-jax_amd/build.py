@@ -24,7 +24,7 @@ PHASES_LIB_PATH = os.path.join(PKG_DIR, "libpaged_attention_phases.so")
 ARCH = "gfx950"
 
 SOURCES = ["pa_errors.cpp", "block_manager.cpp", "kv_store.hip", "decode.hip", "prefill.hip", "qk_norm_rope.hip",
-           "mixed.hip"]
+           "mixed.hip", "any_head.hip"]
 PHASES_SOURCES = ["pa_errors.cpp", "prefill.hip"]
 
 # Packed-FP32 VALU forms are disabled for every device compile: the build

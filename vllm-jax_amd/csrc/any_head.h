@@ -1,0 +1,28 @@
+// Paged attention for head sizes other than 128: launchers of the kernels in
+// any_head.hip, called by pa_prefill and pa_decode when head_dim != 128.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace pa {
+
+struct PrefillParams;
+struct DecodeParams;
+
+constexpr int kAnyRows = 128;  // q rows (token, head) per prefill workgroup
+
+// True for the head sizes the kernels of any_head.hip are built for: the
+// multiples of 16 from 16 to 256 other than 128 (the tuned kernels' size).
+bool any_head_dim(int head_dim);
+
+// Zero pass and prefill of `p` (filled as for the tuned kernel; the work
+// list and pools are not used) with `head_dim`-wide rows.  Returns a PA_*
+// code.
+int prefill_any_launch(const char* name, const PrefillParams& p, int head_dim, hipStream_t s);
+
+// Split kernel and merge of `p` (filled as for the tuned kernel, with
+// head_dim-wide partials in the workspace; no work list) with `head_dim`-wide
+// rows.  Returns a PA_* code.
+int decode_any_launch(const char* name, const DecodeParams& p, int head_dim, hipStream_t s);
+
+}  // namespace pa

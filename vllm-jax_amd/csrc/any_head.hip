@@ -1,0 +1,507 @@
+// Paged attention for head sizes other than 128 (multiples of 16 from 16 to
+// 256): a prefill kernel and a split-K decode kernel with its merge.  The
+// reference takes any head size as long as q and the pages agree
+// (prefill_paged_attention.py:199-203, decode_paged_attention.py:356-360);
+// the tuned kernels of prefill.hip / decode.hip are built for 128, and these
+// cover the rest with the same arithmetic: S in f32 on the matrix core from
+// bf16 q and K, exp2 online softmax, P rounded to bf16 for PV, f32 O.
+//
+// Both kernels use v_mfma_f32_32x32x16_bf16 (lane layouts in pa_common.h)
+// in the same two products per 32-token kv step:
+//   S^T = K Q^T     A = K rows (m = token, from the staged K tile), B = Q^T
+//                   (n = q row or head);
+//                   lane (n, h = lane / 32) ends with column n's logits of
+//                   tokens 8(i/4) + 4h + i%4, i < 16;
+//   O^T += V^T P^T  A = V^T (m = d), B = P^T (n as above): the lane's own
+//                   eight P values of k-step u, tokens 16u + 8(e/4) + 4h +
+//                   e%4, fill its k slots 8h + e.
+// K and V are staged row-major in LDS with whole-row 16-byte writes.  An
+// A operand of V^T is eight 2-byte reads (d = the lane's row, the eight
+// tokens of its k slots): the 32 lanes of a read take 32 consecutive d of
+// one token, so the reads do not conflict.  The online-softmax state of a
+// column lives in the two lanes (n, 0) and (n, 1), exactly where O^T's
+// column n lives, so the rescale needs no exchange.
+#include <climits>
+
+#include "any_head.h"
+#include "decode_impl.h"
+#include "prefill_impl.h"
+
+namespace pa {
+namespace {
+
+constexpr int kAnyWaves = 4;                 // prefill waves per workgroup, 32 q rows each
+constexpr int kAnyStep = 32;                 // kv tokens per step (the MFMA's M)
+
+template <int D>
+struct AnyDims {
+  static_assert(D % 16 == 0 && D >= 16 && D <= 256, "head size");
+  static constexpr int kKs = D / 16;         // k-steps of S = K Q^T
+  static constexpr int kDt = (D + 31) / 32;  // 32-row blocks of O^T
+  static constexpr int kChunks = D / 8;      // 16-byte chunks of a K / V row
+  static constexpr int kRow = 2 * D + 16;    // bytes per K / V row in LDS (16 bytes of padding)
+  // the V tile: the last rows' V^T operands of a partial 32-row block read
+  // up to 16 bytes past the tile
+  static constexpr int kVTile = kAnyStep * kRow + 32;
+};
+
+typedef char __attribute__((address_space(3))) lds_char;
+
+// A operand of V^T for rows d0 .. d0 + 31 and k-step u from the row-major
+// V tile (rows of `row` bytes): lane (m, h) takes d = d0 + m of the tokens
+// 16u + 4h + {0,1,2,3} and 16u + 8 + 4h + {0,1,2,3}.  Rows d >= the head
+// size read the row padding or the next row: finite or not, they only feed
+// rows of O^T that are never stored.
+template <int kRowBytes>
+__device__ __forceinline__ u32x4 vt_operand(const lds_char* v, int d0, int u, int lane) {
+  typedef const uint16_t __attribute__((address_space(3))) lds_u16;
+  const lds_char* col = v + 2 * (d0 + (lane & 31)) + (16 * u + 4 * (lane >> 5)) * kRowBytes;
+  u32x4 a;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int t = (q & 1) * 2 + (q >> 1) * 8;  // token offsets 0, 2, 8, 10 (pairs t, t + 1)
+    const uint32_t lo = *reinterpret_cast<lds_u16*>(col + t * kRowBytes);
+    const uint32_t hi = *reinterpret_cast<lds_u16*>(col + (t + 1) * kRowBytes);
+    a[q] = lo | (hi << 16);
+  }
+  return a;
+}
+
+__device__ __forceinline__ u32x4 lds_ld16(const lds_char* a) {
+  return *reinterpret_cast<const u32x4 __attribute__((address_space(3)))*>(a);
+}
+__device__ __forceinline__ void lds_st16(lds_char* a, const u32x4& v) {
+  *reinterpret_cast<u32x4 __attribute__((address_space(3)))*>(a) = v;
+}
+
+// Logit in log2 units: x * scale * log2 e, or with the soft cap
+// cap * log2 e * tanh(x * scale / cap) (scale = logit_scale of the params).
+template <bool kSoftCap>
+__device__ __forceinline__ float any_logit(float x, float logit_scale, float cap) {
+  if constexpr (kSoftCap) return cap * kLog2e * tanhf(x * logit_scale / cap);
+  else return x * logit_scale;
+}
+
+// Online softmax of one step's logits `s` (masked ones -inf) for the lane's
+// column, then O^T += V^T P^T from the staged V^T tile.
+template <int kDt, int kRowBytes>
+__device__ __forceinline__ void any_softmax_pv(const f32x16& s, float& m_run, float& l_run, f32x16 (&acc)[kDt],
+                                               const lds_char* v, int lane) {
+  float mx = s[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+  mx = max_xor32(mx);
+  const float m_new = fmaxf(m_run, mx);
+  const float ms = m_new == -INFINITY ? 0.f : m_new;  // a column that has seen no key yet keeps P = 0
+  const float corr = fast_exp2(m_run - ms);
+  m_run = m_new;
+  float ls = 0.f;
+  u32x4 pw[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = fast_exp2(s[8 * u + 2 * e] - ms);
+      const float b = fast_exp2(s[8 * u + 2 * e + 1] - ms);
+      pw[u][e] = pack_bf16x2(a, b);
+      ls += a + b;
+    }
+  l_run = l_run * corr + ls;
+#pragma unroll
+  for (int dt = 0; dt < kDt; ++dt) {
+    acc[dt] = acc[dt] * corr;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      acc[dt] = mfma32(as_bf16x8(vt_operand<kRowBytes>(v, 32 * dt, u, lane)), as_bf16x8(pw[u]), acc[dt]);
+  }
+}
+
+// ---- prefill: one workgroup of 4 waves per (q tile of kAnyRows / G tokens,
+// sequence, kv head), grid order of prefill_item (no work list).  Row 32w + n
+// of wave w is token row / G, head row % G of the kv head's group.  All
+// waves share the step's K and V tiles (row-major); the next step's
+// K / V chunks are loaded into registers while this step computes.
+template <int D, bool kSoftCap>
+__global__ void __launch_bounds__(64 * kAnyWaves)
+prefill_any_kernel(PrefillParams p) {
+  using A = AnyDims<D>;
+  constexpr int kThreads = 64 * kAnyWaves;
+  constexpr int kStepChunks = kAnyStep * A::kChunks;
+  constexpr int kPer = (kStepChunks + kThreads - 1) / kThreads;  // chunks of K (and of V) per thread and step
+  __shared__ __attribute__((aligned(16))) char k_tile_g[kAnyStep * A::kRow];
+  __shared__ __attribute__((aligned(16))) char v_tile_g[A::kVTile];
+  __shared__ int red_hi[kAnyWaves];
+  lds_char* k_tile = (lds_char*)k_tile_g;
+  lds_char* v_tile = (lds_char*)v_tile_g;
+
+  PrefillWork w;
+  if (!prefill_resolve(p, blockIdx.x, w)) return;  // uniform across the workgroup
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int n = lane & 31;
+  const int h = lane >> 5;
+  const int G = p.group;
+  const int row = 32 * wave + n;
+  const int rtok = w.qt * p.tile_tokens + row / G;
+  const bool row_ok = row < p.tile_tokens * G && rtok < w.lq_rows;
+  const int ltok = min(rtok, w.lq_rows - 1);  // lanes without a row compute on a real row, never stored
+  const int head = w.kvh * G + row % G;
+  const uint16_t* qrow = p.q + (int64_t)(w.q0 + ltok) * p.q_ts + (int64_t)head * p.q_hs;
+  bf16x8 qb[A::kKs];
+#pragma unroll
+  for (int ks = 0; ks < A::kKs; ++ks) qb[ks] = as_bf16x8(ld16(qrow + 16 * ks + 8 * h));
+  const int qpos = p.positions[w.q0 + ltok];
+
+  // kv index j is visible to some row iff j < lk and j + kv_pos_off <= the
+  // tile's largest position
+  int mx = row_ok ? qpos : INT_MIN, mn = mx;
+  minmax32(mx, mn);
+  if (lane == 0) red_hi[wave] = mx;
+  __syncthreads();
+  int qmax = red_hi[0];
+#pragma unroll
+  for (int i = 1; i < kAnyWaves; ++i) qmax = max(qmax, red_hi[i]);
+  const int64_t kv_hi64 = min((int64_t)w.lk, (int64_t)qmax - w.kv_pos_off + 1);
+  const int kv_hi = kv_hi64 < 0 ? 0 : (int)kv_hi64;
+  const int n_steps = (kv_hi + kAnyStep - 1) / kAnyStep;
+
+  const int32_t* bt_row = p.block_tables + (int64_t)w.b * p.bt_stride;
+  const int64_t head_off = (int64_t)w.kvh * p.head_stride;
+  u32x4 kr[kPer], vr[kPer];
+  auto load = [&](int j0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = tid + kThreads * i;
+      if (c < kStepChunks) {
+        const int t = c / A::kChunks;
+        const int e = c - t * A::kChunks;
+        // tokens past the kv length read the last valid one (masked below)
+        const int j = min(j0 + t, w.lk - 1);
+        const int64_t off = (int64_t)safe_page(bt_row, j / p.page_size, p.num_pages) * p.page_stride +
+                            (int64_t)(j % p.page_size) * p.slot_stride + head_off + 8 * e;
+        kr[i] = ld16(p.k_cache + off);
+        vr[i] = ld16(p.v_cache + off);
+      }
+    }
+  };
+  auto store = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = tid + kThreads * i;
+      if (c < kStepChunks) {
+        const int t = c / A::kChunks;
+        const int e = c - t * A::kChunks;
+        lds_st16(k_tile + t * A::kRow + 16 * e, kr[i]);
+        lds_st16(v_tile + t * A::kRow + 16 * e, vr[i]);
+      }
+    }
+  };
+
+  f32x16 acc[A::kDt];
+#pragma unroll
+  for (int dt = 0; dt < A::kDt; ++dt) acc[dt] = f32x16{};
+  float m_run = -INFINITY, l_run = 0.f;
+  if (n_steps > 0) load(0);
+  for (int st = 0; st < n_steps; ++st) {
+    __syncthreads();  // every wave is done with the previous step's tiles
+    store();
+    __syncthreads();
+    const int j0 = st * kAnyStep;
+    if (st + 1 < n_steps) load(j0 + kAnyStep);
+    f32x16 s = {};
+#pragma unroll
+    for (int ks = 0; ks < A::kKs; ++ks)
+      s = mfma32(as_bf16x8(lds_ld16(k_tile + n * A::kRow + 2 * (16 * ks + 8 * h))), qb[ks], s);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int j = j0 + 8 * (i >> 2) + 4 * h + (i & 3);
+      const bool vis = j < w.lk && (int64_t)j + w.kv_pos_off <= qpos;
+      s[i] = vis ? any_logit<kSoftCap>(s[i], p.logit_scale, p.soft_cap) : -INFINITY;
+    }
+    any_softmax_pv<A::kDt, A::kRow>(s, m_run, l_run, acc, v_tile, lane);
+  }
+  // a row that sees no key (its position precedes the sequence's first kv
+  // position) is written as zeros
+  const float l_tot = sum_xor32(l_run);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (!row_ok) return;
+  uint16_t* orow = p.out + (int64_t)(w.q0 + rtok) * p.o_ts + (int64_t)head * p.o_hs;
+#pragma unroll
+  for (int dt = 0; dt < A::kDt; ++dt)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d0 = 32 * dt + 8 * g4 + 4 * h;
+      if (d0 < D)
+        *reinterpret_cast<u32x2*>(orow + d0) =
+            u32x2{pack_bf16x2(acc[dt][4 * g4] * inv, acc[dt][4 * g4 + 1] * inv),
+                  pack_bf16x2(acc[dt][4 * g4 + 2] * inv, acc[dt][4 * g4 + 3] * inv)};
+    }
+}
+
+// Rows of tokens [4 zb, 4 zb + 4) that no prefill item writes (outside every
+// sequence or at offset >= max_seqlen_q): zeros, one wave per token.
+__global__ void __launch_bounds__(256)
+prefill_any_zero_kernel(PrefillParams p, int head_dim) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= p.num_tokens) return;
+  bool covered = false;
+  if (p.batch > 0 && t >= p.cu_q[0] && t < p.cu_q[p.batch]) {
+    int lo = 0, hi = p.batch;  // invariant: cu_q[lo] <= t < cu_q[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (p.cu_q[mid] <= t) lo = mid;
+      else hi = mid;
+    }
+    covered = t - p.cu_q[lo] < p.max_seqlen_q;
+  }
+  if (covered) return;
+  const int per_head = head_dim / 8;
+  for (int c = lane; c < p.num_heads * per_head; c += 64) {
+    const int hh = c / per_head;
+    st16(p.out + t * p.o_ts + (int64_t)hh * p.o_hs + 8 * (c - hh * per_head), u32x4{0u, 0u, 0u, 0u});
+  }
+}
+
+// ---- decode: one wave per (sequence, chunk, kv head, block of 32 q heads),
+// grid order item = ((b * n_chunks + chunk) * Hkv + kv head) * hblocks +
+// block.  K and V rows are read with whole-row 16-byte loads (8 lanes per
+// 128 bytes) and staged row-major in the wave's K and V tiles.
+// The chunk's partial (O unnormalised, the log2 max and the sum per head)
+// goes to the workspace; decode_any_merge_kernel combines the chunks of
+// every sequence.
+template <int D, bool kSoftCap>
+__global__ void __launch_bounds__(64)
+decode_any_kernel(DecodeParams p) {
+  using A = AnyDims<D>;
+  constexpr int kPer = kAnyStep * A::kChunks / 64;  // chunks of K (and of V) per lane and step
+  // the next step's rows are loaded while this step computes, up to the head
+  // size whose registers still allow it without spills
+  constexpr bool kPrefetch = D <= 224;
+  __shared__ __attribute__((aligned(16))) char k_tile_g[kAnyStep * A::kRow];
+  __shared__ __attribute__((aligned(16))) char v_tile_g[A::kVTile];
+  lds_char* k_tile = (lds_char*)k_tile_g;
+  lds_char* v_tile = (lds_char*)v_tile_g;
+  const int lane = threadIdx.x;
+  const int n = lane & 31;
+  const int h = lane >> 5;
+  const int hkv = p.num_kv_heads;
+  const int vheads = hkv * p.hblocks;
+  const int item = blockIdx.x;
+  const int vh = item % vheads;
+  const int rest = item / vheads;
+  const int kvh = vh / p.hblocks;
+  const int qc0 = 32 * (vh - kvh * p.hblocks);  // first q head (within the group) of this item
+  const int g_end = min(p.group, qc0 + 32);
+  const int chunk = rest % p.n_chunks;
+  const int b = rest / p.n_chunks;
+  if (!decode_has_row(p, b)) return;
+  // lengths past the block table's span are clamped to it
+  const int len = min(p.lengths[b], p.pages_per_seq * p.page_size);
+  const int t0 = chunk * p.chunk;
+  if (t0 >= len) return;  // the merge writes what this chunk would have held
+  const int t1 = min(t0 + p.chunk, len);
+  const bool live = qc0 + n < g_end;
+  const uint16_t* qrow =
+      p.q + decode_row(p, b) * p.q_bs + (int64_t)(kvh * p.group + qc0 + (live ? n : 0)) * p.q_hs;
+  bf16x8 qb[A::kKs];
+#pragma unroll
+  for (int ks = 0; ks < A::kKs; ++ks) {
+    const u32x4 v = ld16(qrow + 16 * ks + 8 * h);
+    qb[ks] = as_bf16x8(live ? v : u32x4{0u, 0u, 0u, 0u});
+  }
+  const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
+  const int64_t head_off = (int64_t)kvh * p.head_stride;
+  u32x4 kr[kPer], vr[kPer];
+  auto load = [&](int j0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = lane + 64 * i;
+      const int t = c / A::kChunks;
+      const int e = c - t * A::kChunks;
+      // tokens past the chunk read its last token (masked below)
+      const int j = min(j0 + t, t1 - 1);
+      const int64_t off = (int64_t)safe_page(bt_row, j / p.page_size, p.num_pages) * p.page_stride +
+                          (int64_t)(j % p.page_size) * p.slot_stride + head_off + 8 * e;
+      kr[i] = ld16(p.k_cache + off);
+      vr[i] = ld16(p.v_cache + off);
+    }
+  };
+
+  f32x16 acc[A::kDt];
+#pragma unroll
+  for (int dt = 0; dt < A::kDt; ++dt) acc[dt] = f32x16{};
+  float m_run = -INFINITY, l_run = 0.f;
+  if constexpr (kPrefetch) load(t0);
+  for (int j0 = t0; j0 < t1; j0 += kAnyStep) {
+    if constexpr (!kPrefetch) load(j0);
+    __syncthreads();  // the previous step's tile reads are done
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = lane + 64 * i;
+      const int t = c / A::kChunks;
+      const int e = c - t * A::kChunks;
+      lds_st16(k_tile + t * A::kRow + 16 * e, kr[i]);
+      lds_st16(v_tile + t * A::kRow + 16 * e, vr[i]);
+    }
+    __syncthreads();
+    if constexpr (kPrefetch) {
+      if (j0 + kAnyStep < t1) load(j0 + kAnyStep);
+    }
+    f32x16 s = {};
+#pragma unroll
+    for (int ks = 0; ks < A::kKs; ++ks)
+      s = mfma32(as_bf16x8(lds_ld16(k_tile + n * A::kRow + 2 * (16 * ks + 8 * h))), qb[ks], s);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int j = j0 + 8 * (i >> 2) + 4 * h + (i & 3);
+      s[i] = j < t1 ? any_logit<kSoftCap>(s[i], p.logit_scale, p.soft_cap) : -INFINITY;
+    }
+    any_softmax_pv<A::kDt, A::kRow>(s, m_run, l_run, acc, v_tile, lane);
+  }
+  const float l_tot = sum_xor32(l_run);
+  if (!live) return;
+  const int64_t part = (((int64_t)b * hkv + kvh) * p.n_chunks + chunk) * p.group + qc0 + n;
+  float* dst = p.ws_o + part * D;
+#pragma unroll
+  for (int dt = 0; dt < A::kDt; ++dt)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d0 = 32 * dt + 8 * g4 + 4 * h;
+      if (d0 < D)
+        *reinterpret_cast<f32x4*>(dst + d0) =
+            f32x4{acc[dt][4 * g4], acc[dt][4 * g4 + 1], acc[dt][4 * g4 + 2], acc[dt][4 * g4 + 3]};
+    }
+  if (h == 0) {
+    p.ws_ml[2 * part] = m_run;
+    p.ws_ml[2 * part + 1] = l_tot;
+  }
+}
+
+// One wave per (sequence, q head): out = sum_c o_c 2^(m_c - M) / sum_c l_c
+// 2^(m_c - M) over the sequence's chunks; length 0 gives zeros.  Lane l
+// finishes the d pairs 2l and 2l + 128.
+__global__ void __launch_bounds__(256)
+decode_any_merge_kernel(DecodeParams p, int head_dim) {
+  const int lane = threadIdx.x & 63;
+  const int64_t pair = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pair >= (int64_t)p.batch * p.num_heads) return;
+  const int b = (int)(pair / p.num_heads);
+  const int hd = (int)(pair - (int64_t)b * p.num_heads);
+  if (!decode_has_row(p, b)) return;
+  const int kvh = hd / p.group;
+  const int qi = hd - kvh * p.group;
+  const int len = min(p.lengths[b], p.pages_per_seq * p.page_size);
+  const int nc = len > 0 ? min((len + p.chunk - 1) / p.chunk, p.n_chunks) : 0;
+  const int64_t base = ((int64_t)b * p.num_kv_heads + kvh) * p.n_chunks;
+  float mmax = -INFINITY;
+  for (int c = 0; c < nc; ++c) mmax = fmaxf(mmax, p.ws_ml[2 * ((base + c) * p.group + qi)]);
+  float o[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+  float lsum = 0.f;
+  for (int c = 0; c < nc; ++c) {
+    const int64_t part = (base + c) * p.group + qi;
+    const float wgt = fast_exp2(p.ws_ml[2 * part] - mmax);
+    lsum += p.ws_ml[2 * part + 1] * wgt;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int d = 2 * lane + 128 * k;
+      if (d < head_dim) {
+        const float2 v = *reinterpret_cast<const float2*>(p.ws_o + part * head_dim + d);
+        o[k][0] += v.x * wgt;
+        o[k][1] += v.y * wgt;
+      }
+    }
+  }
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  uint16_t* orow = p.out + decode_row(p, b) * p.out_bs + (int64_t)hd * p.out_hs;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int d = 2 * lane + 128 * k;
+    if (d < head_dim) *reinterpret_cast<uint32_t*>(orow + d) = pack_bf16x2(o[k][0] * inv, o[k][1] * inv);
+  }
+}
+
+#define PA_ANY_DIMS(X) \
+  X(16) X(32) X(48) X(64) X(80) X(96) X(112) X(144) X(160) X(176) X(192) X(208) X(224) X(240) X(256)
+
+}  // namespace
+
+bool any_head_dim(int head_dim) {
+  switch (head_dim) {
+#define PA_ANY_CASE(d) case d:
+    PA_ANY_DIMS(PA_ANY_CASE)
+#undef PA_ANY_CASE
+    return true;
+    default:
+      return false;
+  }
+}
+
+int prefill_any_launch(const char* name, const PrefillParams& prm, int head_dim, hipStream_t s) {
+  PrefillParams p = prm;
+  if (p.group > kAnyRows)
+    return fail(PA_ERR_UNSUPPORTED, "%s: %d q heads per kv head not supported at head_dim %d (max %d)", name,
+                p.group, head_dim, kAnyRows);
+  p.plan = nullptr;
+  p.pool = nullptr;
+  p.tile_tokens = kAnyRows / p.group;
+  p.n_qtiles = (p.max_seqlen_q + p.tile_tokens - 1) / p.tile_tokens;
+  if (p.num_tokens > 0) {
+    prefill_any_zero_kernel<<<dim3((unsigned)((p.num_tokens + 3) / 4)), dim3(256), 0, s>>>(p, head_dim);
+    const int rc = launch_status(name);
+    if (rc) return rc;
+  }
+  if (p.batch == 0 || p.max_seqlen_q == 0) return PA_OK;
+  const int64_t items = (int64_t)p.n_qtiles * p.batch * p.num_kv_heads;
+  if (items > 0x7fffffff)
+    return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)items);
+  const dim3 g((unsigned)items), blk(64 * kAnyWaves);
+  const bool cap = p.soft_cap > 0.f;
+  switch (head_dim) {
+#define PA_ANY_LAUNCH(d)                                             \
+  case d:                                                            \
+    if (cap) prefill_any_kernel<d, true><<<g, blk, 0, s>>>(p);       \
+    else prefill_any_kernel<d, false><<<g, blk, 0, s>>>(p);          \
+    break;
+    PA_ANY_DIMS(PA_ANY_LAUNCH)
+#undef PA_ANY_LAUNCH
+    default:
+      return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported", name, head_dim);
+  }
+  return launch_status(name);
+}
+
+int decode_any_launch(const char* name, const DecodeParams& prm, int head_dim, hipStream_t s) {
+  DecodeParams p = prm;
+  p.plan = nullptr;
+  p.hblocks = (p.group + 31) / 32;
+  const int64_t items = (int64_t)p.batch * p.n_chunks * p.num_kv_heads * p.hblocks;
+  if (items > 0x7fffffff)
+    return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)items);
+  if (items > 0) {
+    const dim3 g((unsigned)items), blk(64);
+    const bool cap = p.soft_cap > 0.f;
+    switch (head_dim) {
+#define PA_ANY_LAUNCH(d)                                           \
+  case d:                                                          \
+    if (cap) decode_any_kernel<d, true><<<g, blk, 0, s>>>(p);      \
+    else decode_any_kernel<d, false><<<g, blk, 0, s>>>(p);         \
+    break;
+      PA_ANY_DIMS(PA_ANY_LAUNCH)
+#undef PA_ANY_LAUNCH
+      default:
+        return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported", name, head_dim);
+    }
+    const int rc = launch_status(name);
+    if (rc) return rc;
+  }
+  const int64_t pairs = (int64_t)p.batch * p.num_heads;
+  if (pairs > 0) {
+    decode_any_merge_kernel<<<dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s>>>(p, head_dim);
+    return launch_status(name);
+  }
+  return PA_OK;
+}
+
+}  // namespace pa

@@ -3,6 +3,7 @@
 // prefill_body in prefill_impl.h.
 #include <algorithm>
 
+#include "any_head.h"
 #include "prefill_impl.h"
 
 namespace pa {
@@ -342,8 +343,14 @@ static int prefill_launch(const char* name, const uint16_t* q, int64_t q_tok_str
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "%s: Number of Q heads must be divisible by number of KV heads. Got %d and %d.", name,
                 num_heads, num_kv_heads);
-  if (head_dim != kPHeadDim)
-    return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported (only %d)", name, head_dim, kPHeadDim);
+#ifdef PA_PREFILL_PHASES
+  const bool any_d = false;  // the phase-timestamp build instruments the head_dim 128 kernel only
+#else
+  const bool any_d = head_dim != kPHeadDim && any_head_dim(head_dim);
+#endif
+  if (head_dim != kPHeadDim && !any_d)
+    return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported (128, or a multiple of 16 from 16 to 256)",
+                name, head_dim);
   const int group = num_heads / num_kv_heads;
   if (group > kRows)
     return fail(PA_ERR_UNSUPPORTED, "%s: %d q heads per kv head not supported (max %d)", name, group, kRows);
@@ -354,7 +361,7 @@ static int prefill_launch(const char* name, const uint16_t* q, int64_t q_tok_str
   if ((align_bits & 15u) || (q_tok_stride | q_head_stride | page_stride | slot_stride | head_stride |
                              out_tok_stride | out_head_stride) % 8)
     return fail(PA_ERR_UNSUPPORTED, "%s: operands must be 16-byte aligned with strides multiple of 8", name);
-  if (page_size % kTileN == 0 && !prefill_offsets_fit(slot_stride))
+  if (!any_d && page_size % kTileN == 0 && !prefill_offsets_fit(slot_stride))
     return fail(PA_ERR_UNSUPPORTED, "%s: slot stride %lld too large for 32-bit tile offsets (max %lld)", name,
                 (long long)slot_stride, (long long)((0x7fffffffLL - (kPHeadDim - 1)) / (kTileN - 1)));
   if (workspace) {
@@ -396,6 +403,9 @@ static int prefill_launch(const char* name, const uint16_t* q, int64_t q_tok_str
   prm.out = out;
   prm.o_ts = out_tok_stride;
   prm.o_hs = out_head_stride;
+#ifndef PA_PREFILL_PHASES
+  if (any_d) return prefill_any_launch(name, prm, head_dim, s);
+#endif
   const int64_t items = (int64_t)prm.n_qtiles * batch * num_kv_heads;
   if (items > 0x7fffffff)
     return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)items);
