@@ -26,10 +26,10 @@
  * are skipped by the KV store.
  *
  * Supported shapes: num_heads % num_kv_heads == 0, and
- *   - head_dim 128 in every entry (the tuned kernels); pa_prefill, pa_decode
- *     and pa_decode_noalloc also take any multiple of 16 from 16 to 256
- *     (generic kernels, same arithmetic, lower throughput); float8 pages and
- *     pa_mixed take 128 only;
+ *   - head_dim 128 in every entry (the tuned kernels); pa_prefill, pa_decode,
+ *     pa_decode_noalloc and pa_mixed also take any multiple of 16 from 16 to
+ *     256 (generic kernels, same arithmetic, lower throughput); float8 pages
+ *     take 128 only;
  *   - q heads per kv head: any number for decode, up to 256 for prefill and
  *     pa_mixed (up to 128 for prefill at head sizes other than 128).
  */

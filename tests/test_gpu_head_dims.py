@@ -1,13 +1,13 @@
 """Head sizes other than 128 on gfx950 against the oracle (max-abs <= 2e-2).
 
-pa_prefill and pa_decode take any head size that is a multiple of 16 from
+pa_prefill, pa_decode and pa_mixed take any head size that is a multiple of 16 from
 16 to 256 (the reference only asks q and the pages to agree,
 prefill_paged_attention.py:199-203, decode_paged_attention.py:356-360);
 sizes other than 128 run the kernels of csrc/any_head.hip.  The cases cover
 the head sizes of common model families (64, 80, 96, 256) and the edges
 (16, 48, 240), head groups from 1 to 40, page sizes that do and do not
 divide 32-token steps, the soft cap, cached prefixes, rows that see no key,
-decode chunks, length 0 and the no-alloc decode entry.
+decode chunks, length 0, the mixed launch and the no-alloc decode entry.
 """
 from __future__ import annotations
 
@@ -18,6 +18,8 @@ import vllm_jax_amd.workloads as wl
 from conftest import u16
 from oracle import paged_attention_oracle as ora
 from test_gpu_decode import _run_and_check
+from test_gpu_mixed import _case as _mixed_case
+from test_gpu_mixed import _run as _mixed_run
 from test_gpu_prefill import _prefill
 
 pytestmark = pytest.mark.gpu
@@ -137,3 +139,30 @@ def test_decode_head_dim_noalloc_matches_pa_decode(pkg, dev):
         err = float(np.abs(ora.bf16_to_f32(u16(got)) - ora.bf16_to_f32(want)).max())
         print(f"no-alloc decode at head_dim 64: max-abs err {err:.3e}", flush=True)
         assert err <= TOL
+
+
+@pytest.mark.parametrize("dec,pre_q,pre_p,h,hkv,bs,d,cap", [
+    ([1000, 2000, 513, 0], [130, 257], [0, 100], 16, 8, 256, 64, None),   # d = 64, an empty decode context
+    ([5, 4097, 9000], [64, 300], [0, 0], 32, 8, 64, 96, 6.0),             # several chunks, soft cap
+    ([700, 30], [100, 5], [0, 40], 40, 2, 48, 256, None),                 # G = 20, 48-token pages
+    ([], [17, 128, 300], [0, 0, 0], 16, 8, 16, 80, None),                 # no decode sequence
+    ([10, 600, 4096], [], [], 16, 4, 80, 112, None),                      # no prefill sequence, 80-token pages
+])
+def test_mixed_head_dims(pkg, dev, dec, pre_q, pre_p, h, hkv, bs, d, cap):
+    rng = np.random.default_rng(len(dec) * 100 + h + d)
+    q, kc, vc, bt, cu, kv, pos = _mixed_case(rng, dec, pre_q, pre_p, h, hkv, bs, pad_rows=2, d=d)
+    nd = len(dec)
+    root = float(ora.round_bf16(np.float32(np.sqrt(d))).reshape(-1)[0])
+    got = _mixed_run(pkg, dev, q, kc, vc, bt, cu, kv, pos, nd, max(pre_q) if pre_q else 0, soft_cap=cap,
+                     decode_scale=1.0 / root)
+    want = ora.mixed_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, kv, pos, nd,
+                               soft_cap=cap)
+    err = np.abs(ora.bf16_to_f32(got) - ora.bf16_to_f32(want)).max()
+    print(f"mixed at head_dim {d}: max-abs err {err:.3e}", flush=True)
+    assert err <= TOL
+    zero = np.ones(q.shape[0], bool)
+    zero[cu[:nd]] = False
+    for b in range(nd, len(kv)):
+        zero[cu[b]:cu[b + 1]] = False
+    zero[cu[:nd][kv[:nd] == 0]] = True      # empty decode context
+    assert not got[zero].any()

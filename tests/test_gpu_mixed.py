@@ -22,7 +22,7 @@ def _bf16(rng, shape, scale=0.5):
     return ora.f32_to_bf16(rng.standard_normal(shape).astype(np.float32) * scale)
 
 
-def _case(rng, dec_lens, pre_q, pre_prefix, h, hkv, bs, pad_rows=0, empty_decode_row=None):
+def _case(rng, dec_lens, pre_q, pre_prefix, h, hkv, bs, pad_rows=0, empty_decode_row=None, d=128):
     kv = list(dec_lens) + [p + n for p, n in zip(pre_prefix, pre_q)]
     nb = int(sum(-(-int(n) // bs) for n in kv)) + 3
     width = max(1, max(-(-int(n) // bs) for n in kv))
@@ -41,17 +41,17 @@ def _case(rng, dec_lens, pre_q, pre_prefix, h, hkv, bs, pad_rows=0, empty_decode
     pos = np.concatenate([[max(n - 1, 0)] * q for n, q in zip(dec_lens, q_lens[:len(dec_lens)])] +
                          [np.arange(p, p + n) for p, n in zip(pre_prefix, pre_q)]).astype(np.int32)
     pos = np.concatenate([pos, np.zeros(pad_rows, np.int32)])
-    q = _bf16(rng, (int(cu[-1]) + pad_rows, h, 128))
-    kc, vc = _bf16(rng, (nb, bs, hkv, 128)), _bf16(rng, (nb, bs, hkv, 128))
+    q = _bf16(rng, (int(cu[-1]) + pad_rows, h, d))
+    kc, vc = _bf16(rng, (nb, bs, hkv, d)), _bf16(rng, (nb, bs, hkv, d))
     return q, kc, vc, bt, cu, np.asarray(kv, np.int32), pos
 
 
-def _run(pkg, dev, q, kc, vc, bt, cu, kv, pos, nd, max_q, soft_cap=None):
+def _run(pkg, dev, q, kc, vc, bt, cu, kv, pos, nd, max_q, soft_cap=None, decode_scale=DECODE_SCALE):
     import torch
     i32 = lambda a: torch.as_tensor(np.ascontiguousarray(a), dtype=torch.int32, device=dev)
     kcd, vcd = from_u16(kc, dev), from_u16(vc, dev)
     out = pkg.mixed_paged_attention(from_u16(q, dev), kcd.permute(2, 0, 1, 3), vcd.permute(2, 0, 1, 3), i32(bt),
-                                    i32(cu), i32(kv), i32(pos), nd, max_seqlen_q=max_q, decode_scale=DECODE_SCALE,
+                                    i32(cu), i32(kv), i32(pos), nd, max_seqlen_q=max_q, decode_scale=decode_scale,
                                     attn_logits_soft_cap=soft_cap)
     torch.cuda.synchronize()
     return u16(out)

@@ -27,6 +27,7 @@
 // costliest first, then dealt over the XCDs; the zero pass follows them.
 #include <algorithm>
 
+#include "any_head.h"
 #include "decode_impl.h"
 #include "prefill_impl.h"
 
@@ -292,6 +293,13 @@ extern "C" size_t pa_mixed_workspace_size(int32_t batch, int32_t num_decodes, in
       pages_per_seq < 0 || page_size <= 0)
     return 0;
   const int chunks = pages_per_seq > 0 ? mixed_decode_chunks(pages_per_seq, page_size) : 0;
+  if (head_dim != kPHeadDim) {
+    // the generic kernels: decode partials of every chunk (no work list),
+    // after 256 bytes that keep the size non-zero
+    if (!any_head_dim(head_dim)) return 0;
+    return 256 + ((size_t)num_decodes * num_heads * chunks * ((size_t)head_dim + 2) * sizeof(float) + 255) / 256 *
+                     256;
+  }
   const int64_t pairs = mixed_pairs(batch, num_decodes, max_seqlen_q, num_heads, num_kv_heads, pages_per_seq,
                                     page_size);
   return mixed_partials_bytes(num_decodes, num_heads, head_dim, chunks) +
@@ -320,8 +328,10 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "pa_mixed: Number of Q heads must be divisible by number of KV heads. Got %d and %d.", num_heads,
                 num_kv_heads);
-  if (head_dim != kPHeadDim)
-    return fail(PA_ERR_UNSUPPORTED, "pa_mixed: head_dim %d not supported (only %d)", head_dim, kPHeadDim);
+  const bool any_d = head_dim != kPHeadDim && any_head_dim(head_dim);
+  if (head_dim != kPHeadDim && !any_d)
+    return fail(PA_ERR_UNSUPPORTED, "pa_mixed: head_dim %d not supported (128, or a multiple of 16 from 16 to 256)",
+                head_dim);
   const int group = num_heads / num_kv_heads;
   if (group > kRows)
     return fail(PA_ERR_UNSUPPORTED, "pa_mixed: %d q heads per kv head not supported (max %d)", group, kRows);
@@ -335,7 +345,7 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
     return fail(PA_ERR_UNSUPPORTED, "pa_mixed: operands must be 16-byte aligned with strides multiple of 8");
   if ((int64_t)pages_per_seq * page_size > 0x7fffffffLL)
     return fail(PA_ERR_UNSUPPORTED, "pa_mixed: block table spans more than 2^31 tokens");
-  if (page_size % kTileN == 0 && !prefill_offsets_fit(slot_stride))
+  if (!any_d && page_size % kTileN == 0 && !prefill_offsets_fit(slot_stride))
     return fail(PA_ERR_UNSUPPORTED, "pa_mixed: slot stride %lld too large for 32-bit tile offsets (max %lld)",
                 (long long)slot_stride, (long long)((0x7fffffffLL - (kPHeadDim - 1)) / (kTileN - 1)));
   const int n_chunks = pages_per_seq > 0 ? mixed_decode_chunks(pages_per_seq, page_size) : 0;
@@ -424,6 +434,18 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
   m.out = out;
   m.o_ts = out_tok_stride;
   m.o_hs = out_head_stride;
+  if (any_d) {
+    // head sizes other than 128: the generic prefill (with its zero pass:
+    // every row outside the prefill sequences or past max_seqlen_q, so also
+    // the decode rows, which the decode merge then writes) and the generic
+    // decode, which leaves partials for every chunk
+    hipStream_t gs = (hipStream_t)stream;
+    dp.ws_o = reinterpret_cast<float*>(workspace);
+    dp.ws_ml = dp.ws_o + (size_t)num_decodes * num_heads * n_chunks * head_dim;
+    const int rc = prefill_any_launch("pa_mixed", pp, head_dim, gs);
+    if (rc || num_decodes == 0) return rc;
+    return decode_any_launch("pa_mixed", dp, head_dim, gs);
+  }
 
   // ---- regions.  Prefill level l (q tile n_qtiles-1-l) reaches kv index
   // (n_qtiles-l)*tile_tokens; it goes before the decode items while it costs
