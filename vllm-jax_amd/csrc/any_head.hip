@@ -4,7 +4,9 @@
 // (prefill_paged_attention.py:199-203, decode_paged_attention.py:356-360);
 // the tuned kernels of prefill.hip / decode.hip are built for 128, and these
 // cover the rest with the same arithmetic: S in f32 on the matrix core from
-// bf16 q and K, exp2 online softmax, P rounded to bf16 for PV, f32 O.
+// bf16 q (scaled by scale * log2 e and rounded, without the soft cap) and K,
+// exp2 online softmax with a lazily moved reference max, P rounded to bf16
+// for PV, f32 O.
 //
 // Both kernels use v_mfma_f32_32x32x16_bf16 (lane layouts in pa_common.h)
 // in the same two products per 32-token kv step:
@@ -74,27 +76,70 @@ __device__ __forceinline__ void lds_st16(lds_char* a, const u32x4& v) {
   *reinterpret_cast<u32x4 __attribute__((address_space(3)))*>(a) = v;
 }
 
-// Logit in log2 units: x * scale * log2 e, or with the soft cap
+// Logit in log2 units.  Without the soft cap q arrives scaled by
+// scale * log2 e (any_q_operand), so S already is; with it,
 // cap * log2 e * tanh(x * scale / cap) (scale = logit_scale of the params).
 template <bool kSoftCap>
 __device__ __forceinline__ float any_logit(float x, float logit_scale, float cap) {
   if constexpr (kSoftCap) return cap * kLog2e * tanhf(x * logit_scale / cap);
+  else return x;
+}
+
+// A q operand (8 bf16), scaled by scale * log2 e and rounded to bf16 when
+// the soft cap is off, as the tuned kernels do.
+template <bool kSoftCap>
+__device__ __forceinline__ bf16x8 any_q_operand(const u32x4& raw, float logit_scale) {
+  if constexpr (kSoftCap) {
+    return as_bf16x8(raw);
+  } else {
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = pack_bf16x2(bf16_lo(raw[e]) * logit_scale, bf16_hi(raw[e]) * logit_scale);
+    return as_bf16x8(o);
+  }
+}
+
+// Logit in log2 units from an unscaled q: x * scale * log2 e, or the soft
+// cap as above (decode, whose q is not scaled in bf16 first).
+template <bool kSoftCap>
+__device__ __forceinline__ float any_logit_f32(float x, float logit_scale, float cap) {
+  if constexpr (kSoftCap) return cap * kLog2e * tanhf(x * logit_scale / cap);
   else return x * logit_scale;
 }
 
+constexpr float kAnySlack = 8.f;  // lazy rescale: the reference max moves when a row max exceeds it by more
+
 // Online softmax of one step's logits `s` (masked ones -inf) for the lane's
-// column, then O^T += V^T P^T from the staged V^T tile.
-template <int kDt, int kRowBytes>
+// column, then O^T += V^T P^T from the staged V tile.
+// kLazy: move the reference only past the slack (prefill, where the VALU
+// work of the softmax wave bounds the step); otherwise every step (decode,
+// bound by memory, where the branch costs registers at the large sizes).
+template <int kDt, int kRowBytes, bool kLazy>
 __device__ __forceinline__ void any_softmax_pv(const f32x16& s, float& m_run, float& l_run, f32x16 (&acc)[kDt],
                                                const lds_char* v, int lane) {
   float mx = s[0];
 #pragma unroll
   for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
   mx = max_xor32(mx);
-  const float m_new = fmaxf(m_run, mx);
-  const float ms = m_new == -INFINITY ? 0.f : m_new;  // a column that has seen no key yet keeps P = 0
-  const float corr = fast_exp2(m_run - ms);
-  m_run = m_new;
+  // m_run is the column's reference max: it moves (and O and l are rescaled)
+  // only when some column of the wave exceeds its own by more than the
+  // slack, so P stays below 2^kAnySlack
+  float corr = 1.f;
+  if constexpr (kLazy) {
+    if (__any(mx > m_run + kAnySlack)) {  // uniform over the wave
+      const float m_new = fmaxf(m_run, mx);
+      corr = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
+      m_run = m_new;
+      l_run *= corr;
+#pragma unroll
+      for (int dt = 0; dt < kDt; ++dt) acc[dt] = acc[dt] * corr;
+    }
+  } else {
+    const float m_new = fmaxf(m_run, mx);
+    corr = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
+    m_run = m_new;
+  }
+  const float ms = m_run == -INFINITY ? 0.f : m_run;  // a column that has seen no key yet keeps P = 0
   float ls = 0.f;
   u32x4 pw[2];
 #pragma unroll
@@ -106,10 +151,10 @@ __device__ __forceinline__ void any_softmax_pv(const f32x16& s, float& m_run, fl
       pw[u][e] = pack_bf16x2(a, b);
       ls += a + b;
     }
-  l_run = l_run * corr + ls;
+  l_run = kLazy ? l_run + ls : l_run * corr + ls;
 #pragma unroll
   for (int dt = 0; dt < kDt; ++dt) {
-    acc[dt] = acc[dt] * corr;
+    if constexpr (!kLazy) acc[dt] = acc[dt] * corr;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
       acc[dt] = mfma32(as_bf16x8(vt_operand<kRowBytes>(v, 32 * dt, u, lane)), as_bf16x8(pw[u]), acc[dt]);
@@ -130,7 +175,7 @@ prefill_any_kernel(PrefillParams p) {
   constexpr int kPer = (kStepChunks + kThreads - 1) / kThreads;  // chunks of K (and of V) per thread and step
   __shared__ __attribute__((aligned(16))) char k_tile_g[kAnyStep * A::kRow];
   __shared__ __attribute__((aligned(16))) char v_tile_g[A::kVTile];
-  __shared__ int red_hi[kAnyWaves];
+  __shared__ int red_hi[kAnyWaves], red_lo[kAnyWaves];
   lds_char* k_tile = (lds_char*)k_tile_g;
   lds_char* v_tile = (lds_char*)v_tile_g;
 
@@ -150,18 +195,24 @@ prefill_any_kernel(PrefillParams p) {
   const uint16_t* qrow = p.q + (int64_t)(w.q0 + ltok) * p.q_ts + (int64_t)head * p.q_hs;
   bf16x8 qb[A::kKs];
 #pragma unroll
-  for (int ks = 0; ks < A::kKs; ++ks) qb[ks] = as_bf16x8(ld16(qrow + 16 * ks + 8 * h));
+  for (int ks = 0; ks < A::kKs; ++ks) qb[ks] = any_q_operand<kSoftCap>(ld16(qrow + 16 * ks + 8 * h), p.logit_scale);
   const int qpos = p.positions[w.q0 + ltok];
 
   // kv index j is visible to some row iff j < lk and j + kv_pos_off <= the
   // tile's largest position
-  int mx = row_ok ? qpos : INT_MIN, mn = mx;
+  int mx = row_ok ? qpos : INT_MIN, mn = row_ok ? qpos : INT_MAX;
   minmax32(mx, mn);
-  if (lane == 0) red_hi[wave] = mx;
+  if (lane == 0) {
+    red_hi[wave] = mx;
+    red_lo[wave] = mn;
+  }
   __syncthreads();
-  int qmax = red_hi[0];
+  int qmax = red_hi[0], qmin = red_lo[0];
 #pragma unroll
-  for (int i = 1; i < kAnyWaves; ++i) qmax = max(qmax, red_hi[i]);
+  for (int i = 1; i < kAnyWaves; ++i) {
+    qmax = max(qmax, red_hi[i]);
+    qmin = min(qmin, red_lo[i]);
+  }
   const int64_t kv_hi64 = min((int64_t)w.lk, (int64_t)qmax - w.kv_pos_off + 1);
   const int kv_hi = kv_hi64 < 0 ? 0 : (int)kv_hi64;
   const int n_steps = (kv_hi + kAnyStep - 1) / kAnyStep;
@@ -214,12 +265,16 @@ prefill_any_kernel(PrefillParams p) {
     for (int ks = 0; ks < A::kKs; ++ks)
       s = mfma32(as_bf16x8(lds_ld16(k_tile + n * A::kRow + 2 * (16 * ks + 8 * h))), qb[ks], s);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int j = j0 + 8 * (i >> 2) + 4 * h + (i & 3);
-      const bool vis = j < w.lk && (int64_t)j + w.kv_pos_off <= qpos;
-      s[i] = vis ? any_logit<kSoftCap>(s[i], p.logit_scale, p.soft_cap) : -INFINITY;
+    for (int i = 0; i < 16; ++i) s[i] = any_logit<kSoftCap>(s[i], p.logit_scale, p.soft_cap);
+    // a step below the length and below every row's causal limit needs no mask
+    if (j0 + kAnyStep > w.lk || (int64_t)j0 + kAnyStep - 1 + w.kv_pos_off > qmin) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int j = j0 + 8 * (i >> 2) + 4 * h + (i & 3);
+        s[i] = j < w.lk && (int64_t)j + w.kv_pos_off <= qpos ? s[i] : -INFINITY;
+      }
     }
-    any_softmax_pv<A::kDt, A::kRow>(s, m_run, l_run, acc, v_tile, lane);
+    any_softmax_pv<A::kDt, A::kRow, true>(s, m_run, l_run, acc, v_tile, lane);
   }
   // a row that sees no key (its position precedes the sequence's first kv
   // position) is written as zeros
@@ -278,7 +333,7 @@ decode_any_kernel(DecodeParams p) {
   constexpr int kPer = kAnyStep * A::kChunks / 64;  // chunks of K (and of V) per lane and step
   // the next step's rows are loaded while this step computes, up to the head
   // size whose registers still allow it without spills
-  constexpr bool kPrefetch = D <= 224;
+  constexpr bool kPrefetch = kSoftCap ? D <= 192 : D <= 224;
   __shared__ __attribute__((aligned(16))) char k_tile_g[kAnyStep * A::kRow];
   __shared__ __attribute__((aligned(16))) char v_tile_g[A::kVTile];
   lds_char* k_tile = (lds_char*)k_tile_g;
@@ -309,7 +364,7 @@ decode_any_kernel(DecodeParams p) {
 #pragma unroll
   for (int ks = 0; ks < A::kKs; ++ks) {
     const u32x4 v = ld16(qrow + 16 * ks + 8 * h);
-    qb[ks] = as_bf16x8(live ? v : u32x4{0u, 0u, 0u, 0u});
+    qb[ks] = as_bf16x8(live ? v : u32x4{0u, 0u, 0u, 0u});  // unscaled: the logits are scaled in f32
   }
   const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
   const int64_t head_off = (int64_t)kvh * p.head_stride;
@@ -356,9 +411,9 @@ decode_any_kernel(DecodeParams p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int j = j0 + 8 * (i >> 2) + 4 * h + (i & 3);
-      s[i] = j < t1 ? any_logit<kSoftCap>(s[i], p.logit_scale, p.soft_cap) : -INFINITY;
+      s[i] = j < t1 ? any_logit_f32<kSoftCap>(s[i], p.logit_scale, p.soft_cap) : -INFINITY;
     }
-    any_softmax_pv<A::kDt, A::kRow>(s, m_run, l_run, acc, v_tile, lane);
+    any_softmax_pv<A::kDt, A::kRow, false>(s, m_run, l_run, acc, v_tile, lane);
   }
   const float l_tot = sum_xor32(l_run);
   if (!live) return;
