@@ -6,6 +6,8 @@ to the 64-token prefill tile and the 16-token decode step), the batch, q
 lengths including 0 and 1, cached prefixes and the soft cap.  The prefill
 cases run through the kernel entry, hence with the work list.  Bar as in the
 per-entry tests: max-abs 2e-2 on bf16 outputs, zero rows exactly zero.
+A last sweep draws head sizes other than 128 (multiples of 16 up to 256) for
+the generic kernels, taking prefill, decode and the mixed launch in turn.
 PA_SWEEP_SEEDS=n runs n seeds per sweep instead of the default counts.
 """
 from __future__ import annotations
@@ -193,3 +195,56 @@ def test_fp8_sweep(pkg, dev, seed):
     err_p = float(np.abs(ora.bf16_to_f32(u16(outp)) - ora.bf16_to_f32(want_p)).max())
     print(f"  max-abs err decode {err_d:.3e} prefill {err_p:.3e}")
     assert err_d <= TOL and err_p <= TOL
+
+
+ANY_DIMS = [d for d in range(16, 257, 16) if d != 128]
+
+
+@pytest.mark.parametrize("seed", _seeds(12))
+def test_head_dim_sweep(pkg, dev, seed):
+    """Head sizes other than 128 (the generic kernels): each seed draws the
+    size from the multiples of 16 up to 256, the entry (prefill, decode or
+    the mixed launch, in turn) and a shape as the sweeps above."""
+    from test_gpu_decode import _run_and_check
+    from test_gpu_mixed import _case, _run
+    from test_gpu_prefill import _prefill
+    rng = np.random.default_rng(4000 + seed)
+    d = int(rng.choice(ANY_DIMS))
+    kind = ("prefill", "decode", "mixed")[seed % 3]
+    h, hkv = _heads(rng)
+    bs = int(rng.choice(PAGE_SIZES))
+    cap = 6.0 if rng.random() < 0.25 else None
+    print(f"head-dim sweep seed {seed}: {kind} d {d} H {h} Hkv {hkv} page {bs} cap {cap}", flush=True)
+    if kind == "prefill":
+        batch = int(rng.integers(1, 9))
+        new = rng.integers(1, 300, batch).tolist()
+        prefix = np.where(rng.random(batch) < 0.5, rng.integers(0, 500, batch), 0).tolist()
+        pb = wl.make_prefix_prefill(prefix, new, num_heads=h, num_kv_heads=hkv, page_size=bs, head_dim=d,
+                                    rng=np.random.default_rng(seed))
+        _prefill(pkg, dev, pb, seed, soft_cap=cap, use_seam=cap is None)
+    elif kind == "decode":
+        lens = rng.integers(0, 4000, int(rng.integers(1, 13))).tolist()
+        width = 1 << (max(max(-(-n // bs) for n in lens), 1) - 1).bit_length()
+        db = wl.make_decode(lens, num_heads=h, num_kv_heads=hkv, page_size=bs, head_dim=d,
+                            rng=np.random.default_rng(seed), table_width=width)
+        _run_and_check(pkg, dev, db, seed, soft_cap=cap)
+    else:
+        nd, npre = int(rng.integers(1, 6)), int(rng.integers(0, 4))
+        dec = rng.integers(0, 3000, nd).tolist()
+        pre_q = rng.integers(1, 200, npre).tolist()
+        pre_p = np.where(rng.random(npre) < 0.5, rng.integers(0, 400, npre), 0).tolist()
+        q, kc, vc, bt, cu, kv, pos = _case(rng, dec, pre_q, pre_p, h, hkv, bs, pad_rows=1, d=d)
+        root = float(ora.round_bf16(np.float32(np.sqrt(d))).reshape(-1)[0])
+        got = _run(pkg, dev, q, kc, vc, bt, cu, kv, pos, nd, max(pre_q) if pre_q else 0, soft_cap=cap,
+                   decode_scale=1.0 / root)
+        want = ora.mixed_attention(q, kc.transpose(2, 0, 1, 3), vc.transpose(2, 0, 1, 3), bt, cu, kv, pos, nd,
+                                   soft_cap=cap)
+        err = float(np.abs(ora.bf16_to_f32(got) - ora.bf16_to_f32(want)).max())
+        print(f"  max-abs err {err:.3e}")
+        assert err <= TOL
+        zero = np.ones(q.shape[0], bool)
+        zero[cu[:nd]] = False
+        for b in range(nd, len(kv)):
+            zero[cu[b]:cu[b + 1]] = False
+        zero[cu[:nd][kv[:nd] == 0]] = True
+        assert not got[zero].any()
