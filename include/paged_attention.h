@@ -31,7 +31,7 @@
  *     256 (generic kernels, same arithmetic, lower throughput); float8 pages
  *     take 128 only;
  *   - q heads per kv head: any number for decode, up to 256 for prefill and
- *     pa_mixed (up to 128 for prefill at head sizes other than 128).
+ *     pa_mixed (up to 128 for prefill at head sizes from 144 on).
  */
 #ifndef VLLM_JAX_AMD_PAGED_ATTENTION_H_
 #define VLLM_JAX_AMD_PAGED_ATTENTION_H_

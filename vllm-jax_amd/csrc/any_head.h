@@ -9,8 +9,6 @@ namespace pa {
 struct PrefillParams;
 struct DecodeParams;
 
-constexpr int kAnyRows = 128;  // q rows (token, head) per prefill workgroup
-
 // True for the head sizes the kernels of any_head.hip are built for: the
 // multiples of 16 from 16 to 256 other than 128 (the tuned kernels' size).
 bool any_head_dim(int head_dim);

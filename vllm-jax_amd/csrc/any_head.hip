@@ -32,7 +32,9 @@
 namespace pa {
 namespace {
 
-constexpr int kAnyWaves = 4;                 // prefill waves per workgroup, 32 q rows each
+// Prefill waves per workgroup (32 q rows each): 8 while the registers allow
+// two waves per SIMD (head sizes up to 112), else 4.
+__host__ __device__ constexpr int any_prefill_waves(int d) { return d <= 112 ? 8 : 4; }
 constexpr int kAnyStep = 32;                 // kv tokens per step (the MFMA's M)
 
 template <int D>
@@ -161,15 +163,16 @@ __device__ __forceinline__ void any_softmax_pv(const f32x16& s, float& m_run, fl
   }
 }
 
-// ---- prefill: one workgroup of 4 waves per (q tile of kAnyRows / G tokens,
+// ---- prefill: one workgroup of 8 or 4 waves per (q tile of 32 * waves / G tokens,
 // sequence, kv head), grid order of prefill_item (no work list).  Row 32w + n
 // of wave w is token row / G, head row % G of the kv head's group.  All
 // waves share the step's K and V tiles (row-major); the next step's
 // K / V chunks are loaded into registers while this step computes.
 template <int D, bool kSoftCap>
-__global__ void __launch_bounds__(64 * kAnyWaves)
+__global__ void __launch_bounds__(64 * any_prefill_waves(D))
 prefill_any_kernel(PrefillParams p) {
   using A = AnyDims<D>;
+  constexpr int kAnyWaves = any_prefill_waves(D);
   constexpr int kThreads = 64 * kAnyWaves;
   constexpr int kStepChunks = kAnyStep * A::kChunks;
   constexpr int kPer = (kStepChunks + kThreads - 1) / kThreads;  // chunks of K (and of V) per thread and step
@@ -495,12 +498,13 @@ bool any_head_dim(int head_dim) {
 
 int prefill_any_launch(const char* name, const PrefillParams& prm, int head_dim, hipStream_t s) {
   PrefillParams p = prm;
-  if (p.group > kAnyRows)
+  const int waves = any_prefill_waves(head_dim);
+  if (p.group > 32 * waves)
     return fail(PA_ERR_UNSUPPORTED, "%s: %d q heads per kv head not supported at head_dim %d (max %d)", name,
-                p.group, head_dim, kAnyRows);
+                p.group, head_dim, 32 * waves);
   p.plan = nullptr;
   p.pool = nullptr;
-  p.tile_tokens = kAnyRows / p.group;
+  p.tile_tokens = 32 * waves / p.group;
   p.n_qtiles = (p.max_seqlen_q + p.tile_tokens - 1) / p.tile_tokens;
   if (p.num_tokens > 0) {
     prefill_any_zero_kernel<<<dim3((unsigned)((p.num_tokens + 3) / 4)), dim3(256), 0, s>>>(p, head_dim);
@@ -511,7 +515,7 @@ int prefill_any_launch(const char* name, const PrefillParams& prm, int head_dim,
   const int64_t items = (int64_t)p.n_qtiles * p.batch * p.num_kv_heads;
   if (items > 0x7fffffff)
     return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)items);
-  const dim3 g((unsigned)items), blk(64 * kAnyWaves);
+  const dim3 g((unsigned)items), blk(64 * waves);
   const bool cap = p.soft_cap > 0.f;
   switch (head_dim) {
 #define PA_ANY_LAUNCH(d)                                             \
