@@ -18,9 +18,8 @@
 //                   eight P values of k-step u, tokens 16u + 8(e/4) + 4h +
 //                   e%4, fill its k slots 8h + e.
 // K and V are staged row-major in LDS with whole-row 16-byte writes.  An
-// A operand of V^T is eight 2-byte reads (d = the lane's row, the eight
-// tokens of its k slots): the 32 lanes of a read take 32 consecutive d of
-// one token, so the reads do not conflict.  The online-softmax state of a
+// A operand of V^T (d = the lane's row, the eight tokens of its k slots) is
+// two transposing 8-byte reads (vt_operand).  The online-softmax state of a
 // column lives in the two lanes (n, 0) and (n, 1), exactly where O^T's
 // column n lives, so the rescale needs no exchange.
 #include <climits>
@@ -53,22 +52,20 @@ typedef char __attribute__((address_space(3))) lds_char;
 
 // A operand of V^T for rows d0 .. d0 + 31 and k-step u from the row-major
 // V tile (rows of `row` bytes): lane (m, h) takes d = d0 + m of the tokens
-// 16u + 4h + {0,1,2,3} and 16u + 8 + 4h + {0,1,2,3}.  Rows d >= the head
-// size read the row padding or the next row: finite or not, they only feed
-// rows of O^T that are never stored.
+// 16u + 4h + {0,1,2,3} and 16u + 8 + 4h + {0,1,2,3}, in two transposing
+// reads (ds_read_b64_tr_b16): in each 16-lane group, lane s addresses 4
+// bf16 of token row s / 4 at columns 4 (s % 4) .. +3 of the group's 16
+// columns and receives column s of the 4 rows.  Rows d >= the head size
+// read the row padding or the next row: finite or not, they only feed rows
+// of O^T that are never stored.
 template <int kRowBytes>
 __device__ __forceinline__ u32x4 vt_operand(const lds_char* v, int d0, int u, int lane) {
-  typedef const uint16_t __attribute__((address_space(3))) lds_u16;
-  const lds_char* col = v + 2 * (d0 + (lane & 31)) + (16 * u + 4 * (lane >> 5)) * kRowBytes;
-  u32x4 a;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int t = (q & 1) * 2 + (q >> 1) * 8;  // token offsets 0, 2, 8, 10 (pairs t, t + 1)
-    const uint32_t lo = *reinterpret_cast<lds_u16*>(col + t * kRowBytes);
-    const uint32_t hi = *reinterpret_cast<lds_u16*>(col + (t + 1) * kRowBytes);
-    a[q] = lo | (hi << 16);
-  }
-  return a;
+  const int sl = lane & 15;
+  const lds_char* a =
+      v + (16 * u + 4 * (lane >> 5) + (sl >> 2)) * kRowBytes + 2 * (d0 + 16 * ((lane >> 4) & 1) + 4 * (sl & 3));
+  const u32x2 lo = __builtin_bit_cast(u32x2, ds_read_tr16((lds_cbytes)a));
+  const u32x2 hi = __builtin_bit_cast(u32x2, ds_read_tr16((lds_cbytes)(a + 8 * kRowBytes)));
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
 }
 
 __device__ __forceinline__ u32x4 lds_ld16(const lds_char* a) {
