@@ -319,6 +319,8 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   // and O never mixes with other rows and is not stored.
   const int ltok = min(rtok, lq_rows - 1);
   const int qpos_ld = p.positions[q0 + ltok];
+  // rows grow with the token: a wave whose first row has no token has none
+  const bool wave_live = 32 * wave < p.tile_tokens * p.group && tok0 + (32 * wave) / p.group < lq_rows;
 
   // Wave w stages its Q rows and, at the end, its O rows in its own LDS:
   // 1 KiB blocks 2w and 2w+1 of K and of V in every stage, the only blocks
@@ -702,6 +704,11 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     constexpr bool kQk = decltype(has_qk)::value;
     using KS = std::integral_constant<int, s>;
     using VS = std::integral_constant<int, (s + kStages - 1) % kStages>;
+    // A wave with no row (past the last token of a sequence's last q tile)
+    // skips its MFMA and softmax work in the steady-state iterations; its
+    // tile loads, waits and barriers stay.  Under the part's power limit the
+    // energy it saves goes to the other waves.
+    if (!(kPv && kQk) || wave_live) {
     if constexpr (kPv) pv(VS{});
     if constexpr (kQk) qk(KS{});
     if constexpr (kPv && kQk) {
@@ -716,6 +723,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
         if (next <= 16) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
         else if (next <= 32) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
       }
+    }
     }
     wait_vm_lgkm0<15>();  // LDS reads of this segment retired (vmcnt untouched)
     barrier();
@@ -739,7 +747,12 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
       if constexpr (kPv || kQk) dma_issue(ta, u, dstage);
     };
     if constexpr (kQk) {
-      softmax(t, between);
+      if (!kPv || wave_live) {
+        softmax(t, between);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) between(u);
+      }
     } else {
 #pragma unroll
       for (int u = 0; u < 4; ++u) between(u);
