@@ -215,3 +215,22 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(lib_mod, "lib_path", lambda: str(tmp_path / "missing.so"))
     with pytest.raises(RuntimeError, match="missing"):
         lib_mod.load()
+
+
+def test_generic_head_sizes_at_the_boundary():
+    """Head sizes other than 128: multiples of 16 up to 256 are taken by
+    pa_prefill / pa_decode / pa_mixed (they then fail here only on their null
+    pointers), float8 pages keep refusing them, and the mixed workspace of a
+    generic size holds the decode partials of every chunk after 256 bytes."""
+    lib = PKG._lib.load()
+    r256 = lambda n: (n + 255) // 256 * 256
+    # 2 decodes, 16 heads, 40-page tables of 256-token pages: 3 chunks of 4096 tokens
+    assert lib.pa_mixed_workspace_size(5, 2, 300, 16, 8, 64, 40, 256) == 256 + r256(2 * 16 * 3 * (64 + 2) * 4)
+    assert lib.pa_mixed_workspace_size(5, 0, 300, 16, 8, 96, 40, 256) == 256          # no decode sequence
+    assert lib.pa_mixed_workspace_size(5, 2, 300, 16, 8, 100, 40, 256) == 0           # not a multiple of 16
+    assert lib.pa_mixed_workspace_size(5, 2, 300, 16, 8, 272, 40, 256) == 0           # above 256
+    # float8 decode: head size 64 is refused before any pointer is looked at
+    fp8 = [None, 2048, 64, None, None, None, None, 16, 256, 131072, 512, 64, 4096, 256, None, 4, 4, None, 2,
+           32, 8, 64, 1.0, 0.0, None, 2048, 64, None, 0, None]
+    assert lib.pa_decode_fp8(*fp8) == -2
+    assert "head_dim" in lib.pa_last_error().decode()
