@@ -330,12 +330,16 @@ template <int D, bool kSoftCap>
 __global__ void __launch_bounds__(64)
 decode_any_kernel(DecodeParams p) {
   using A = AnyDims<D>;
-  constexpr int kPer = kAnyStep * A::kChunks / 64;  // chunks of K (and of V) per lane and step
-  // the next step's rows are loaded while this step computes, up to the head
-  // size whose registers still allow it without spills
+  // Up to head size 64 a load batch is two 32-token steps (more bytes in
+  // flight per wave for one wave less per SIMD); the next batch is loaded
+  // while this one computes, up to the head size whose registers still allow
+  // it without spills.
+  constexpr int kSub = D <= 64 ? 2 : 1;
+  constexpr int kTok = kAnyStep * kSub;             // tokens per load batch
+  constexpr int kPer = kTok * A::kChunks / 64;      // chunks of K (and of V) per lane and batch
   constexpr bool kPrefetch = kSoftCap ? D <= 192 : D <= 224;
-  __shared__ __attribute__((aligned(16))) char k_tile_g[kAnyStep * A::kRow];
-  __shared__ __attribute__((aligned(16))) char v_tile_g[A::kVTile];
+  __shared__ __attribute__((aligned(16))) char k_tile_g[kTok * A::kRow];
+  __shared__ __attribute__((aligned(16))) char v_tile_g[kTok * A::kRow + 32];  // V^T operands read 16 bytes past
   lds_char* k_tile = (lds_char*)k_tile_g;
   lds_char* v_tile = (lds_char*)v_tile_g;
   const int lane = threadIdx.x;
@@ -389,7 +393,7 @@ decode_any_kernel(DecodeParams p) {
   for (int dt = 0; dt < A::kDt; ++dt) acc[dt] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
   if constexpr (kPrefetch) load(t0);
-  for (int j0 = t0; j0 < t1; j0 += kAnyStep) {
+  for (int j0 = t0; j0 < t1; j0 += kTok) {
     if constexpr (!kPrefetch) load(j0);
     __syncthreads();  // the previous step's tile reads are done
 #pragma unroll
@@ -402,18 +406,25 @@ decode_any_kernel(DecodeParams p) {
     }
     __syncthreads();
     if constexpr (kPrefetch) {
-      if (j0 + kAnyStep < t1) load(j0 + kAnyStep);
+      if (j0 + kTok < t1) load(j0 + kTok);
     }
-    f32x16 s = {};
 #pragma unroll
-    for (int ks = 0; ks < A::kKs; ++ks)
-      s = mfma32(as_bf16x8(lds_ld16(k_tile + n * A::kRow + 2 * (16 * ks + 8 * h))), qb[ks], s);
+    for (int sub = 0; sub < kSub; ++sub) {
+      const int js = j0 + kAnyStep * sub;
+      if (sub == 0 || js < t1) {  // uniform: a batch's second step may hold no token
+        f32x16 s = {};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int j = j0 + 8 * (i >> 2) + 4 * h + (i & 3);
-      s[i] = j < t1 ? any_logit_f32<kSoftCap>(s[i], p.logit_scale, p.soft_cap) : -INFINITY;
+        for (int ks = 0; ks < A::kKs; ++ks)
+          s = mfma32(as_bf16x8(lds_ld16(k_tile + (kAnyStep * sub + n) * A::kRow + 2 * (16 * ks + 8 * h))), qb[ks],
+                     s);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int j = js + 8 * (i >> 2) + 4 * h + (i & 3);
+          s[i] = j < t1 ? any_logit_f32<kSoftCap>(s[i], p.logit_scale, p.soft_cap) : -INFINITY;
+        }
+        any_softmax_pv<A::kDt, A::kRow, false>(s, m_run, l_run, acc, v_tile + kAnyStep * sub * A::kRow, lane);
+      }
     }
-    any_softmax_pv<A::kDt, A::kRow, false>(s, m_run, l_run, acc, v_tile, lane);
   }
   const float l_tot = sum_xor32(l_run);
   if (!live) return;
