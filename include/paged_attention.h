@@ -130,7 +130,9 @@ int pa_decode(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
  * those of pa_decode; a launch whose pa_decode_workspace_size exceeds the
  * array returns PA_ERR_WORKSPACE before touching the device.  The array's
  * device address is looked up once per device, on the first call with that
- * device current (the stream must belong to the current device).  Calls
+ * device current (the stream must belong to the current device); a caller
+ * that captures the call in a HIP graph makes one call on the device before
+ * the capture, after which a call records only kernel launches.  Calls
  * that overlap on one GPU share the array and race: serialise them (one
  * stream, or events).  No counterpart in the reference: it exists for callers
  * that cannot allocate device memory (code under HIP graph capture, serving

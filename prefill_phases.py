@@ -1,8 +1,9 @@
 """Per-workgroup phase table of the prefill kernel.
 
 Runs ``pa_prefill`` from ``libpaged_attention_phases.so`` (the prefill
-entry points built with ``PA_PREFILL_PHASES``; ``build.py`` makes it) on one
-of the benchmark workloads and prints where each workgroup's time goes.  The
+entry points built with ``PA_PREFILL_PHASES``; ``python3
+vllm-jax_amd/build.py --phases`` makes it next to this script, and the
+package never loads it) on one of the benchmark workloads and prints where each workgroup's time goes.  The
 kernel stamps ``s_memrealtime`` (100 MHz) at five points of every item:
 
     T0 item start          T1 kv range and tile count known
@@ -18,10 +19,11 @@ ran, its loop time per tile and its CUs' last ends.
 
 Usage (one GPU)::
 
-    python3 vllm-jax_amd/prefill_phases.py long     # Qwen3-32B, 8 x ~26.7k tokens
-    python3 vllm-jax_amd/prefill_phases.py prefix   # Qwen3-8B prefix-cached
-    python3 vllm-jax_amd/prefill_phases.py short    # 64 x 1024 tokens, 16/8 heads
-    python3 vllm-jax_amd/prefill_phases.py prefix --dump stamps.npy
+    python3 vllm-jax_amd/build.py --phases         # once, on the build machine
+    python3 prefill_phases.py long     # Qwen3-32B, 8 x ~26.7k tokens
+    python3 prefill_phases.py prefix   # Qwen3-8B prefix-cached
+    python3 prefill_phases.py short    # 64 x 1024 tokens, 16/8 heads
+    python3 prefill_phases.py prefix --dump stamps.npy
 
 ``--dump FILE`` also saves the raw records (one row of 8 uint64 per
 workgroup that ran an item: T0..T4, HW_ID | XCC_ID << 32, tiles,
@@ -40,15 +42,14 @@ import sys
 
 import numpy as np
 
-PKG_DIR = os.path.dirname(os.path.abspath(__file__))
-ROOT = os.path.dirname(PKG_DIR)
-PHASES_LIB = os.path.join(PKG_DIR, "libpaged_attention_phases.so")
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PHASES_LIB = os.path.join(ROOT, "libpaged_attention_phases.so")
 SLOTS = 1 << 17  # workgroup ids the kernel records (8 words each)
 
 
 def _load(pkg):
     if not os.path.exists(PHASES_LIB):
-        raise RuntimeError(f"{PHASES_LIB} is missing: run python vllm-jax_amd/build.py first")
+        raise RuntimeError(f"{PHASES_LIB} is missing: run python3 vllm-jax_amd/build.py --phases first")
     lib = ctypes.CDLL(PHASES_LIB)
     for name in ("pa_prefill", "pa_prefill_workspace_size", "pa_last_error"):
         res, args = pkg._lib.SIGNATURES[name]

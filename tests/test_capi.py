@@ -33,18 +33,23 @@ def test_library_exports_every_declared_symbol():
     assert set(declared) <= set(PKG._lib.SIGNATURES)
 
 
-def test_phase_timestamp_build_exports_its_readers():
-    """The prefill build with per-workgroup phase stamps (a measurement
-    library, never loaded by the package) carries the prefill entry points
-    and the stamp readers; the library proper has no stamps."""
-    path = os.path.join(ROOT, "vllm-jax_amd", "libpaged_attention_phases.so")
-    assert os.path.exists(path), "build the libraries first (__graft_entry__.build())"
-    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
-    exported = set(re.findall(r"\bT (pa_\w+)$", out, re.M))
-    assert {"pa_prefill", "pa_prefill_workspace_size", "pa_prefill_phases_read", "pa_prefill_phases_clear"} <= exported
+def test_library_has_no_phase_stamps():
+    """The per-workgroup phase stamps live only in the opt-in measurement
+    build (``build.py --phases``); the library proper carries none."""
     proper = subprocess.run(["nm", "-D", "--defined-only", PKG._lib.lib_path()], capture_output=True, text=True,
                             check=True).stdout
     assert "pa_prefill_phases" not in proper
+
+
+def test_phase_timestamp_build_exports_its_readers():
+    """When the measurement build exists it carries the prefill entry points
+    and the stamp readers that ``prefill_phases.py`` binds."""
+    path = os.path.join(ROOT, "libpaged_attention_phases.so")
+    if not os.path.exists(path):
+        pytest.skip("opt-in measurement build not present (python vllm-jax_amd/build.py --phases)")
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (pa_\w+)$", out, re.M))
+    assert {"pa_prefill", "pa_prefill_workspace_size", "pa_prefill_phases_read", "pa_prefill_phases_clear"} <= exported
 
 
 def test_error_codes_match_header():
@@ -84,6 +89,21 @@ def test_decode_rejects_bad_arguments_without_a_device():
     assert "null pointer" in lib.pa_last_error().decode()
     assert lib.pa_decode(*_decode_args(batch=0)) == 0                  # nothing to do
     assert lib.pa_decode(*_decode_args(page_size=0)) == -1
+
+
+def test_decode_noalloc_refuses_oversized_launch_without_a_device():
+    """pa_decode_noalloc checks its workspace need against the static
+    scratch (64 MiB) before it touches a device: a launch that would need
+    more returns PA_ERR_WORKSPACE with the sizes in the message."""
+    lib = PKG._lib.load()
+    # 4096 sequences x 64 q heads x 64 chunks of 2048 tokens: ~8.7 GB of partials
+    a = _decode_args(batch=4096, heads=64, kv_heads=8, pps=512, bt_stride=512)
+    need = lib.pa_decode_workspace_size(4096, 64, 128, 512, 256)
+    assert need > lib.pa_decode_noalloc_max_workspace()
+    rc = lib.pa_decode_noalloc(*a[:-2], a[-1])
+    assert rc == -3
+    msg = lib.pa_last_error().decode()
+    assert "more than the 67108864 bytes" in msg and str(need) in msg, msg
 
 
 def test_prefill_rejects_bad_arguments_without_a_device():

@@ -243,14 +243,20 @@ def _expected_list(pb, num_tokens, max_seqlen):
     return want
 
 
-@pytest.mark.parametrize("case", ["prefix", "many", "padded"])
+@pytest.mark.parametrize("case", ["prefix", "many", "padded", "pooled"])
 def test_prefill_work_list(pkg, dev, case):
     """The work list (caller workspace) holds every (sequence, q tile) pair
     with rows once, with its geometry, in non-increasing cost class, a
     sequence's q tiles of one class in descending order; and the output with
-    the list is bit-identical to the grid-order output without."""
+    the list is bit-identical to the grid-order output without.  "pooled"
+    is the smallest launch that runs the pooled kernel (16 384 items: 16
+    sequences of 4 096 tokens, 64 q / 8 kv heads): a pool item dropped or
+    run twice would change the output, and every XCD's pool counter must
+    have reached its pool size (a quarter of that XCD's items)."""
     import torch
-    if case == "prefix":
+    if case == "pooled":
+        pb = wl.make_prefill([4096] * 16, num_heads=64, num_kv_heads=8, rng=np.random.default_rng(13))
+    elif case == "prefix":
         pb = wl.make_prefix_prefill([0, 300, 512, 40, 1500, 3], [130, 64, 200, 1, 700, 260], num_heads=32,
                                     num_kv_heads=8, rng=np.random.default_rng(7), shared_prefix_tokens=1600)
     elif case == "many":
@@ -273,6 +279,12 @@ def test_prefill_work_list(pkg, dev, case):
     want = _expected_list(pb, t["q"].shape[0], pb.max_seqlen_bucket)
     count = int(plan[0])
     assert count == len(want)
+    if case == "pooled":
+        items_per_xcd = count * (pb.num_kv_heads // 8)
+        assert count * pb.num_kv_heads >= 16384, "the launch is below the pooled kernel's threshold"
+        counters = plan[8:16]
+        print(f"pool counters {counters.tolist()} (pool size {items_per_xcd // 4})", flush=True)
+        assert (counters >= items_per_xcd // 4).all(), counters
     rec = plan[64:64 + 8 * count].reshape(count, 8)
     seen = set()
     costs = []

@@ -77,7 +77,7 @@ def test_decode_shape_errors_match_reference():
         PKG.decode_paged_attention(*a, k_scales_pages=torch.zeros(1))
     hkv, nb, bs = a[1].shape[:3]
     sc = torch.ones(hkv, nb, bs)
-    with pytest.raises(ValueError, match="float8_e4m3fn"):        # bf16 pages with scales
+    with pytest.raises(NotImplementedError, match="float8_e4m3fn"):        # bf16 pages with scales
         PKG.decode_paged_attention(*a, k_scales_pages=sc, v_scales_pages=sc)
     with pytest.raises(ValueError, match="k_scales_pages must have shape"):
         PKG.decode_paged_attention(*a, k_scales_pages=sc[:, :1], v_scales_pages=sc)
@@ -123,3 +123,26 @@ def test_check_slot_mapping_finds_duplicates():
     with pytest.raises(ValueError, match="2 slot"):
         check_slot_mapping(torch.tensor([9, 9, 2, 2, 63], dtype=torch.int32), 64)
     check_slot_mapping(torch.tensor([9, 9, 64, 64], dtype=torch.int32)[2:], 64)  # both past the pool
+
+
+@pytest.mark.parametrize("dtype", [torch.uint8, torch.int8])
+def test_integer_pages_are_refused_not_read_as_float8(dtype):
+    """The reference casts quantized pages of any dtype to q's dtype
+    (decode_paged_attention.py:72-75,108-115; prefill_paged_attention.py:
+    84-85,118-123), so uint8 / int8 pages mean integer values.  The entries
+    take float8_e4m3fn codes only and refuse integer pages before any device
+    work, instead of reading their bytes as e4m3 codes."""
+    q, kp, _, bt, lens = _decode_args()
+    hkv, nb, bs, d = kp.shape
+    pages = torch.zeros(hkv, nb, bs, d, dtype=dtype)
+    sc = torch.ones(hkv, nb, bs)
+    with pytest.raises(NotImplementedError, match="must be float8_e4m3fn"):
+        PKG.decode_paged_attention(q, pages, pages, bt, lens, k_scales_pages=sc, v_scales_pages=sc)
+    a = _prefill_args(hkv=hkv, nb=nb, bs=bs)
+    with pytest.raises(NotImplementedError, match="must be float8_e4m3fn"):
+        PKG.prefill_paged_attention(a[0], pages, pages, *a[3:], max_seqlen_bucket=8,
+                                    k_scales_pages=sc, v_scales_pages=sc)
+    with pytest.raises(ValueError, match="float8_e4m3fn pool"):
+        PKG.update_kv_cache_fp8(torch.zeros(2, nb, bs, hkv, d, dtype=dtype), torch.ones(2, hkv, nb, bs),
+                                torch.zeros(5, dtype=torch.int32), torch.zeros(5, hkv, d, dtype=torch.bfloat16),
+                                torch.zeros(5, hkv, d, dtype=torch.bfloat16))

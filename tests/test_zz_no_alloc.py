@@ -79,3 +79,44 @@ def test_decode_noalloc_two_calls_match_pa_decode(pkg, dev):
         print(f"no-alloc decode vs oracle max-abs err {err:.3e}", flush=True)
         assert err <= TOL, err
     torch.cuda.synchronize()
+
+
+def test_decode_noalloc_replays_from_a_hip_graph(pkg, dev):
+    """The use the entry is for: a caller that captures its decode step in a
+    HIP graph.  The first call on a device looks up the scratch address
+    (hipGetSymbolAddress), so it is made before the capture; the captured
+    call then allocates nothing and records no memset.  Every replay, with a
+    new q written into the captured buffer and eager pa_decode work between
+    replays, must equal pa_decode on that q bit for bit."""
+    import torch
+    rng = np.random.default_rng(44)
+    lens = rng.integers(1, 8192, 64)
+    lens[:3] = [1, 2049, 8192]
+    db = wl.make_decode(lens.tolist(), num_heads=32, num_kv_heads=8, page_size=256, rng=rng, table_width=32)
+    d = wl.materialize_decode(db, 44, dev)
+    _decode(pkg, d, db, noalloc=True)          # first call on this device, outside the capture
+    kv = d["kv_cache"]
+    kp, vp = kv[0].permute(2, 0, 1, 3), kv[1].permute(2, 0, 1, 3)
+    hs, ps, ss, _ = kp.stride()
+    q, bt, lens_d = d["q"], d["block_tables"], d["context_lens"]
+    out = torch.full_like(q, 3.0)
+    args = [q.data_ptr(), q.stride(0), q.stride(1), kp.data_ptr(), vp.data_ptr(), db.num_pages, db.page_size,
+            ps, ss, hs, bt.data_ptr(), bt.stride(0), bt.shape[1], lens_d.data_ptr(), db.batch, db.num_heads,
+            db.num_kv_heads, 128, 1.0 / 11.3125, 0.0, out.data_ptr(), out.stride(0), out.stride(1)]
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        pkg._lib.call("pa_decode_noalloc", *args, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    gen = torch.Generator(device="cpu").manual_seed(45)
+    for replay in range(3):
+        q.copy_((torch.randn(q.shape, generator=gen) * 0.5).to(torch.bfloat16))
+        out.fill_(3.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = _decode(pkg, d, db, noalloc=False)   # eager work between replays
+        same = torch.equal(out, ref)
+        print(f"graph replay {replay}: bit-identical to pa_decode {same}", flush=True)
+        assert same, f"replay {replay} differs from pa_decode"
+    del graph
+    torch.cuda.synchronize()

@@ -205,19 +205,19 @@ def qk_norm_rope_store(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm
 def update_kv_cache_fp8(kv_codes: torch.Tensor, kv_scales: torch.Tensor, slot_mapping: torch.Tensor,
                         k: torch.Tensor, v: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     """Quantising KV store into float8 pages, in place: ``kv_codes`` is the
-    pool ``[2, NB, BS, Hkv, d]`` of float8_e4m3fn (or uint8) codes and
+    pool ``[2, NB, BS, Hkv, d]`` of float8_e4m3fn codes and
     ``kv_scales`` ``[2, Hkv, NB, BS]`` float32 (index 0 = K, 1 = V; each half
     is the reference's ``k_scales_pages`` layout).  Each (token, kv head) row
     is scaled by 448 / max|row| and rounded to e4m3 (round to nearest even);
     the stored scale is max|row| / 448.  Slots outside the pool are skipped.
     Returns ``(kv_codes, kv_scales)``."""
+    if kv_codes.dim() != 5 or kv_codes.shape[0] != 2 or kv_codes.dtype != torch.float8_e4m3fn:
+        raise ValueError("kv_codes must be a [2, NB, BS, Hkv, d] float8_e4m3fn pool")
     for name, t in (("kv_codes", kv_codes), ("kv_scales", kv_scales), ("slot_mapping", slot_mapping),
                     ("k", k), ("v", v)):
         require_device(name, t)
     require_bf16("k", k)
     require_bf16("v", v)
-    if kv_codes.dim() != 5 or kv_codes.shape[0] != 2 or kv_codes.dtype not in (torch.float8_e4m3fn, torch.uint8):
-        raise ValueError("kv_codes must be a [2, NB, BS, Hkv, d] float8_e4m3fn / uint8 pool")
     _, nb, bs, hkv, d = kv_codes.shape
     if tuple(kv_scales.shape) != (2, hkv, nb, bs) or kv_scales.dtype != torch.float32:
         raise ValueError(f"kv_scales must be float32 [2, {hkv}, {nb}, {bs}]")

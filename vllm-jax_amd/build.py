@@ -4,9 +4,12 @@ Compiles every HIP/C++ source under ``csrc/`` with hipcc into one shared
 library next to this file.  Run ``python vllm-jax_amd/build.py`` or call
 :func:`build`.  hipcc cross-compiles for gfx950 without a GPU present.
 
-It also builds ``libpaged_attention_phases.so``: the prefill entry points
-compiled with ``PA_PREFILL_PHASES``, whose kernel records per-workgroup
-phase timestamps (read by ``prefill_phases.py``).  Nothing else loads it.
+``python vllm-jax_amd/build.py --phases`` (or ``build(phases=True)``) builds
+only ``libpaged_attention_phases.so`` at the repository root instead: the
+prefill entry points compiled with ``PA_PREFILL_PHASES``, whose kernel
+records per-workgroup phase timestamps for the measurement script
+``prefill_phases.py``.  The package never loads it, and the default build
+does not make it.
 """
 from __future__ import annotations
 
@@ -20,7 +23,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 LIB_NAME = "libpaged_attention.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-PHASES_LIB_PATH = os.path.join(PKG_DIR, "libpaged_attention_phases.so")
+PHASES_LIB_PATH = os.path.join(os.path.dirname(PKG_DIR), "libpaged_attention_phases.so")
 ARCH = "gfx950"
 
 SOURCES = ["pa_errors.cpp", "block_manager.cpp", "kv_store.hip", "decode.hip", "prefill.hip", "qk_norm_rope.hip",
@@ -43,13 +46,13 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found: cannot build the gfx950 paged-attention library")
 
 
-def build(verbose: bool = False, jobs: int = 4) -> str:
-    """Compile all sources and link ``libpaged_attention.so`` (and the
-    phase-timestamp build of prefill); returns the product library's path."""
+def build(verbose: bool = False, jobs: int = 4, phases: bool = False) -> str:
+    """Compile all sources and link ``libpaged_attention.so``; returns its
+    path.  With ``phases`` build only the phase-timestamp prefill library."""
     hipcc = _hipcc()
     with tempfile.TemporaryDirectory(prefix="pa_build_") as tmp:
         procs = []
-        libs = ((SOURCES, LIB_PATH, []), (PHASES_SOURCES, PHASES_LIB_PATH, ["-DPA_PREFILL_PHASES"]))
+        libs = ((PHASES_SOURCES, PHASES_LIB_PATH, ["-DPA_PREFILL_PHASES"]),) if phases else ((SOURCES, LIB_PATH, []),)
         for i, (sources, _, defines) in enumerate(libs):
             for src in sources:
                 obj = os.path.join(tmp, f"{i}_{src}.o")
@@ -78,7 +81,7 @@ def build(verbose: bool = False, jobs: int = 4) -> str:
             # Replace atomically so a process that has the old library mapped keeps it.
             shutil.copyfile(tmp_lib, lib_path + ".tmp")
             os.replace(lib_path + ".tmp", lib_path)
-    return LIB_PATH
+    return libs[0][1]
 
 
 def _wait(item, verbose):
@@ -94,4 +97,4 @@ def _wait(item, verbose):
 
 
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    print(build(verbose="-v" in sys.argv, phases="--phases" in sys.argv))

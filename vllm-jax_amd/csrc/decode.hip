@@ -53,7 +53,7 @@ decode_plan_kernel(DecodeParams p, int32_t* __restrict__ plan) {
   if (tid == 0) plan[0] = count;
 }
 
-template <bool kAligned, bool kSoftCap, bool kFp8 = false>
+template <bool kAligned, bool kSoftCap, bool kFp8 = false, bool kShared = false>
 __global__ void __launch_bounds__(256, 2)
 decode_split_kernel(DecodeParams p) {
   __shared__ DecodeLds red;
@@ -75,7 +75,8 @@ decode_split_kernel(DecodeParams p) {
   } else {
     item = xcd_grouped_item(blockIdx.x, gridDim.x);
   }
-  decode_item<kDecodeWaves, kAligned, kSoftCap, kFp8>(p, item, &red.o[0][0][0], &red.m[0][0], &red.l[0][0]);
+  decode_item<kDecodeWaves, kAligned, kSoftCap, kFp8, kShared>(p, item, &red.o[0][0][0], &red.m[0][0],
+                                                               &red.l[0][0]);
 }
 
 // One wave per (sequence, q head): out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M).
@@ -284,8 +285,13 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
     const bool aligned = page_size % kDecodeStep == 0;
     const bool cap = prm.soft_cap > 0.f;
     const dim3 grid((unsigned)blocks), block(64 * kDecodeWaves);
-    if (fp8 && !cap) decode_split_kernel<true, false, true><<<grid, block, 0, s>>>(prm);
+    // more than 16 q heads per kv head: several items read each kv head's
+    // K/V, so the loads stay cacheable (the soft cap keeps the streaming form)
+    const bool shared = prm.hblocks > 1;
+    if (fp8 && !cap && shared) decode_split_kernel<true, false, true, true><<<grid, block, 0, s>>>(prm);
+    else if (fp8 && !cap) decode_split_kernel<true, false, true><<<grid, block, 0, s>>>(prm);
     else if (fp8) decode_split_kernel<true, true, true><<<grid, block, 0, s>>>(prm);
+    else if (aligned && !cap && shared) decode_split_kernel<true, false, false, true><<<grid, block, 0, s>>>(prm);
     else if (aligned && !cap) decode_split_kernel<true, false><<<grid, block, 0, s>>>(prm);
     else if (aligned) decode_split_kernel<true, true><<<grid, block, 0, s>>>(prm);
     else if (!cap) decode_split_kernel<false, false><<<grid, block, 0, s>>>(prm);

@@ -119,6 +119,20 @@ __device__ __forceinline__ u32x4 ld16_stream(const void* p) {
 __device__ __forceinline__ u32x2 ld8_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
 }
+// K/V loads of a decode item: streamed, unless kShared (more than 16 q heads
+// per kv head: the item's q-head blocks are separate items on one XCD, run
+// next to each other, and each reads the kv head's K and V; cacheable loads
+// let the later blocks hit the XCD's L2 instead of HBM).
+template <bool kShared>
+__device__ __forceinline__ u32x4 ld16_kv(const void* p) {
+  if constexpr (kShared) return *reinterpret_cast<const u32x4*>(p);
+  else return ld16_stream(p);
+}
+template <bool kShared>
+__device__ __forceinline__ u32x2 ld8_kv(const void* p) {
+  if constexpr (kShared) return *reinterpret_cast<const u32x2*>(p);
+  else return ld8_stream(p);
+}
 
 __device__ __forceinline__ f32x4 mfma16k16(const bf16x4v& a, const bf16x4v& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
@@ -157,7 +171,7 @@ __host__ __device__ inline int decode_chunk_tokens(int page_size) { return page_
 // (decode_paged_attention.py:72-81,108-115): K is widened to bf16 exactly
 // and its logits multiplied by the token's K scale; P is multiplied by the
 // token's V scale before PV.  Half the K/V bytes of the bf16 path.
-template <int kWaves, bool kAligned, bool kSoftCap, bool kFp8 = false>
+template <int kWaves, bool kAligned, bool kSoftCap, bool kFp8 = false, bool kShared = false>
 __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, float* red_o, float* red_m,
                                             float* red_l) {
   static_assert(kWaves == 4 || kWaves == 8, "the combine splits d over the waves");
@@ -273,9 +287,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
       // gives lane l row 8r + l / 8, 16-byte chunk l % 8
 #pragma unroll
       for (int r = 0; r < kKLoads; ++r)
-        kd[r] = ld16_stream(kbase + (int64_t)min(8 * r + (lane >> 3), lim) * rs + 16 * (lane & 7));
+        kd[r] = ld16_kv<kShared>(kbase + (int64_t)min(8 * r + (lane >> 3), lim) * rs + 16 * (lane & 7));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vd[i] = ld8_stream(vbase + (int64_t)min(4 * g + i, lim) * rs + 8 * n);
+      for (int i = 0; i < 4; ++i) vd[i] = ld8_kv<kShared>(vbase + (int64_t)min(4 * g + i, lim) * rs + 8 * n);
       sb[j][0] = ld16(ksp);
       sb[j][1] = ld16(vsp);
     } else if constexpr (kAligned) {
@@ -294,9 +308,9 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
       // K rows whole (one 256-byte row per 16-lane group), streamed like V:
       // load i gives lane (n, g) row 4i + g, chunk n
 #pragma unroll
-      for (int i = 0; i < 4; ++i) kd[i] = ld16_stream(kbase + (int64_t)min(4 * i + g, lim) * rs + 8 * n);
+      for (int i = 0; i < 4; ++i) kd[i] = ld16_kv<kShared>(kbase + (int64_t)min(4 * i + g, lim) * rs + 8 * n);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vd[i] = ld16_stream(vbase + (int64_t)min(4 * g + i, lim) * rs + 8 * n);
+      for (int i = 0; i < 4; ++i) vd[i] = ld16_kv<kShared>(vbase + (int64_t)min(4 * g + i, lim) * rs + 8 * n);
     } else {
       if (!valid) {
 #pragma unroll
@@ -314,7 +328,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
 #pragma unroll
       for (int s = 0; s < 4; ++s) kd[s] = ld16(krow + 8 * (4 * s + g));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) vd[i] = ld16_stream(p.v_cache + tok_off(t0 + min(4 * g + i, lim)) + 8 * n);
+      for (int i = 0; i < 4; ++i) vd[i] = ld16_kv<kShared>(p.v_cache + tok_off(t0 + min(4 * g + i, lim)) + 8 * n);
     }
   };
 

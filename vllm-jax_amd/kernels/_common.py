@@ -74,8 +74,12 @@ def check_quantized_pages(k_pages: torch.Tensor, v_pages: torch.Tensor, k_scales
     if tuple(k_scales_pages.stride()) != tuple(v_scales_pages.stride()):
         raise ValueError("k_scales_pages and v_scales_pages must share strides")
     for name, t in (("k_pages", k_pages), ("v_pages", v_pages)):
-        if t.dtype not in (torch.float8_e4m3fn, torch.uint8):
-            raise ValueError(f"{name} of quantized pages must be float8_e4m3fn (or its uint8 codes), got {t.dtype}")
+        if t.dtype != torch.float8_e4m3fn:
+            # The reference casts pages of any dtype to q's dtype before the
+            # dot (decode...:72-75, prefill...:84-85), so integer pages would
+            # mean integer values: refuse them rather than read their bytes
+            # as float8 codes.
+            raise NotImplementedError(f"{name} of quantized pages must be float8_e4m3fn, got {t.dtype}")
         if t.stride(-1) != 1:
             raise ValueError(f"{name} must be contiguous in its last dimension")
     require_device("k_scales_pages", k_scales_pages)
