@@ -246,8 +246,9 @@ def _expected_list(pb, num_tokens, max_seqlen):
 @pytest.mark.parametrize("case", ["prefix", "many", "padded", "pooled"])
 def test_prefill_work_list(pkg, dev, case):
     """The work list (caller workspace) holds every (sequence, q tile) pair
-    with rows once, with its geometry, in non-increasing cost class, a
-    sequence's q tiles of one class in descending order; and the output with
+    with rows once, with its geometry, in non-increasing cost class, the
+    pairs of one class and one 64-pair planner run adjacent with their q
+    tiles descending; and the output with
     the list is bit-identical to the grid-order output without.  "pooled"
     is the smallest launch that runs the pooled kernel (16 384 items: 16
     sequences of 4 096 tokens, 64 q / 8 kv heads): a pool item dropped or
@@ -296,12 +297,21 @@ def test_prefill_work_list(pkg, dev, case):
         assert tuple(int(x) for x in r[2:6]) == (q0, rows, lk, off), (key, r)
         costs.append(cost)
     assert all(a >= b for a, b in zip(costs, costs[1:])), "work list not in non-increasing cost class"
-    # inside a class, a sequence's q tiles appear costliest (last) first
-    last_qt = {}
-    for r, c in zip(rec, costs):
-        key = (c, int(r[0]))
-        assert int(r[1]) < last_qt.get(key, 1 << 30), (key, int(r[1]))
-        last_qt[key] = int(r[1])
+    # The planner walks pair i = b * nq + (nq - 1 - qt) (a sequence's q tiles
+    # in a row, costliest first) in runs of 64, one run per wave, and each run
+    # reserves its pairs of one class with one atomic: so the pairs of one
+    # (class, run) are adjacent in the list, in lane order (ascending pair
+    # index: a sequence's q tiles descending).
+    nq = -(-pb.max_seqlen_bucket // (256 // (pb.num_heads // pb.num_kv_heads)))
+    groups = {}
+    for rank, (r, c) in enumerate(zip(rec, costs)):
+        run = (int(r[0]) * nq + nq - 1 - int(r[1])) // 64
+        groups.setdefault((c, run), []).append((rank, int(r[0]) * nq + nq - 1 - int(r[1])))
+    for key, members in groups.items():
+        ranks = [m[0] for m in members]
+        pair_ids = [m[1] for m in members]
+        assert ranks == list(range(ranks[0], ranks[0] + len(ranks))), ("run not contiguous", key, ranks[:8])
+        assert all(a < b for a, b in zip(pair_ids, pair_ids[1:])), ("run not in lane order", key, pair_ids[:8])
 
 
 def test_prefill_more_sequences_than_the_planner_holds(pkg, dev):
