@@ -167,7 +167,7 @@ def run_gpu(args):
     # ---------------- prefill: Qwen3-32B long context
     pb = wl.qwen3_32b_long_prefill(seed=4)
     pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False) \
-        if args.only not in ("decode", "mixed", "decode_fp8", "prefix", "prefill_fp8") else None
+        if args.only not in ("decode", "mixed", "decode_fp8", "prefix", "prefill_fp8", "long8", "g32") else None
     if pt is None:  # decode-only profiling run: keep the prefill half tiny
         pb = wl.make_prefill([64], num_heads=64, num_kv_heads=8, rng=np.random.default_rng(0))
         pt = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=False)
@@ -184,7 +184,7 @@ def run_gpu(args):
                                     max_seqlen_bucket=pb.max_seqlen_bucket, out=out_p)
 
     # ---------------- decode: Qwen3-8B
-    db = wl.qwen3_8b_decode(seed=2) if args.only not in ("prefill", "rope", "mixed", "prefix") else \
+    db = wl.qwen3_8b_decode(seed=2) if args.only not in ("prefill", "rope", "mixed", "prefix", "long8", "g32") else \
         wl.make_decode([64], num_heads=32, num_kv_heads=8, rng=np.random.default_rng(0))
     dt_ = wl.materialize_decode(db, seed=2, device=dev)
     kv_d = dt_["kv_cache"]
@@ -256,6 +256,9 @@ def run_gpu(args):
         prefix["roofline"]["traffic"] = _load_traffic().get("prefill_kernel_prefix_cached")
     dec8 = run_decode_fp8(args, torch, pkg, db, dt_, ws, dscale, float(d_attn.mean()) if run_d else None) \
         if run_f else None
+
+    long8 = run_long8(args, torch, pkg, wl, dev) if args.only in (None, "long8") else None
+    g32 = run_g32(args, torch, pkg, wl, dev) if args.only in (None, "g32") else None
 
     traffic = _load_traffic()
     res = {
@@ -333,7 +336,70 @@ def run_gpu(args):
     if dec8 is not None:
         dec8["roofline"]["traffic"] = traffic.get("decode_fp8_split_kernel")
         res["decode_fp8"] = dec8
+    if long8 is not None:
+        long8["roofline"]["traffic"] = traffic.get("prefill_kernel_qwen3_8b_long")
+        res["qwen3_8b_long_prefill"] = long8
+    if g32 is not None:
+        g32["roofline"]["traffic"] = traffic.get("decode_split_kernel_g32")
+        res["decode_g32"] = g32
     return res, (pb, pt, db, dt_)
+
+
+def run_long8(args, torch, pkg, wl, dev):
+    """Time a plain Qwen3-8B-shaped prefill: the long prefill's 8 sequence
+    lengths (213 732 tokens) at 32 q / 8 kv heads (64-token q tiles of 4
+    heads), attention only."""
+    pb = wl.qwen3_8b_long_prefill(seed=4)
+    t = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=True)
+    kp, vp = t["kv_cache"][0].permute(2, 0, 1, 3), t["kv_cache"][1].permute(2, 0, 1, 3)
+    out = torch.empty_like(t["q"])
+
+    def attn():
+        pkg.prefill_paged_attention(t["q"], kp, vp, t["block_tables"], t["cu_seqlens_q"], t["slot_mapping"],
+                                    t["input_positions"], max_seqlen_bucket=pb.max_seqlen_bucket, out=out)
+    quick = argparse.Namespace(warmup=min(args.warmup, 2), steps=min(max(args.steps, 3), 5))
+    ms = _time_ms(torch, attn, quick)
+    tf = pb.flops() / (ms * 1e-3) / 1e12
+    del t, kp, vp, out
+    torch.cuda.empty_cache()
+    return {
+        "metric": "Qwen3-8B-shaped long prefill attn TFLOP/s",
+        "seqs": int(pb.batch), "tokens": int(pb.num_tokens), "num_heads": 32, "num_kv_heads": 8,
+        "algorithmic_tflop": round(pb.flops() / 1e12, 4), "attn_ms": round(ms, 4), "steps": quick.steps,
+        "roofline": {"kernel": "prefill_kernel_pooled", "bound": "mfma", "achieved": round(tf, 2),
+                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": None},
+    }
+
+
+def run_g32(args, torch, pkg, wl, dev):
+    """Time decode with 32 q heads per kv head (64 q / 2 kv heads, the
+    Qwen3-8B decode batch's contexts): each kv head is read by two items of
+    16 q heads, whose K/V loads stay cacheable."""
+    db = wl.g32_decode(seed=2)
+    d = wl.materialize_decode(db, seed=2, device=dev)
+    kv = d["kv_cache"]
+    kp, vp = kv[0].permute(2, 0, 1, 3), kv[1].permute(2, 0, 1, 3)
+    out = torch.empty_like(d["q"])
+    from vllm_jax_amd.kernels.decode_paged_attention import decode_workspace_bytes
+    ws = torch.empty(decode_workspace_bytes(db.batch, db.num_heads, db.head_dim, db.block_tables.shape[1],
+                                            db.page_size), dtype=torch.uint8, device=dev)
+
+    def call():
+        pkg.decode_paged_attention(d["q"], kp, vp, d["block_tables"], d["context_lens"], scale=1.0 / 11.3125,
+                                   workspace=ws, out=out)
+    ms = _time_ms(torch, call, args)
+    gbs = db.hbm_bytes() / (ms * 1e-3) / 1e9
+    del d, kv, kp, vp, out, ws
+    torch.cuda.empty_cache()
+    return {
+        "metric": "decode attn GB/s, 32 q heads per kv head",
+        "seqs": int(db.batch), "num_heads": 64, "num_kv_heads": 2, "algorithmic_gb": round(db.hbm_bytes() / 1e9, 4),
+        "attn_ms": round(ms, 4),
+        "roofline": {"kernel": "decode_split_kernel<true, false, false, true> + decode_merge_kernel", "bound": "hbm",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
 
 
 def run_decode_fp8(args, torch, pkg, db, dt_, ws, dscale, bf16_ms):
@@ -726,6 +792,7 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=24.0, help="seconds of CPU oracle work (total)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["prefill", "decode", "rope", "mixed", "decode_fp8", "prefix", "prefill_fp8",
+                                       "long8", "g32",
                                        "copy", "head_dims"],
                     default=None,
                     help="profiling aid: run one kernel family only (the JSON line then covers that part)")

@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 import vllm_jax_amd.workloads as wl
-from conftest import from_u16, u16
+from conftest import boundary_rows, from_u16, u16
 from oracle import paged_attention_oracle as ora
 
 pytestmark = pytest.mark.gpu
@@ -96,37 +96,89 @@ def test_decode_fp8_matches_oracle(pkg, dev, lens, h, hkv, bs, cap):
     assert not got[np.asarray(lens) == 0].any()
 
 
+def _quantize_pool_on_device(pkg, kv):
+    """The bf16 pool ``[2, NB, BS, Hkv, d]`` quantised to float8 pages with
+    per-token scales by the device store (every slot)."""
+    import torch
+    nb, bs, hkv, d = kv.shape[1:]
+    codes = torch.empty((2, nb, bs, hkv, d), dtype=torch.float8_e4m3fn, device=kv.device)
+    scales = torch.empty((2, hkv, nb, bs), dtype=torch.float32, device=kv.device)
+    slots = torch.arange(nb * bs, dtype=torch.int32, device=kv.device)
+    pkg.update_kv_cache_fp8(codes, scales, slots, kv[0].reshape(-1, hkv, d), kv[1].reshape(-1, hkv, d))
+    return codes, scales
+
+
+def _compact_pages(codes, scales, block_tables, seqs):
+    """The pages the sequences ``seqs`` use, copied to the host as a compact
+    pool with the tables rewritten to it (the oracle reads only these)."""
+    import torch
+    used = sorted(set(int(x) for x in block_tables[seqs].ravel() if x >= 0))
+    remap = {blk: i for i, blk in enumerate(used)}
+    bt = np.array([[remap.get(int(x), 0) if x >= 0 else -1 for x in block_tables[s]] for s in seqs], np.int32)
+    idx = torch.as_tensor(used, dtype=torch.long, device=codes.device)
+    return (_u8(codes[0][idx]), _u8(codes[1][idx]), scales[0][:, idx].cpu().numpy(),
+            scales[1][:, idx].cpu().numpy(), bt)
+
+
 def test_decode_fp8_qwen3_8b_full_pool(pkg, dev):
-    """The Qwen3-8B decode workload with its whole pool quantised on the
-    device; sampled sequences against the oracle over the same codes."""
+    """The Qwen3-8B decode workload (256 sequences, contexts U[512, 8192])
+    with its whole pool quantised on the device; every sequence against the
+    oracle over the same codes and scales, 32 sequences per oracle call."""
     import torch
     db = wl.qwen3_8b_decode(seed=2)
     t = wl.materialize_decode(db, seed=2, device=dev)
-    nb, bs, hkv = db.num_pages, db.page_size, db.num_kv_heads
-    codes = torch.empty((2, nb, bs, hkv, 128), dtype=torch.float8_e4m3fn, device=dev)
-    scales = torch.empty((2, hkv, nb, bs), dtype=torch.float32, device=dev)
-    kv = t["kv_cache"]
-    slots = torch.arange(nb * bs, dtype=torch.int32, device=dev)
-    pkg.update_kv_cache_fp8(codes, scales, slots, kv[0].reshape(-1, hkv, 128), kv[1].reshape(-1, hkv, 128))
+    codes, scales = _quantize_pool_on_device(pkg, t["kv_cache"])
     out = pkg.decode_paged_attention(t["q"], codes[0].permute(2, 0, 1, 3), codes[1].permute(2, 0, 1, 3),
                                      t["block_tables"], t["context_lens"], k_scales_pages=scales[0],
                                      v_scales_pages=scales[1], scale=1 / 11.3125)
     torch.cuda.synchronize()
-    got = u16(out)
-    seqs = [0, int(np.argmax(db.context_lens)), int(np.argmin(db.context_lens)), db.batch - 1]
-    used = sorted(set(int(x) for x in db.block_tables[seqs].ravel() if x >= 0))
-    remap = {blk: i for i, blk in enumerate(used)}
-    bt = np.array([[remap.get(int(x), 0) if x >= 0 else -1 for x in db.block_tables[s]] for s in seqs], np.int32)
-    idx = torch.as_tensor(used, dtype=torch.long, device=dev)
-    kq, vq = _u8(codes[0][idx]), _u8(codes[1][idx])
-    ks = scales[0][:, idx].cpu().numpy()
-    vs = scales[1][:, idx].cpu().numpy()
-    qs = ora.f32_to_bf16(ora.round_bf16(ora.bf16_to_f32(u16(t["q"][seqs])) / np.float32(11.3125)))
-    want = ora.decode_attention(qs, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, db.context_lens[seqs],
-                                k_scales_pages=ks, v_scales_pages=vs)
-    err = np.abs(ora.bf16_to_f32(got[seqs]) - ora.bf16_to_f32(want)).max()
-    print(f"fp8 Qwen3-8B decode max-abs err {err:.3e}")
+    got = ora.bf16_to_f32(u16(out))
+    qs_all = ora.f32_to_bf16(ora.round_bf16(ora.bf16_to_f32(u16(t["q"])) / np.float32(11.3125)))
+    err = 0.0
+    for s0 in range(0, db.batch, 32):
+        seqs = list(range(s0, min(s0 + 32, db.batch)))
+        kq, vq, ks, vs, bt = _compact_pages(codes, scales, db.block_tables, seqs)
+        want = ora.decode_attention(qs_all[seqs], kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt,
+                                    db.context_lens[seqs], k_scales_pages=ks, v_scales_pages=vs)
+        err = max(err, float(np.abs(got[seqs] - ora.bf16_to_f32(want)).max()))
+    print(f"fp8 Qwen3-8B decode, all {db.batch} sequences: max-abs err {err:.3e}", flush=True)
     assert err <= TOL
+
+
+def test_prefill_fp8_qwen3_8b_prefix_workload(pkg, dev):
+    """The Qwen3-8B prefix-cached prefill (64 sequences, cached prefixes
+    U[0, 4096] in shared pages, new chunks U[128, 1024]) over float8 pages:
+    the pool, new tokens stored, quantised on the device; the first, last and
+    q-tile / kv-tile / page-edge rows of every sequence against the oracle
+    over the same codes and scales."""
+    import torch
+    pb = wl.qwen3_8b_prefix_prefill(seed=3)
+    t = wl.materialize_prefill(pb, seed=3, device=dev, fill_pool=True)
+    kv = pkg.update_kv_cache(t["kv_cache"], t["slot_mapping"], t["k"], t["v"])
+    codes, scales = _quantize_pool_on_device(pkg, kv)
+    out = pkg.prefill_paged_attention(t["q"], codes[0].permute(2, 0, 1, 3), codes[1].permute(2, 0, 1, 3),
+                                      t["block_tables"], t["cu_seqlens_q"], t["slot_mapping"],
+                                      t["input_positions"], max_seqlen_bucket=pb.max_seqlen_bucket,
+                                      cu_seqlens_k=t["cu_seqlens_k"], k_scales_pages=scales[0],
+                                      v_scales_pages=scales[1])
+    torch.cuda.synchronize()
+    got = ora.bf16_to_f32(u16(out))
+    prefix = np.diff(pb.cu_seqlens_k) - np.diff(pb.cu_seqlens_q)
+    rows = boundary_rows(pb.cu_seqlens_q, prefix, np.random.default_rng(3),
+                         tile_tokens=256 // (pb.num_heads // pb.num_kv_heads), per_seq=6)
+    cu = pb.cu_seqlens_q
+    assert set(cu[:-1]) <= set(rows) and set(cu[1:] - 1) <= set(rows)
+    kq, vq, ks, vs, bt = _compact_pages(codes, scales, pb.block_tables, list(range(pb.batch)))
+    q = u16(t["q"])
+    want = ora.prefill_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, pb.cu_seqlens_q,
+                                 pb.input_positions, cu_seqlens_k=pb.cu_seqlens_k, rows=rows,
+                                 k_scales_pages=ks, v_scales_pages=vs)
+    err = float(np.abs(got[rows] - ora.bf16_to_f32(want)[rows]).max())
+    print(f"fp8 Qwen3-8B prefix-cached prefill, {rows.size} rows of {pb.batch} sequences: max-abs err {err:.3e}",
+          flush=True)
+    assert err <= TOL
+    padded = np.setdiff1d(np.arange(q.shape[0]), np.arange(cu[-1]))
+    assert not got[padded].any()
 
 
 @pytest.mark.parametrize("lens,prefix,h,hkv,bs", [

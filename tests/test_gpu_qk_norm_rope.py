@@ -138,3 +138,45 @@ def test_qwen3_attention_core_matches_separate_steps(pkg, dev):
     torch.cuda.synchronize()
     err = np.abs(ora.bf16_to_f32(u16(out)) - ora.bf16_to_f32(want)).max()
     assert err <= 2e-2, err
+
+
+def test_qk_norm_rope_store_qwen3_32b_long_workload(pkg, dev):
+    """The Qwen3-32B long-prefill step the bench times: 213 732 tokens of
+    8 sequences (positions 0 .. L-1 each), 64 q / 8 kv heads, into its
+    256-token-page pool.  Every q and k row of 384 sampled tokens (the first
+    and last token of every sequence among them) against the oracle; V of
+    every token and every slot no token writes, bit-exact, on the device."""
+    import torch
+    import vllm_jax_amd.workloads as wl
+    pb = wl.qwen3_32b_long_prefill(seed=4)
+    t = wl.materialize_prefill(pb, seed=4, device=dev, fill_pool=True)
+    rng = np.random.default_rng(17)
+    d, h, hkv = pb.head_dim, pb.num_heads, pb.num_kv_heads
+    qw = ora.f32_to_bf16(rng.uniform(0.5, 1.5, d).astype(np.float32))
+    kw = ora.f32_to_bf16(rng.uniform(0.5, 1.5, d).astype(np.float32))
+    kv = t["kv_cache"]
+    before = kv.clone()
+    q_out, _ = pkg.qk_norm_rope_store(t["q"], t["k"], t["v"], from_u16(qw, dev), from_u16(kw, dev),
+                                      t["input_positions"], t["slot_mapping"], kv, eps=1e-6, rope_theta=1e6)
+    torch.cuda.synchronize()
+    n_tok = pb.num_tokens
+    slots = torch.as_tensor(pb.slot_mapping, dtype=torch.long, device=dev)
+    flat_k, flat_v = kv[0].reshape(-1, hkv, d), kv[1].reshape(-1, hkv, d)
+    assert torch.equal(flat_v[slots], t["v"]), "V rows not stored bit-exact"
+    untouched = torch.ones(flat_k.shape[0], dtype=torch.bool, device=dev)
+    untouched[slots] = False
+    for i in range(2):
+        assert torch.equal(kv[i].reshape(-1, hkv, d)[untouched], before[i].reshape(-1, hkv, d)[untouched]), \
+            "a slot no token writes changed"
+    cu = pb.cu_seqlens_q
+    sel = np.unique(np.concatenate([cu[:-1], cu[1:] - 1, rng.integers(0, n_tok, 384 - 2 * pb.batch)]))
+    print(f"qk norm + rope + store: {n_tok} tokens, {sel.size} sampled", flush=True)
+    idx = torch.as_tensor(sel, dtype=torch.long, device=dev)
+    q_s, k_s, v_s = u16(t["q"][idx]), u16(t["k"][idx]), u16(t["v"][idx])
+    pos = pb.input_positions[sel].astype(np.int32)
+    # the oracle's store into a compact cache of one slot per sampled token
+    kc0 = np.zeros((sel.size, 1, hkv, d), np.uint16)
+    q_want, kc_want, _ = ora.qk_norm_rope_store(q_s, k_s, v_s, qw, kw, pos, np.arange(sel.size, dtype=np.int32),
+                                                kc0, kc0.copy(), eps=1e-6, rope_theta=1e6)
+    _close(u16(q_out[idx]), q_want)
+    _close(u16(flat_k[slots[idx]]), kc_want.reshape(sel.size, hkv, d))

@@ -311,12 +311,31 @@ def qwen3_32b_long_prefill(seed=4) -> PrefillBatch:
     return make_prefill(lens, num_heads=64, num_kv_heads=8, rng=rng)
 
 
+def qwen3_8b_long_prefill(seed=4) -> PrefillBatch:
+    """The long prefill's 8 sequence lengths (L~U[8192,32768], same draws)
+    at Qwen3-8B's heads: 32q/8kv, pool sized to fit."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(8192, 32769, size=8)
+    return make_prefill(lens, num_heads=32, num_kv_heads=8, rng=rng)
+
+
+def g32_decode(seed=2) -> DecodeBatch:
+    """The Qwen3-8B decode batch (256 seqs, ctx~U[512,8192], same draws) with
+    32 q heads per kv head: 64q/2kv, so every kv head is read by two blocks
+    of 16 q heads."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(512, 8193, size=256)
+    return make_decode(lens, num_heads=64, num_kv_heads=2, num_pages=16384, rng=rng)
+
+
 WORKLOADS = {
     "qwen3_0.6b_prefill": qwen3_06b_prefill,
     "qwen3_0.6b_mixed": qwen3_06b_mixed,
     "qwen3_8b_decode": qwen3_8b_decode,
     "qwen3_8b_prefix_prefill": qwen3_8b_prefix_prefill,
     "qwen3_32b_long_prefill": qwen3_32b_long_prefill,
+    "qwen3_8b_long_prefill": qwen3_8b_long_prefill,
+    "g32_decode": g32_decode,
 }
 
 
