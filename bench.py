@@ -576,9 +576,6 @@ def run_mixed(args, torch, pkg, wl, dev):
                                     cu_seqlens_k=cuk, out=op)
 
     def timed(fn):
-        for _ in range(args.warmup):
-            fn()
-        torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(max(args.steps, 10)):   # launches queue ahead of the host
@@ -587,7 +584,17 @@ def run_mixed(args, torch, pkg, wl, dev):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / max(args.steps, 10)
 
-    ms_one, ms_two = timed(one), timed(two)
+    # The part is power-limited, so a launch's speed depends on what ran just
+    # before it: the two paths alternate, the order swapped every round, and
+    # each reports the median of its rounds.
+    for _ in range(args.warmup):
+        one(); two()
+    torch.cuda.synchronize()
+    t_one, t_two = [], []
+    for r in range(6):
+        for fn, acc in (((one, t_one), (two, t_two)) if r % 2 == 0 else ((two, t_two), (one, t_one))):
+            acc.append(timed(fn))
+    ms_one, ms_two = float(np.median(t_one)), float(np.median(t_two))
     flops, dbytes = pre.flops(), dec.hbm_bytes()
     # The step is a prefill half bound by the matrix cores and a decode half
     # bound by HBM; the serial roof is the time of each half at its own peak,
