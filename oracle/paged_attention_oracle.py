@@ -674,17 +674,27 @@ def fp8_e4m3_encode(x) -> np.ndarray:
 
 def quantize_fp8_rows(x):
     """Per-row float8 quantisation of bf16 rows ``[..., d]`` (bit patterns):
-    ``amax = max |x|``, stored scale ``s = amax / 448`` and codes
-    ``e4m3(x * (448 / amax))``, both divisions in float32; an all-zero row
-    stores scale 1 and zero codes.  Returns (codes uint8 [..., d], scales
-    float32 [...]).  This is the library's own quantiser (the reference
-    reads quantized pages but has no writer)."""
+    ``amax = max |x|``; the stored scale is the smallest power of two
+    ``s = 2^e`` with ``amax / s <= 448``, but at least ``2^-126`` (a normal
+    float); the codes are ``e4m3(x / s)`` (the division by a power of two is
+    exact).  An all-zero row stores scale 1 and zero codes.  Returns (codes
+    uint8 [..., d], scales float32 [...]).  This is the library's own
+    quantiser (the reference reads quantized pages but has no writer); a
+    power-of-two scale lets a reader widen code and scale in one exact step."""
     xf = _as_f32(x)
-    amax = np.abs(xf).max(axis=-1)
+    amax = np.abs(xf).max(axis=-1).astype(np.float64)
     nz = amax > 0
-    safe = np.where(nz, amax, np.float32(1.0)).astype(np.float32)
-    inv = np.where(nz, np.float32(E4M3_MAX) / safe, np.float32(1.0)).astype(np.float32)
-    scale = np.where(nz, safe / np.float32(E4M3_MAX), np.float32(1.0)).astype(np.float32)
+    # smallest e with amax <= 448 * 2^e, found from an estimate by exact
+    # float64 comparisons (448 * 2^e is exact)
+    est = np.where(nz, np.ceil(np.log2(np.where(nz, amax, 1.0) / E4M3_MAX)), 0.0).astype(np.int64)
+    e = est.copy()
+    for _ in range(3):
+        e = np.where(nz & (amax > E4M3_MAX * np.exp2(e.astype(np.float64))), e + 1, e)
+    for _ in range(3):
+        e = np.where(nz & (amax <= E4M3_MAX * np.exp2((e - 1).astype(np.float64))), e - 1, e)
+    e = np.maximum(e, -126)
+    scale = np.where(nz, np.exp2(e.astype(np.float64)), 1.0).astype(np.float32)
+    inv = np.where(nz, np.exp2(-e.astype(np.float64)), 1.0).astype(np.float32)
     codes = fp8_e4m3_encode((xf * inv[..., None]).astype(np.float32))
     return codes, scale
 

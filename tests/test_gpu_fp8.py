@@ -273,3 +273,61 @@ def test_prefill_fp8_shared_pages_widened_once(pkg, dev, width):
     err = np.abs(ora.bf16_to_f32(u16(out)) - ora.bf16_to_f32(want)).max()
     print(f"fp8 prefill shared pages max-abs err {err:.3e}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("scale_mult,h,hkv,bs,lens,prefix,cap", [
+    (1.0, 32, 8, 256, [300, 77, 1000], [0, 600, 100], None),   # power-of-two scales: one exact conversion per pair
+    (1.3, 32, 8, 64, [300, 77, 1000], [0, 600, 100], None),    # any scale: widened in float32, one rounding
+    (1.0, 64, 8, 128, [129, 2100], [0, 0], None),              # G = 8, 128-token pages
+    (0.7, 16, 8, 256, [5, 200, 64], [250, 0, 3], 25.0),        # soft cap, G = 2
+    (1.0, 8, 1, 64, [3, 700], [0, 130], None),                 # one kv head
+])
+def test_prefill_fp8_equals_bf16_prefill_over_widened_pages(pkg, dev, scale_mult, h, hkv, bs, lens, prefix, cap):
+    """The float8 prefill widens every distinct page in use to
+    bf16(code * scale) and then runs the bf16 prefill unchanged: its output
+    must equal, bit for bit, pa_prefill over a bf16 pool widened the same way
+    on the host (float32 product, one round to bf16).  With power-of-two
+    scales (the library's quantiser) that product is exact, so the logits are
+    the reference's (q . k_code) * k_scale up to summation order; with other
+    scales each widened element is rounded once.  Both also within the bar of
+    the oracle over the codes and scales."""
+    import torch
+    rng = np.random.default_rng(sum(lens) + h + int(scale_mult * 10))
+    kv = [p + n for p, n in zip(prefix, lens)]
+    pages = [(n + bs - 1) // bs for n in kv]
+    nb = sum(pages) + 2
+    kq, vq, ks, vs = _quantized_pool(rng, nb, bs, hkv)
+    ks = (ks * np.float32(scale_mult)).astype(np.float32)
+    vs = (vs * np.float32(scale_mult)).astype(np.float32)
+    perm = rng.permutation(nb)
+    bt = np.full((len(lens), max(pages)), -1, np.int32)
+    c = 0
+    for b, p in enumerate(pages):
+        bt[b, :p] = perm[c:c + p]
+        c += p
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cuk = np.concatenate([[0], np.cumsum(kv)]).astype(np.int32)
+    pos = np.concatenate([np.arange(p, p + n) for p, n in zip(prefix, lens)]).astype(np.int32)
+    q = _bf16(rng, (int(cu[-1]), h, 128))
+    i32 = lambda x: torch.as_tensor(np.ascontiguousarray(x, dtype=np.int32), device=dev)
+    # host widening: [NB, BS, Hkv, d] codes times the [Hkv, NB, BS] scales
+    kw = ora.f32_to_bf16(ora.fp8_e4m3_decode(kq) * ks.transpose(1, 2, 0)[..., None])
+    vw = ora.f32_to_bf16(ora.fp8_e4m3_decode(vq) * vs.transpose(1, 2, 0)[..., None])
+    kd = torch.from_numpy(kq).to(dev).view(torch.float8_e4m3fn)
+    vd = torch.from_numpy(vq).to(dev).view(torch.float8_e4m3fn)
+    common = dict(max_seqlen_bucket=max(lens), cu_seqlens_k=i32(cuk), attn_logits_soft_cap=cap)
+    got = pkg.prefill_paged_attention(from_u16(q, dev), kd.permute(2, 0, 1, 3), vd.permute(2, 0, 1, 3), i32(bt),
+                                      i32(cu), None, i32(pos), k_scales_pages=torch.from_numpy(ks).to(dev),
+                                      v_scales_pages=torch.from_numpy(vs).to(dev), **common)
+    base = pkg.prefill_paged_attention(from_u16(q, dev), from_u16(kw, dev).permute(2, 0, 1, 3),
+                                       from_u16(vw, dev).permute(2, 0, 1, 3), i32(bt), i32(cu), None, i32(pos),
+                                       **common)
+    torch.cuda.synchronize()
+    same = torch.equal(got, base)
+    want = ora.prefill_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, cu, pos,
+                                 cu_seqlens_k=cuk, k_scales_pages=ks, v_scales_pages=vs, soft_cap=cap)
+    err = np.abs(ora.bf16_to_f32(u16(got)) - ora.bf16_to_f32(want)).max()
+    print(f"fp8 prefill (scales x{scale_mult}): bit-identical to bf16 over widened pages {same}, "
+          f"max-abs err vs oracle {err:.3e}", flush=True)
+    assert same
+    assert err <= TOL

@@ -491,10 +491,21 @@ def test_fp8_row_quantiser():
     back = ora.fp8_e4m3_decode(codes) * sc[:, None]
     assert sc[3] == 1.0 and not codes[3].any()
     amax = np.abs(xf).max(axis=1)
-    # the row maximum maps to +-448 and every element is within half an e4m3 step
-    assert np.all(np.abs(ora.fp8_e4m3_decode(codes)).max(axis=1)[amax > 0] == 448.0)
+    # scales are powers of two, the smallest that keep the row within 448:
+    # the row maximum lands in (224, 448] before rounding
+    m, _ = np.frexp(sc)
+    assert np.all(m == 0.5)
+    assert np.all(amax[amax > 0] / sc[amax > 0] <= 448.0) and np.all(amax[amax > 0] / sc[amax > 0] > 224.0)
+    # every element within half an e4m3 step of its value (relative 2^-4 of the row maximum)
     rel = np.abs(back - xf) / np.maximum(amax[:, None], 1e-30)
     assert rel.max() <= 2.0 ** -4 * 1.0001
+    # edge cases of the scale rule: a maximum of exactly 448 * 2^k and one
+    # just above (next bf16), and a tiny row whose scale stops at 2^-126
+    edge = ora.f32_to_bf16(np.array([[448.0, 1.0], [450.0, 1.0], [2.0 ** -130, 0.0], [1.75 * 2 ** 10, -3.0]],
+                                    dtype=np.float32))
+    ce, se = ora.quantize_fp8_rows(edge)
+    assert list(se) == [1.0, 2.0, 2.0 ** -126, 4.0]
+    assert ora.fp8_e4m3_decode(ce[0, :1])[0] == 448.0 and ora.fp8_e4m3_decode(ce[3, :1])[0] == 448.0
 
 
 def test_decode_fp8_vs_brute_force():

@@ -83,10 +83,14 @@ gather_kv_kernel(const uint16_t* __restrict__ cache, int32_t num_pages, int32_t 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // Quantising KV store: one 16-lane group per (token, kv head) row of d = 128,
-// 8 values per lane.  amax over the row (16-lane butterfly), stored scale
-// amax / 448 and codes e4m3(x * (448 / amax)) with round-to-nearest-even
-// (v_cvt_pk_fp8_f32); an all-zero row stores scale 1.  Codes go to the
-// (page, slot, head) byte pool, scales to a [Hkv, NB, BS]-strided float pool.
+// 8 values per lane.  amax over the row (16-lane butterfly); the stored
+// scale is the smallest power of two s with amax / s <= 448 (at least
+// 2^-126), and the codes are e4m3(x / s) with round-to-nearest-even
+// (v_cvt_pk_fp8_f32), x / s exact; an all-zero row stores scale 1.  A power
+// of two lets the readers widen a code with its scale in one exact
+// conversion (v_cvt_scalef32_pk_bf16_fp8 scales by a power of two).  Codes
+// go to the (page, slot, head) byte pool, scales to a [Hkv, NB, BS]-strided
+// float pool.
 __global__ void __launch_bounds__(256)
 kv_store_fp8_kernel(const uint16_t* __restrict__ k, int64_t k_ts, int64_t k_hs,
                     const uint16_t* __restrict__ v, int64_t v_ts, int64_t v_hs,
@@ -122,9 +126,14 @@ kv_store_fp8_kernel(const uint16_t* __restrict__ k, int64_t k_ts, int64_t k_hs,
     a = fmaxf(a, __shfl_xor(a, 2, 16));
     a = fmaxf(a, __shfl_xor(a, 4, 16));
     a = fmaxf(a, __shfl_xor(a, 8, 16));
+    // a = 1.m * 2^E: a / 2^(E-8) = 1.m * 256 <= 448 iff 1.m <= 1.75, else
+    // 2^(E-7) is the smallest; exponent fields below 1 are raised to 1
+    const uint32_t ab = __float_as_uint(a);
+    const int ef = (int)(ab >> 23) - 8 + ((ab & 0x7fffffu) > 0x600000u ? 1 : 0);
+    const int e = ef < 1 ? 1 : ef;                                   // scale 2^(e - 127)
     const bool nz = a > 0.f;
-    const float inv = nz ? 448.f / a : 1.f;
-    const float sc = nz ? a / 448.f : 1.f;
+    const float sc = nz ? __uint_as_float((uint32_t)e << 23) : 1.f;
+    const float inv = nz ? __uint_as_float((uint32_t)(254 - e) << 23) : 1.f;  // 1 / sc, exact
     int lo = 0, hi = 0;
     lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[0] * inv, f[1] * inv, lo, false);
     lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[2] * inv, f[3] * inv, lo, true);

@@ -303,12 +303,28 @@ fp8_pages_widen_kernel(const uint8_t* __restrict__ k8, const uint8_t* __restrict
       const u32x4 x = ld16((which ? v8 : k8) + src);
       const float sc = (which ? vs : ks)[sidx];
       u32x4 o[2];
+      // A positive normal power-of-two scale (what pa_kv_store_fp8 writes):
+      // v_cvt_scalef32_pk_bf16_fp8 multiplies by 2^exponent(sc), so one
+      // conversion per pair gives code * sc exactly.  Any other scale:
+      // widen to float32, multiply, round to bf16 once.  The two agree
+      // wherever both apply.
+      const uint32_t sb = __float_as_uint(sc);
+      if ((sb & 0x807fffffu) == 0u && sb >= 0x00800000u && sb < 0x7f800000u) {
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], false);
-        const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], true);
-        o[w >> 1][2 * (w & 1)] = pack_bf16x2(lo[0] * sc, lo[1] * sc);
-        o[w >> 1][2 * (w & 1) + 1] = pack_bf16x2(hi[0] * sc, hi[1] * sc);
+        for (int w = 0; w < 4; ++w) {
+          o[w >> 1][2 * (w & 1)] =
+              __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[w], sc, false));
+          o[w >> 1][2 * (w & 1) + 1] =
+              __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[w], sc, true));
+        }
+      } else {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], false);
+          const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], true);
+          o[w >> 1][2 * (w & 1)] = pack_bf16x2(lo[0] * sc, lo[1] * sc);
+          o[w >> 1][2 * (w & 1) + 1] = pack_bf16x2(hi[0] * sc, hi[1] * sc);
+        }
       }
       uint16_t* d = (which ? wv : wk) + dst;
       st16(d, o[0]);
