@@ -217,9 +217,10 @@ int pa_qk_norm_rope_store(const uint16_t* q, int64_t q_tok_stride, int64_t q_hea
 /*
  * Quantising KV store for float8 pages: for every token t with a slot in the
  * pool and every kv head h, the row x = k[t, h] (bf16, d = 128) is stored as
- * e4m3fn codes e4m3(x * (448 / amax)) (round to nearest even) with scale
- * amax / 448 (amax = max |x|; an all-zero row stores scale 1), and likewise
- * v.  Code pools: (page, slot, head) byte strides as in pa_kv_store; scale
+ * e4m3fn codes e4m3(x / s) (round to nearest even) with scale s, the
+ * smallest power of two with amax / s <= 448 and s >= 2^-126 (amax = max |x|;
+ * an all-zero row stores scale 1), and likewise v.  Readers take any
+ * scales; power-of-two ones widen exactly in one conversion.  Code pools: (page, slot, head) byte strides as in pa_kv_store; scale
  * pools: float (page, slot, head) strides, e.g. the [Hkv, NB, BS] layout of
  * k_scales_pages (decode_paged_attention.py:206-217).  The reference reads
  * quantised pages but has no writer; this quantiser is the library's own.

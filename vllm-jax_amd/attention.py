@@ -208,8 +208,9 @@ def update_kv_cache_fp8(kv_codes: torch.Tensor, kv_scales: torch.Tensor, slot_ma
     pool ``[2, NB, BS, Hkv, d]`` of float8_e4m3fn codes and
     ``kv_scales`` ``[2, Hkv, NB, BS]`` float32 (index 0 = K, 1 = V; each half
     is the reference's ``k_scales_pages`` layout).  Each (token, kv head) row
-    is scaled by 448 / max|row| and rounded to e4m3 (round to nearest even);
-    the stored scale is max|row| / 448.  Slots outside the pool are skipped.
+    is divided by its scale s and rounded to e4m3 (round to nearest even); s
+    is the smallest power of two with max|row| / s <= 448 (at least 2^-126).
+    Slots outside the pool are skipped.
     Returns ``(kv_codes, kv_scales)``."""
     if kv_codes.dim() != 5 or kv_codes.shape[0] != 2 or kv_codes.dtype != torch.float8_e4m3fn:
         raise ValueError("kv_codes must be a [2, NB, BS, Hkv, d] float8_e4m3fn pool")
