@@ -236,6 +236,17 @@ int pa_kv_store_fp8(const uint16_t* k, int64_t k_tok_stride, int64_t k_head_stri
                     void* stream);
 
 /*
+ * Code types of 1-byte quantized pages (pa_decode_quant, pa_prefill_quant).
+ * The reference casts quantized pages of any dtype to q's dtype before the
+ * dot (decode_paged_attention.py:72-75, prefill_paged_attention.py:84-85):
+ * e4m3fn codes are their float8 values, int8 / uint8 codes the integers
+ * -128..127 / 0..255; all are exact in bf16.
+ */
+#define PA_CODE_E4M3 0
+#define PA_CODE_INT8 1
+#define PA_CODE_UINT8 2
+
+/*
  * pa_decode over float8 e4m3fn pages with per-token scales: the logit of
  * token j is (q . bf16(k_j)) * k_scales[j] * scale, and P is multiplied by
  * v_scales[j] before PV (decode_paged_attention.py:72-81,108-115, the
@@ -257,7 +268,28 @@ int pa_decode_fp8(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stri
                   uint16_t* out, int64_t out_batch_stride, int64_t out_head_stride,
                   void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace bytes pa_prefill_fp8 needs: room for two bf16 pages per
+/*
+ * pa_decode_fp8 for any code type (PA_CODE_*; pa_decode_fp8 is code_type
+ * PA_CODE_E4M3): k_j is the code's value, exact in bf16, and the logit and P
+ * scaling are the same.  Replaces the k_scales_pages / v_scales_pages path of
+ * decode_paged_attention (decode_paged_attention.py:72-81,108-115) for int8
+ * and uint8 pages as well.  An unknown code_type returns
+ * PA_ERR_INVALID_ARGUMENT before the device is touched.
+ */
+int pa_decode_quant(int32_t code_type, const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
+                    const uint8_t* k_cache, const uint8_t* v_cache,
+                    const float* k_scales, const float* v_scales,
+                    int32_t num_pages, int32_t page_size,
+                    int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                    int64_t scale_page_stride, int64_t scale_head_stride,
+                    const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                    const int32_t* lengths, int32_t batch,
+                    int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                    float scale, float soft_cap,
+                    uint16_t* out, int64_t out_batch_stride, int64_t out_head_stride,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes pa_prefill_fp8 / pa_prefill_quant need: room for two bf16 pages per
  * block-table entry (K and V), two int32 per entry and a count, then
  * pa_prefill's work list. */
 size_t pa_prefill_fp8_workspace_size(int32_t batch, int32_t pages_per_seq, int32_t page_size,
@@ -288,6 +320,29 @@ int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_strid
                    float scale, float soft_cap,
                    uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * pa_prefill_fp8 for any code type (PA_CODE_*; pa_prefill_fp8 is code_type
+ * PA_CODE_E4M3): pages are widened to bf16(code value * token scale) and the
+ * bf16 prefill runs on them.  Replaces the k_scales_pages / v_scales_pages
+ * path of prefill_paged_attention (prefill_paged_attention.py:84-92,118-123)
+ * for int8 and uint8 pages as well.  An unknown code_type returns
+ * PA_ERR_INVALID_ARGUMENT before the device is touched.
+ */
+int pa_prefill_quant(int32_t code_type, const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                     const uint8_t* k_cache, const uint8_t* v_cache,
+                     const float* k_scales, const float* v_scales,
+                     int32_t num_pages, int32_t page_size,
+                     int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                     int64_t scale_page_stride, int64_t scale_head_stride,
+                     const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                     const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                     const int32_t* input_positions,
+                     int32_t batch, int32_t num_tokens, int32_t max_seqlen_q,
+                     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                     float scale, float soft_cap,
+                     uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
+                     void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Workspace bytes pa_mixed needs (0 for bad sizes): decode partials when a

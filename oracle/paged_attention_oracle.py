@@ -249,7 +249,8 @@ def _merge_splits(o_parts, l_parts, m_parts):
 def prefill_attention(q, k_pages, v_pages, block_tables, cu_seqlens,
                       input_positions, *, cu_seqlens_k=None, k_splits=8,
                       pages_per_compute_block=8, soft_cap=None,
-                      mask_value=DEFAULT_MASK_VALUE, rows=None, k_scales_pages=None, v_scales_pages=None):
+                      mask_value=DEFAULT_MASK_VALUE, rows=None, k_scales_pages=None, v_scales_pages=None,
+                      code_type="e4m3"):
     """Ragged causal GQA paged prefill, restating the reference kernel.
 
     Layouts follow the reference kernel entry (prefill...:407-429):
@@ -282,8 +283,8 @@ def prefill_attention(q, k_pages, v_pages, block_tables, cu_seqlens,
     ``rows`` (optional int array) restricts the computation to those q rows
     (other rows of the result stay 0) so large workloads can be sampled.
     Quantized pages (prefill...:169-170,255-266, in-kernel :84-92,120-123):
-    float8 e4m3fn codes with ``[Hkv, NB, BS]`` float32 per-token scales, as in
-    decode_attention.
+    1-byte codes with ``[Hkv, NB, BS]`` float32 per-token scales, as in
+    decode_attention (``code_type``).
     Returns bf16 bit patterns ``[T, H, d]``.
     """
     qf = _as_f32(q)
@@ -332,8 +333,8 @@ def prefill_attention(q, k_pages, v_pages, block_tables, cu_seqlens,
         valid = (np.arange(p * bs)[None, :] < lk) & (kv_pos[None, :] <= q_pos[:, None])
         for kh in range(hkv):
             if quant:
-                k_ctx = fp8_e4m3_decode(kp[kh][safe[b]].reshape(p * bs, d))
-                v_ctx = fp8_e4m3_decode(vp[kh][safe[b]].reshape(p * bs, d))
+                k_ctx = code_values(kp[kh][safe[b]].reshape(p * bs, d), code_type)
+                v_ctx = code_values(vp[kh][safe[b]].reshape(p * bs, d), code_type)
                 k_sc = ksp[kh][safe[b]].reshape(p * bs)
                 v_sc = vsp[kh][safe[b]].reshape(p * bs)
             else:
@@ -357,7 +358,8 @@ def prefill_attention(q, k_pages, v_pages, block_tables, cu_seqlens,
 # ----------------------------------------------------------------------------
 def decode_attention(q, k_pages, v_pages, block_tables, lengths, *,
                      k_splits=None, pages_per_compute_block=8, soft_cap=None,
-                     mask_value=DEFAULT_MASK_VALUE, seqs=None, k_scales_pages=None, v_scales_pages=None):
+                     mask_value=DEFAULT_MASK_VALUE, seqs=None, k_scales_pages=None, v_scales_pages=None,
+                     code_type="e4m3"):
     """Split-K paged GQA decode, restating the reference kernel.
 
     q ``[B, H, d]`` is used as given -- the reference kernel applies no scale;
@@ -369,9 +371,11 @@ def decode_attention(q, k_pages, v_pages, block_tables, lengths, *,
 
     ``seqs`` (optional) restricts the computation to those sequences.
     Quantized pages (decode...:158-159,206-217): ``k_pages`` / ``v_pages``
-    hold float8 e4m3fn codes (uint8) and ``k_scales_pages`` /
-    ``v_scales_pages`` ``[Hkv, NB, BS]`` float32 per-token scales; K is cast to
-    bf16 exactly (decode...:72-74).
+    hold 1-byte codes -- ``code_type`` "e4m3" (float8 e4m3fn bit patterns),
+    "int8" or "uint8" (integers; the reference's ``astype`` to q's dtype
+    keeps the integer value) -- and ``k_scales_pages`` / ``v_scales_pages``
+    ``[Hkv, NB, BS]`` float32 per-token scales; K is cast to bf16 exactly
+    (decode...:72-74), V to float32 (decode...:108-115).
     Returns bf16 bit patterns ``[B, H, d]``.
     """
     qf = round_bf16(_as_f32(q))
@@ -405,8 +409,8 @@ def decode_attention(q, k_pages, v_pages, block_tables, lengths, *,
             if ln <= 0:
                 continue
             if quant:
-                k_ctx = fp8_e4m3_decode(kp[kh][safe[b]].reshape(p * bs, d))
-                v_ctx = fp8_e4m3_decode(vp[kh][safe[b]].reshape(p * bs, d))
+                k_ctx = code_values(kp[kh][safe[b]].reshape(p * bs, d), code_type)
+                v_ctx = code_values(vp[kh][safe[b]].reshape(p * bs, d), code_type)
                 k_sc = ksp[kh][safe[b]].reshape(p * bs)
                 v_sc = vsp[kh][safe[b]].reshape(p * bs)
             else:
@@ -654,6 +658,21 @@ E4M3_MAX = 448.0
 def fp8_e4m3_decode(codes) -> np.ndarray:
     """uint8 e4m3fn codes -> float32 values (exact)."""
     return _E4M3[np.asarray(codes, dtype=np.uint8)]
+
+
+def code_values(codes, code_type="e4m3") -> np.ndarray:
+    """Values of 1-byte page codes as the reference's cast sees them
+    (decode...:72-75,108-115; prefill...:84-85,118-123): "e4m3" float8
+    e4m3fn bit patterns, "int8" / "uint8" the integers (codes may be given
+    as int8 or as their uint8 bit patterns); exact in float32 and bf16."""
+    c = np.asarray(codes)
+    if code_type == "e4m3":
+        return fp8_e4m3_decode(c.view(np.uint8) if c.dtype == np.int8 else c)
+    if code_type == "int8":
+        return (c if c.dtype == np.int8 else c.astype(np.uint8).view(np.int8)).astype(np.float32)
+    if code_type == "uint8":
+        return (c.view(np.uint8) if c.dtype == np.int8 else c.astype(np.uint8)).astype(np.float32)
+    raise ValueError(f"unknown code_type {code_type!r}")
 
 
 def fp8_e4m3_encode(x) -> np.ndarray:

@@ -54,7 +54,7 @@ def test_phase_timestamp_build_exports_its_readers():
 
 def test_error_codes_match_header():
     text = open(HEADER).read()
-    codes = dict(re.findall(r"#define (PA_\w+) \(?(-?\d+)\)?", text))
+    codes = dict(re.findall(r"#define (PA_(?:OK|ERR_\w+)) \(?(-?\d+)\)?", text))
     assert codes == {"PA_OK": "0", "PA_ERR_INVALID_ARGUMENT": "-1", "PA_ERR_UNSUPPORTED": "-2",
                      "PA_ERR_WORKSPACE": "-3", "PA_ERR_LAUNCH": "-4"}
 
@@ -104,6 +104,28 @@ def test_decode_noalloc_refuses_oversized_launch_without_a_device():
     assert rc == -3
     msg = lib.pa_last_error().decode()
     assert "more than the 67108864 bytes" in msg and str(need) in msg, msg
+
+
+def test_quant_entries_reject_unknown_code_types_without_a_device():
+    """pa_decode_quant / pa_prefill_quant take PA_CODE_E4M3 (0), PA_CODE_INT8
+    (1) or PA_CODE_UINT8 (2); any other code type is refused before the
+    device is touched (null pointers here)."""
+    lib = PKG._lib.load()
+    text = open(HEADER).read()
+    assert dict(re.findall(r"#define (PA_CODE_\w+) (\d+)", text)) == {"PA_CODE_E4M3": "0", "PA_CODE_INT8": "1",
+                                                                    "PA_CODE_UINT8": "2"}
+    d = [None, 128 * 32, 128, None, None, None, None, 16, 256, 256 * 8 * 128, 8 * 128, 128, 256 * 8, 256,
+         None, 4, 4, None, 2, 32, 8, 128, 1.0, 0.0, None, 128 * 32, 128, None, 0, None]
+    for code in (3, -1, 7):
+        assert lib.pa_decode_quant(code, *d) == -1
+        assert "code_type" in lib.pa_last_error().decode()
+    p = [None, 2048, 128, None, None, None, None, 16, 256, 256 * 8 * 128, 8 * 128, 128, 256 * 8, 256,
+         None, 4, 4, None, None, None, 2, 100, 64, 16, 8, 128, 0.088, 0.0, None, 2048, 128, None, 0, None]
+    assert lib.pa_prefill_quant(5, *p) == -1
+    assert "code_type" in lib.pa_last_error().decode()
+    # a valid code type gets as far as the null pointers
+    assert lib.pa_decode_quant(1, *d) == -1
+    assert "null pointer" in lib.pa_last_error().decode()
 
 
 def test_prefill_rejects_bad_arguments_without_a_device():

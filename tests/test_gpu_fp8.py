@@ -331,3 +331,92 @@ def test_prefill_fp8_equals_bf16_prefill_over_widened_pages(pkg, dev, scale_mult
           f"max-abs err vs oracle {err:.3e}", flush=True)
     assert same
     assert err <= TOL
+
+
+def _int_pool(rng, nb, bs, hkv, kind):
+    """Integer codes ([NB, BS, Hkv, d], int8 or uint8) with [Hkv, NB, BS]
+    per-token scales that keep code * scale around 0.5 * N(0, 1)'s range."""
+    lo, hi, dt = (-128, 128, np.int8) if kind == "int8" else (0, 256, np.uint8)
+    kq = rng.integers(lo, hi, (nb, bs, hkv, 128)).astype(dt)
+    vq = rng.integers(lo, hi, (nb, bs, hkv, 128)).astype(dt)
+    ks = (rng.uniform(0.5, 1.5, (hkv, nb, bs)) / 128).astype(np.float32)
+    vs = (rng.uniform(0.5, 1.5, (hkv, nb, bs)) / 256).astype(np.float32)
+    return kq, vq, ks, vs
+
+
+def _tables_for(rng, kv_lens, bs, nb, pow2_width=False):
+    pages = [(int(n) + bs - 1) // bs for n in kv_lens]
+    width = max(1, max(pages))
+    if pow2_width:
+        width = 1 << (width - 1).bit_length()
+    perm = rng.permutation(nb)
+    bt = np.full((len(kv_lens), width), -1, np.int32)
+    c = 0
+    for b, p in enumerate(pages):
+        bt[b, :p] = perm[c:c + p]
+        c += p
+    return bt
+
+
+@pytest.mark.parametrize("kind", ["int8", "uint8"])
+@pytest.mark.parametrize("lens,h,hkv,bs,cap", [
+    ([1, 15, 300, 0, 2049], 32, 8, 256, None),     # Qwen3-8B heads, two chunks, length 0
+    ([70, 500], 16, 16, 32, 30.0),                 # MHA, soft cap
+    ([17, 1100, 2050], 32, 1, 16, None),           # G = 32 (two q-head blocks), 16-token pages
+])
+def test_decode_integer_pages_match_oracle(pkg, dev, kind, lens, h, hkv, bs, cap):
+    """Decode over int8 / uint8 pages with per-token scales: the reference
+    casts the codes to q's dtype as integers (decode_paged_attention.py:
+    72-75,108-115); every sequence against the oracle."""
+    import torch
+    rng = np.random.default_rng(sum(lens) + h + (7 if kind == "int8" else 0))
+    nb = sum((n + bs - 1) // bs for n in lens) + 2
+    kq, vq, ks, vs = _int_pool(rng, nb, bs, hkv, kind)
+    bt = _tables_for(rng, lens, bs, nb, pow2_width=True)
+    q = _bf16(rng, (len(lens), h, 128))
+    out = pkg.decode_paged_attention(from_u16(q, dev), torch.from_numpy(kq).to(dev).permute(2, 0, 1, 3),
+                                     torch.from_numpy(vq).to(dev).permute(2, 0, 1, 3),
+                                     torch.as_tensor(bt, device=dev), torch.as_tensor(np.asarray(lens, np.int32),
+                                                                                    device=dev),
+                                     k_scales_pages=torch.from_numpy(ks).to(dev),
+                                     v_scales_pages=torch.from_numpy(vs).to(dev), attn_logits_soft_cap=cap)
+    torch.cuda.synchronize()
+    got = u16(out)
+    want = ora.decode_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, np.asarray(lens),
+                                soft_cap=cap, k_scales_pages=ks, v_scales_pages=vs, code_type=kind)
+    err = np.abs(ora.bf16_to_f32(got) - ora.bf16_to_f32(want)).max()
+    print(f"{kind} decode max-abs err {err:.3e}", flush=True)
+    assert err <= TOL
+    assert not got[np.asarray(lens) == 0].any()
+
+
+@pytest.mark.parametrize("kind", ["int8", "uint8"])
+@pytest.mark.parametrize("lens,prefix,h,hkv,bs", [
+    ([17, 128, 300, 511], [0, 0, 0, 0], 16, 8, 256),   # the Qwen3-0.6B single-layer prefill
+    ([5, 40, 130], [0, 20, 300], 32, 8, 16),            # cached prefixes, small pages
+])
+def test_prefill_integer_pages_match_oracle(pkg, dev, kind, lens, prefix, h, hkv, bs):
+    """Prefill over int8 / uint8 pages with per-token scales (the pages
+    widened once to bf16(integer * scale)) against the oracle, every row."""
+    import torch
+    rng = np.random.default_rng(sum(lens) + h + (5 if kind == "int8" else 0))
+    kv = [p + n for p, n in zip(prefix, lens)]
+    nb = sum((n + bs - 1) // bs for n in kv) + 2
+    kq, vq, ks, vs = _int_pool(rng, nb, bs, hkv, kind)
+    bt = _tables_for(rng, kv, bs, nb)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cuk = np.concatenate([[0], np.cumsum(kv)]).astype(np.int32)
+    pos = np.concatenate([np.arange(p, p + n) for p, n in zip(prefix, lens)]).astype(np.int32)
+    q = _bf16(rng, (int(cu[-1]), h, 128))
+    i32 = lambda x: torch.as_tensor(np.ascontiguousarray(x, dtype=np.int32), device=dev)
+    out = pkg.prefill_paged_attention(from_u16(q, dev), torch.from_numpy(kq).to(dev).permute(2, 0, 1, 3),
+                                      torch.from_numpy(vq).to(dev).permute(2, 0, 1, 3), i32(bt), i32(cu), None,
+                                      i32(pos), max_seqlen_bucket=max(lens), cu_seqlens_k=i32(cuk),
+                                      k_scales_pages=torch.from_numpy(ks).to(dev),
+                                      v_scales_pages=torch.from_numpy(vs).to(dev))
+    torch.cuda.synchronize()
+    want = ora.prefill_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, cu, pos,
+                                 cu_seqlens_k=cuk, k_scales_pages=ks, v_scales_pages=vs, code_type=kind)
+    err = np.abs(ora.bf16_to_f32(u16(out)) - ora.bf16_to_f32(want)).max()
+    print(f"{kind} prefill max-abs err {err:.3e}", flush=True)
+    assert err <= TOL

@@ -77,7 +77,7 @@ def test_decode_shape_errors_match_reference():
         PKG.decode_paged_attention(*a, k_scales_pages=torch.zeros(1))
     hkv, nb, bs = a[1].shape[:3]
     sc = torch.ones(hkv, nb, bs)
-    with pytest.raises(NotImplementedError, match="float8_e4m3fn"):        # bf16 pages with scales
+    with pytest.raises(NotImplementedError, match="float8_e4m3fn, int8 or uint8"):   # bf16 pages with scales
         PKG.decode_paged_attention(*a, k_scales_pages=sc, v_scales_pages=sc)
     with pytest.raises(ValueError, match="k_scales_pages must have shape"):
         PKG.decode_paged_attention(*a, k_scales_pages=sc[:, :1], v_scales_pages=sc)
@@ -126,23 +126,42 @@ def test_check_slot_mapping_finds_duplicates():
 
 
 @pytest.mark.parametrize("dtype", [torch.uint8, torch.int8])
-def test_integer_pages_are_refused_not_read_as_float8(dtype):
+def test_integer_pages_pass_the_dtype_check(dtype):
     """The reference casts quantized pages of any dtype to q's dtype
     (decode_paged_attention.py:72-75,108-115; prefill_paged_attention.py:
-    84-85,118-123), so uint8 / int8 pages mean integer values.  The entries
-    take float8_e4m3fn codes only and refuse integer pages before any device
-    work, instead of reading their bytes as e4m3 codes."""
+    84-85,118-123), so uint8 / int8 pages mean integer values: the entries
+    take them as such (code types PA_CODE_UINT8 / PA_CODE_INT8), and these
+    host tensors then stop at the device check.  The library's own quantising
+    store writes float8 codes only."""
+    from vllm_jax_amd.kernels._common import _CODE_TYPES
     q, kp, _, bt, lens = _decode_args()
     hkv, nb, bs, d = kp.shape
     pages = torch.zeros(hkv, nb, bs, d, dtype=dtype)
     sc = torch.ones(hkv, nb, bs)
-    with pytest.raises(NotImplementedError, match="must be float8_e4m3fn"):
+    assert _CODE_TYPES[dtype] == (PKG._lib.PA_CODE_INT8 if dtype == torch.int8 else PKG._lib.PA_CODE_UINT8)
+    with pytest.raises(ValueError, match="HIP device"):
         PKG.decode_paged_attention(q, pages, pages, bt, lens, k_scales_pages=sc, v_scales_pages=sc)
     a = _prefill_args(hkv=hkv, nb=nb, bs=bs)
-    with pytest.raises(NotImplementedError, match="must be float8_e4m3fn"):
+    with pytest.raises(ValueError, match="HIP device"):
         PKG.prefill_paged_attention(a[0], pages, pages, *a[3:], max_seqlen_bucket=8,
                                     k_scales_pages=sc, v_scales_pages=sc)
     with pytest.raises(ValueError, match="float8_e4m3fn pool"):
         PKG.update_kv_cache_fp8(torch.zeros(2, nb, bs, hkv, d, dtype=dtype), torch.ones(2, hkv, nb, bs),
                                 torch.zeros(5, dtype=torch.int32), torch.zeros(5, hkv, d, dtype=torch.bfloat16),
                                 torch.zeros(5, hkv, d, dtype=torch.bfloat16))
+
+
+def test_other_quantized_page_dtypes_are_refused():
+    """Pages with scales must be 1-byte codes (float8_e4m3fn, int8, uint8);
+    K and V of one dtype."""
+    from vllm_jax_amd.kernels._common import check_quantized_pages
+    q, kp, _, bt, lens = _decode_args()
+    hkv, nb, bs, d = kp.shape
+    sc = torch.ones(hkv, nb, bs)
+    for dt in (torch.float16, torch.bfloat16, torch.int16):
+        pages = torch.zeros(hkv, nb, bs, d, dtype=dt)
+        with pytest.raises(NotImplementedError, match="float8_e4m3fn, int8 or uint8"):
+            check_quantized_pages(pages, pages, sc, sc)
+    with pytest.raises(ValueError, match="same dtype"):
+        check_quantized_pages(torch.zeros(hkv, nb, bs, d, dtype=torch.int8),
+                              torch.zeros(hkv, nb, bs, d, dtype=torch.uint8), sc, sc)

@@ -569,3 +569,81 @@ def test_prefill_fp8_vs_brute_force():
                 w = np.exp(lg - lg.max())
                 want[row, hh] = (w / w.sum()) @ vctx[vis, hh // 4]
     assert np.abs(got - want).max() <= BRUTE_TOL
+
+
+# ---------------------------------------------------------------------------
+# integer pages (int8 / uint8 codes): the reference's astype keeps the integer
+# ---------------------------------------------------------------------------
+def test_code_values_follow_the_reference_cast():
+    """int8 / uint8 codes are the integers (jnp.astype of an integer page to
+    bf16 or float32, decode...:72-75,108-115), e4m3 codes their float8 value;
+    either integer kind may come as its uint8 bit pattern."""
+    raw = np.arange(256, dtype=np.uint8)
+    assert np.array_equal(ora.code_values(raw, "uint8"), np.arange(256, dtype=np.float32))
+    assert np.array_equal(ora.code_values(raw, "int8"), raw.view(np.int8).astype(np.float32))
+    assert np.array_equal(ora.code_values(raw.view(np.int8), "int8"), ora.code_values(raw, "int8"))
+    assert ora.code_values(np.array([0x80, 0x7F, 0xFF], np.uint8), "int8").tolist() == [-128.0, 127.0, -1.0]
+    fin = np.isfinite(ora.fp8_e4m3_decode(raw))
+    assert np.array_equal(ora.code_values(raw, "e4m3")[fin], ora.fp8_e4m3_decode(raw)[fin])
+    # every integer code is exact in bf16
+    for kind in ("int8", "uint8"):
+        v = ora.code_values(raw, kind)
+        assert np.array_equal(ora.bf16_to_f32(ora.f32_to_bf16(v)), v)
+
+
+@pytest.mark.parametrize("kind", ["int8", "uint8"])
+def test_integer_pages_vs_brute_force(kind):
+    """Decode and prefill over integer codes with per-token scales == float64
+    attention over code * scale (K and V), within the oracle's bf16 bar."""
+    rng = np.random.default_rng(31 if kind == "int8" else 32)
+    lens, h, hkv, bs = [5, 40, 0, 33], 8, 2, 16
+    nb = int(sum(-(-n // bs) for n in lens)) + 1
+    lo, hi = (-128, 128) if kind == "int8" else (0, 256)
+    dt = np.int8 if kind == "int8" else np.uint8
+    kq = rng.integers(lo, hi, (nb, bs, hkv, 128)).astype(dt)
+    vq = rng.integers(lo, hi, (nb, bs, hkv, 128)).astype(dt)
+    ks = (rng.uniform(0.5, 1.5, (nb, bs, hkv)) / 256).astype(np.float32)
+    vs = (rng.uniform(0.5, 1.5, (nb, bs, hkv)) / 256).astype(np.float32)
+    bt = _tables(rng, lens, bs, nb)
+    bt = np.concatenate([bt, np.full((len(lens), 4 - bt.shape[1]), -1, np.int32)], axis=1)
+    q = _bf16(rng, (len(lens), h, 128))
+    got = ora.bf16_to_f32(ora.decode_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, lens,
+                                               k_scales_pages=ks.transpose(2, 0, 1),
+                                               v_scales_pages=vs.transpose(2, 0, 1), code_type=kind))
+    kd64 = kq.astype(np.float64) * ks[..., None]
+    vd64 = vq.astype(np.float64) * vs[..., None]
+    want = np.zeros_like(got, dtype=np.float64)
+    for b, n in enumerate(lens):
+        if n == 0:
+            continue
+        pages = bt[b, :(n + bs - 1) // bs]
+        kc = kd64[pages].reshape(-1, hkv, 128)[:n]
+        vc = vd64[pages].reshape(-1, hkv, 128)[:n]
+        for hh in range(h):
+            kh = hh // (h // hkv)
+            lg = kc[:, kh] @ ora.bf16_to_f32(q[b, hh]).astype(np.float64)
+            w = np.exp(lg - lg.max())
+            want[b, hh] = (w / w.sum()) @ vc[:, kh]
+    assert np.abs(got - want).max() <= BRUTE_TOL
+    assert not got[2].any()
+    # prefill over the same pool, one sequence with a cached prefix
+    cu = np.array([0, 12], np.int32)
+    cuk = np.array([0, 40], np.int32)
+    pos = np.arange(28, 40, dtype=np.int32)
+    qp = _bf16(rng, (12, h, 128))
+    btp = bt[1:2]
+    gp = ora.bf16_to_f32(ora.prefill_attention(qp, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), btp, cu, pos,
+                                               cu_seqlens_k=cuk, k_scales_pages=ks.transpose(2, 0, 1),
+                                               v_scales_pages=vs.transpose(2, 0, 1), code_type=kind))
+    sc = float(ora.round_bf16(np.float32(1 / math.sqrt(128))).reshape(-1)[0])
+    qs = ora.bf16_to_f32(ora.f32_to_bf16(ora.round_bf16(ora.bf16_to_f32(qp) * np.float32(sc)))).astype(np.float64)
+    kctx = kd64[btp[0, :3]].reshape(-1, hkv, 128)[:40]
+    vctx = vd64[btp[0, :3]].reshape(-1, hkv, 128)[:40]
+    wantp = np.zeros_like(gp, dtype=np.float64)
+    for i in range(12):
+        vis = np.arange(40) <= pos[i]
+        for hh in range(h):
+            lg = kctx[vis, hh // 4] @ qs[i, hh]
+            w = np.exp(lg - lg.max())
+            wantp[i, hh] = (w / w.sum()) @ vctx[vis, hh // 4]
+    assert np.abs(gp - wantp).max() <= BRUTE_TOL

@@ -160,6 +160,11 @@ SIGNATURES = {
         c_vp, c_sz, c_vp,              # workspace, bytes, stream
     ]),
 }
+# pa_decode_quant / pa_prefill_quant: a code_type (PA_CODE_*) before the
+# arguments of pa_decode_fp8 / pa_prefill_fp8
+SIGNATURES["pa_decode_quant"] = (ctypes.c_int, [c_i32] + SIGNATURES["pa_decode_fp8"][1])
+SIGNATURES["pa_prefill_quant"] = (ctypes.c_int, [c_i32] + SIGNATURES["pa_prefill_fp8"][1])
+PA_CODE_E4M3, PA_CODE_INT8, PA_CODE_UINT8 = 0, 1, 2
 
 
 class PagedAttentionError(RuntimeError):

@@ -53,7 +53,7 @@ decode_plan_kernel(DecodeParams p, int32_t* __restrict__ plan) {
   if (tid == 0) plan[0] = count;
 }
 
-template <bool kAligned, bool kSoftCap, bool kFp8 = false, bool kShared = false>
+template <bool kAligned, bool kSoftCap, bool kFp8 = false, bool kShared = false, int kCode = kCodeE4M3>
 __global__ void __launch_bounds__(256, 2)
 decode_split_kernel(DecodeParams p) {
   __shared__ DecodeLds red;
@@ -75,8 +75,8 @@ decode_split_kernel(DecodeParams p) {
   } else {
     item = xcd_grouped_item(blockIdx.x, gridDim.x);
   }
-  decode_item<kDecodeWaves, kAligned, kSoftCap, kFp8, kShared>(p, item, &red.o[0][0][0], &red.m[0][0],
-                                                               &red.l[0][0]);
+  decode_item<kDecodeWaves, kAligned, kSoftCap, kFp8, kShared, kCode>(p, item, &red.o[0][0][0], &red.m[0][0],
+                                                                      &red.l[0][0]);
 }
 
 // One wave per (sequence, q head): out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M).
@@ -185,13 +185,26 @@ extern "C" size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int
 
 // Shared argument checks and launch of pa_decode / pa_decode_fp8.  `prm`
 // arrives with the cache pointers (and scales) set; the rest is filled here.
+// Launch of the split kernel over 1-byte codes of type `code` (kCodeE4M3,
+// kCodeI8, kCodeU8).
+template <int kCode>
+static void launch_decode_codes(const DecodeParams& prm, bool cap, bool shared, dim3 grid, dim3 block,
+                                hipStream_t s) {
+  if (!cap && shared) decode_split_kernel<true, false, true, true, kCode><<<grid, block, 0, s>>>(prm);
+  else if (!cap) decode_split_kernel<true, false, true, false, kCode><<<grid, block, 0, s>>>(prm);
+  else decode_split_kernel<true, true, true, false, kCode><<<grid, block, 0, s>>>(prm);
+}
+
 static int decode_common(const char* name, DecodeParams& prm, bool fp8, const uint16_t* q, int64_t q_batch_stride,
                          int64_t q_head_stride, int32_t num_pages, int32_t page_size, int64_t page_stride,
                          int64_t slot_stride, int64_t head_stride, const int32_t* block_tables, int64_t bt_stride,
                          int32_t pages_per_seq, const int32_t* lengths, int32_t batch, int32_t num_heads,
                          int32_t num_kv_heads, int32_t head_dim, float scale, float soft_cap, uint16_t* out,
                          int64_t out_batch_stride, int64_t out_head_stride, void* workspace, size_t workspace_bytes,
-                         void* stream) {
+                         void* stream, int code = kCodeE4M3) {
+  if (fp8 && code != kCodeE4M3 && code != kCodeI8 && code != kCodeU8)
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: code_type %d is not one of PA_CODE_E4M3 (0), PA_CODE_INT8 (1), "
+                "PA_CODE_UINT8 (2)", name, code);
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_pages <= 0 || page_size <= 0 ||
       pages_per_seq < 0)
     return fail(PA_ERR_INVALID_ARGUMENT,
@@ -205,10 +218,10 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
   const bool any_d = head_dim != kHeadDim && !fp8 && any_head_dim(head_dim);
   if (head_dim != kHeadDim && !any_d)
     return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported (%s)", name, head_dim,
-                fp8 ? "float8 pages: only 128" : "128, or a multiple of 16 from 16 to 256");
+                fp8 ? "quantized pages: only 128" : "128, or a multiple of 16 from 16 to 256");
   const int group = num_heads / num_kv_heads;
   if (fp8 && page_size % kDecodeStep != 0)
-    return fail(PA_ERR_UNSUPPORTED, "%s: float8 pages need page_size %% %d == 0 (got %d)", name, kDecodeStep,
+    return fail(PA_ERR_UNSUPPORTED, "%s: quantized pages need page_size %% %d == 0 (got %d)", name, kDecodeStep,
                 page_size);
   if (batch == 0) return PA_OK;
   if (num_kv_heads == 1) {  // a size-1 dimension's stride is arbitrary (and never used)
@@ -288,9 +301,9 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
     // more than 16 q heads per kv head: several items read each kv head's
     // K/V, so the loads stay cacheable (the soft cap keeps the streaming form)
     const bool shared = prm.hblocks > 1;
-    if (fp8 && !cap && shared) decode_split_kernel<true, false, true, true><<<grid, block, 0, s>>>(prm);
-    else if (fp8 && !cap) decode_split_kernel<true, false, true><<<grid, block, 0, s>>>(prm);
-    else if (fp8) decode_split_kernel<true, true, true><<<grid, block, 0, s>>>(prm);
+    if (fp8 && code == kCodeI8) launch_decode_codes<kCodeI8>(prm, cap, shared, grid, block, s);
+    else if (fp8 && code == kCodeU8) launch_decode_codes<kCodeU8>(prm, cap, shared, grid, block, s);
+    else if (fp8) launch_decode_codes<kCodeE4M3>(prm, cap, shared, grid, block, s);
     else if (aligned && !cap && shared) decode_split_kernel<true, false, false, true><<<grid, block, 0, s>>>(prm);
     else if (aligned && !cap) decode_split_kernel<true, false><<<grid, block, 0, s>>>(prm);
     else if (aligned) decode_split_kernel<true, true><<<grid, block, 0, s>>>(prm);
@@ -354,6 +367,31 @@ extern "C" int pa_decode_noalloc(const uint16_t* q, int64_t q_batch_stride, int6
                        ws ? kNoAllocScratchBytes : 0, stream);
 }
 
+extern "C" int pa_decode_quant(int32_t code_type, const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
+                               const uint8_t* k_cache, const uint8_t* v_cache,
+                               const float* k_scales, const float* v_scales,
+                               int32_t num_pages, int32_t page_size,
+                               int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                               int64_t scale_page_stride, int64_t scale_head_stride,
+                               const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                               const int32_t* lengths, int32_t batch,
+                               int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                               float scale, float soft_cap,
+                               uint16_t* out, int64_t out_batch_stride, int64_t out_head_stride,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  DecodeParams prm{};
+  prm.k8 = k_cache;
+  prm.v8 = v_cache;
+  prm.k_scales = k_scales;
+  prm.v_scales = v_scales;
+  prm.sc_page_stride = scale_page_stride;
+  prm.sc_head_stride = scale_head_stride;
+  return decode_common("pa_decode_quant", prm, true, q, q_batch_stride, q_head_stride, num_pages, page_size,
+                       page_stride, slot_stride, head_stride, block_tables, bt_stride, pages_per_seq, lengths, batch,
+                       num_heads, num_kv_heads, head_dim, scale, soft_cap, out, out_batch_stride, out_head_stride,
+                       workspace, workspace_bytes, stream, code_type);
+}
+
 extern "C" int pa_decode_fp8(const uint16_t* q, int64_t q_batch_stride, int64_t q_head_stride,
                              const uint8_t* k_cache, const uint8_t* v_cache,
                              const float* k_scales, const float* v_scales,
@@ -376,5 +414,5 @@ extern "C" int pa_decode_fp8(const uint16_t* q, int64_t q_batch_stride, int64_t 
   return decode_common("pa_decode_fp8", prm, true, q, q_batch_stride, q_head_stride, num_pages, page_size,
                        page_stride, slot_stride, head_stride, block_tables, bt_stride, pages_per_seq, lengths, batch,
                        num_heads, num_kv_heads, head_dim, scale, soft_cap, out, out_batch_stride, out_head_stride,
-                       workspace, workspace_bytes, stream);
+                       workspace, workspace_bytes, stream, kCodeE4M3);
 }

@@ -167,11 +167,12 @@ __host__ __device__ inline int decode_chunk_tokens(int page_size) { return page_
 // red_m / red_l are LDS arrays of [kWaves][16][d] and [kWaves][16] floats.
 // kAligned: page_size % 16 == 0, so a 16-token step never crosses a page and
 // the chunk's page ids (at most 64) are read once, one per lane.
-// kFp8: K/V pages hold float8 e4m3 codes with per-token scales
-// (decode_paged_attention.py:72-81,108-115): K is widened to bf16 exactly
-// and its logits multiplied by the token's K scale; P is multiplied by the
-// token's V scale before PV.  Half the K/V bytes of the bf16 path.
-template <int kWaves, bool kAligned, bool kSoftCap, bool kFp8 = false, bool kShared = false>
+// kFp8: K/V pages hold 1-byte codes with per-token scales
+// (decode_paged_attention.py:72-81,108-115), float8 e4m3 or integers by
+// kCode: K is widened to bf16 exactly and its logits multiplied by the
+// token's K scale; P is multiplied by the token's V scale before PV.  Half
+// the K/V bytes of the bf16 path.
+template <int kWaves, bool kAligned, bool kSoftCap, bool kFp8 = false, bool kShared = false, int kCode = kCodeE4M3>
 __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, float* red_o, float* red_m,
                                             float* red_l) {
   static_assert(kWaves == 4 || kWaves == 8, "the combine splits d over the waves");
@@ -359,7 +360,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           const u32x4& w = kr[s >> 1];
-          const u32x4 kk = fp8x8_to_bf16x8((s & 1) ? u32x2{w[2], w[3]} : u32x2{w[0], w[1]});
+          const u32x4 kk = codes8_to_bf16x8<kCode>((s & 1) ? u32x2{w[2], w[3]} : u32x2{w[0], w[1]});
           sc = mfma16(as_bf16x8(kk), qt[s], sc);
         }
       } else {
@@ -418,7 +419,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
     u32x4 vd[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      if constexpr (kFp8) vd[i] = fp8x8_to_bf16x8(vdr[i]);
+      if constexpr (kFp8) vd[i] = codes8_to_bf16x8<kCode>(vdr[i]);
       else vd[i] = vdr[i];
     }
     // V^T tile j: lane (n, g) supplies d = 8n + j of tokens 4g .. 4g+3

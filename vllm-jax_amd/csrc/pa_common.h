@@ -83,6 +83,37 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
+// Codes of 1-byte quantized pages (the code_type argument of pa_decode_quant
+// and pa_prefill_quant): OCP float8 e4m3fn, or integers.  The reference casts
+// pages of any dtype to q's dtype before the dot (decode_paged_attention.py:
+// 72-75, prefill_paged_attention.py:84-85), so int8 / uint8 codes are the
+// integers -128..127 / 0..255, exact in bf16.
+constexpr int kCodeE4M3 = 0;
+constexpr int kCodeI8 = 1;
+constexpr int kCodeU8 = 2;
+
+// Eight 1-byte codes (one u32x2, byte 0 first) to eight bf16 (one u32x4), in
+// order, exactly.  Integers: v_cvt_f32_ubyte per byte (int8 flips the sign
+// bit first, so the byte reads code + 128, then subtracts 128), two per pack.
+template <int kCode>
+__device__ __forceinline__ u32x4 codes8_to_bf16x8(const u32x2& c) {
+  if constexpr (kCode == kCodeE4M3) {
+    return fp8x8_to_bf16x8(c);
+  } else {
+    u32x4 r;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t w = kCode == kCodeI8 ? c[i] ^ 0x80808080u : c[i];
+      const float bias = kCode == kCodeI8 ? 128.f : 0.f;
+      const float f0 = (float)(w & 0xffu) - bias, f1 = (float)((w >> 8) & 0xffu) - bias;
+      const float f2 = (float)((w >> 16) & 0xffu) - bias, f3 = (float)(w >> 24) - bias;
+      r[2 * i] = pack_bf16x2(f0, f1);
+      r[2 * i + 1] = pack_bf16x2(f2, f3);
+    }
+    return r;
+  }
+}
+
 // Value of `x` in lane l^32 / l^16 combined with the own value.  permlane
 // swaps exchange halves of two registers; passing the same register twice
 // yields (own, partner) in some order in every lane.

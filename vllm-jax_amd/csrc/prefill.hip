@@ -180,11 +180,12 @@ prefill_prep_kernel(PrefillParams p, int32_t* __restrict__ plan) {
   }
 }
 
-// Float8 pages for the prefill.  A block-table entry (b, lp) is in use when
-// lp * page_size < the sequence's kv length.  Every distinct physical page
-// in use is widened once into a compact bf16 pool (slot i of the pool holds
-// the i-th distinct page), each element bf16(code * scale of its token), one
-// rounding; the remapped table points there (-1 for unused entries, which
+// Quantized pages for the prefill (float8 e4m3 or integer codes).  A
+// block-table entry (b, lp) is in use when lp * page_size < the sequence's
+// kv length.  Every distinct physical page in use is widened once into a
+// compact bf16 pool (slot i of the pool holds the i-th distinct page), each
+// element bf16(code value * scale of its token), one rounding (exact for an
+// e4m3 code with a power-of-two scale); the remapped table points there (-1 for unused entries, which
 // the prefill never reads).  Pages shared between sequences (cached
 // prefixes) are widened once.
 //
@@ -281,7 +282,8 @@ fp8_pages_widen_kernel(const uint8_t* __restrict__ k8, const uint8_t* __restrict
                        int64_t sc_page_stride, int64_t sc_head_stride, const int32_t* __restrict__ bt,
                        int64_t bt_stride, int32_t pages_per_seq, const int32_t* __restrict__ cu_q,
                        const int32_t* __restrict__ cu_k, int32_t num_kv_heads, const int32_t* __restrict__ owner,
-                       const int32_t* __restrict__ count, uint16_t* __restrict__ wk, uint16_t* __restrict__ wv) {
+                       const int32_t* __restrict__ count, uint16_t* __restrict__ wk, uint16_t* __restrict__ wv,
+                       int32_t code) {
   const int32_t sl = blockIdx.x / kWidenSplit;
   const int part_w = blockIdx.x - sl * kWidenSplit;
   if (sl >= *count) return;
@@ -309,7 +311,19 @@ fp8_pages_widen_kernel(const uint8_t* __restrict__ k8, const uint8_t* __restrict
       // widen to float32, multiply, round to bf16 once.  The two agree
       // wherever both apply.
       const uint32_t sb = __float_as_uint(sc);
-      if ((sb & 0x807fffffu) == 0u && sb >= 0x00800000u && sb < 0x7f800000u) {
+      if (code != kCodeE4M3) {
+        // integer codes (uniform over the launch): the integer times the
+        // scale, rounded to bf16 once
+        const uint32_t flip = code == kCodeI8 ? 0x80808080u : 0u;
+        const float bias = code == kCodeI8 ? 128.f : 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t c = x[w] ^ flip;
+          o[w >> 1][2 * (w & 1)] = pack_bf16x2(((float)(c & 0xffu) - bias) * sc, ((float)((c >> 8) & 0xffu) - bias) * sc);
+          o[w >> 1][2 * (w & 1) + 1] =
+              pack_bf16x2(((float)((c >> 16) & 0xffu) - bias) * sc, ((float)(c >> 24) - bias) * sc);
+        }
+      } else if ((sb & 0x807fffffu) == 0u && sb >= 0x00800000u && sb < 0x7f800000u) {
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
           o[w >> 1][2 * (w & 1)] =
@@ -511,51 +525,51 @@ extern "C" size_t pa_prefill_fp8_workspace_size(int32_t batch, int32_t pages_per
   return fp8_widened_bytes(batch, pages_per_seq, page_size, num_kv_heads, head_dim) + plan;
 }
 
-extern "C" int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
-                              const uint8_t* k_cache, const uint8_t* v_cache,
-                              const float* k_scales, const float* v_scales,
-                              int32_t num_pages, int32_t page_size,
-                              int64_t page_stride, int64_t slot_stride, int64_t head_stride,
-                              int64_t scale_page_stride, int64_t scale_head_stride,
-                              const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
-                              const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
-                              const int32_t* input_positions,
-                              int32_t batch, int32_t num_tokens, int32_t max_seqlen_q,
-                              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
-                              float scale, float soft_cap,
-                              uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
-                              void* workspace, size_t workspace_bytes, void* stream) {
+// pa_prefill over 1-byte codes of type `code` (pa_prefill_fp8, pa_prefill_quant).
+static int prefill_quant(const char* name, int32_t code, const uint16_t* q, int64_t q_tok_stride,
+                         int64_t q_head_stride, const uint8_t* k_cache, const uint8_t* v_cache,
+                         const float* k_scales, const float* v_scales, int32_t num_pages, int32_t page_size,
+                         int64_t page_stride, int64_t slot_stride, int64_t head_stride, int64_t scale_page_stride,
+                         int64_t scale_head_stride, const int32_t* block_tables, int64_t bt_stride,
+                         int32_t pages_per_seq, const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                         const int32_t* input_positions, int32_t batch, int32_t num_tokens, int32_t max_seqlen_q,
+                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale, float soft_cap,
+                         uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  if (code != kCodeE4M3 && code != kCodeI8 && code != kCodeU8)
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: code_type %d is not one of PA_CODE_E4M3 (0), PA_CODE_INT8 (1), "
+                "PA_CODE_UINT8 (2)", name, code);
   if (batch < 0 || num_pages <= 0 || page_size <= 0 || pages_per_seq < 0 || num_kv_heads <= 0)
-    return fail(PA_ERR_INVALID_ARGUMENT, "pa_prefill_fp8: bad sizes (batch=%d, num_pages=%d, page_size=%d, "
-                "pages_per_seq=%d, num_kv_heads=%d)", batch, num_pages, page_size, pages_per_seq, num_kv_heads);
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: bad sizes (batch=%d, num_pages=%d, page_size=%d, "
+                "pages_per_seq=%d, num_kv_heads=%d)", name, batch, num_pages, page_size, pages_per_seq, num_kv_heads);
   if (head_dim != kPHeadDim)
-    return fail(PA_ERR_UNSUPPORTED, "pa_prefill_fp8: head_dim %d not supported (only %d)", head_dim, kPHeadDim);
+    return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported (only %d)", name, head_dim, kPHeadDim);
   if (batch == 0 || pages_per_seq == 0 || num_tokens == 0)  // nothing to widen: zero rows only
-    return prefill_launch("pa_prefill_fp8", q, q_tok_stride, q_head_stride, nullptr, nullptr, 1, page_size,
+    return prefill_launch(name, q, q_tok_stride, q_head_stride, nullptr, nullptr, 1, page_size,
                           (int64_t)page_size * num_kv_heads * head_dim, (int64_t)num_kv_heads * head_dim, head_dim,
                           block_tables, bt_stride, pages_per_seq, cu_seqlens_q, cu_seqlens_k, input_positions, 0,
                           num_tokens, max_seqlen_q, num_heads, num_kv_heads, head_dim, scale, soft_cap, out,
                           out_tok_stride, out_head_stride, nullptr, 0, stream);
   if (!k_cache || !v_cache || !k_scales || !v_scales || !block_tables || !cu_seqlens_q)
-    return fail(PA_ERR_INVALID_ARGUMENT, "pa_prefill_fp8: null pointer");
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
   if (num_kv_heads == 1) {  // a size-1 dimension's stride is arbitrary (and never used)
     head_stride = 0;
     scale_head_stride = 0;
   }
   if ((((uintptr_t)k_cache | (uintptr_t)v_cache) & 15u) || (page_stride | slot_stride | head_stride) % 16 ||
       (((uintptr_t)k_scales | (uintptr_t)v_scales) & 3u))
-    return fail(PA_ERR_UNSUPPORTED, "pa_prefill_fp8: code rows must be 16-byte aligned");
+    return fail(PA_ERR_UNSUPPORTED, "%s: code rows must be 16-byte aligned", name);
   const size_t need = pa_prefill_fp8_workspace_size(batch, pages_per_seq, page_size, num_kv_heads, head_dim,
                                                     max_seqlen_q, num_heads);
   if (!need)
-    return fail(PA_ERR_INVALID_ARGUMENT, "pa_prefill_fp8: bad sizes (max_seqlen_q=%d, num_heads=%d, "
-                "num_kv_heads=%d)", max_seqlen_q, num_heads, num_kv_heads);
+    return fail(PA_ERR_INVALID_ARGUMENT, "%s: bad sizes (max_seqlen_q=%d, num_heads=%d, "
+                "num_kv_heads=%d)", name, max_seqlen_q, num_heads, num_kv_heads);
   if (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u))
-    return fail(PA_ERR_WORKSPACE, "pa_prefill_fp8: 256-byte aligned workspace of %zu bytes needed, %zu given", need,
+    return fail(PA_ERR_WORKSPACE, "%s: 256-byte aligned workspace of %zu bytes needed, %zu given", name, need,
                 workspace_bytes);
   const int64_t entries = (int64_t)batch * pages_per_seq;
   if (entries > 0x7fffffff / kWidenSplit)
-    return fail(PA_ERR_UNSUPPORTED, "pa_prefill_fp8: %lld table entries", (long long)entries);
+    return fail(PA_ERR_UNSUPPORTED, "%s: %lld table entries", name, (long long)entries);
   const int64_t page_elems = (int64_t)page_size * num_kv_heads * head_dim;
   uint16_t* wk = reinterpret_cast<uint16_t*>(workspace);
   uint16_t* wv = wk + entries * page_elems;
@@ -570,20 +584,62 @@ extern "C" int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q
   fp8_pages_plan_kernel<<<dim3(1), dim3(1024), 0, s>>>(block_tables, bt_stride, pages_per_seq, batch, page_size,
                                                        num_pages, cu_seqlens_q, cu_seqlens_k, hbits, bt2, owner,
                                                        n_slots);
-  int rc = launch_status("pa_prefill_fp8(plan)");
+  int rc = launch_status(name);
   if (rc) return rc;
   fp8_pages_widen_kernel<<<dim3((unsigned)(entries * kWidenSplit)), dim3(256), 0, s>>>(
       k_cache, v_cache, k_scales, v_scales, num_pages, page_size, page_stride, slot_stride, head_stride,
       scale_page_stride, scale_head_stride, block_tables, bt_stride, pages_per_seq, cu_seqlens_q, cu_seqlens_k,
-      num_kv_heads, owner, n_slots, wk, wv);
-  rc = launch_status("pa_prefill_fp8(widen)");
+      num_kv_heads, owner, n_slots, wk, wv, code);
+  rc = launch_status(name);
   if (rc) return rc;
-  return prefill_launch("pa_prefill_fp8", q, q_tok_stride, q_head_stride, wk, wv, (int32_t)std::min<int64_t>(entries, 0x7fffffff),
+  return prefill_launch(name, q, q_tok_stride, q_head_stride, wk, wv, (int32_t)std::min<int64_t>(entries, 0x7fffffff),
                         page_size, page_elems, (int64_t)num_kv_heads * head_dim, head_dim, bt2, pages_per_seq,
                         pages_per_seq, cu_seqlens_q, cu_seqlens_k, input_positions, batch, num_tokens, max_seqlen_q,
                         num_heads, num_kv_heads, head_dim, scale, soft_cap, out, out_tok_stride, out_head_stride,
                         (char*)workspace + fp8_widened_bytes(batch, pages_per_seq, page_size, num_kv_heads, head_dim),
                         need - fp8_widened_bytes(batch, pages_per_seq, page_size, num_kv_heads, head_dim), stream);
+}
+
+extern "C" int pa_prefill_quant(int32_t code_type, const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                                const uint8_t* k_cache, const uint8_t* v_cache,
+                                const float* k_scales, const float* v_scales,
+                                int32_t num_pages, int32_t page_size,
+                                int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                                int64_t scale_page_stride, int64_t scale_head_stride,
+                                const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                                const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                                const int32_t* input_positions,
+                                int32_t batch, int32_t num_tokens, int32_t max_seqlen_q,
+                                int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                                float scale, float soft_cap,
+                                uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  return prefill_quant("pa_prefill_quant", code_type, q, q_tok_stride, q_head_stride, k_cache, v_cache, k_scales,
+                       v_scales, num_pages, page_size, page_stride, slot_stride, head_stride, scale_page_stride,
+                       scale_head_stride, block_tables, bt_stride, pages_per_seq, cu_seqlens_q, cu_seqlens_k,
+                       input_positions, batch, num_tokens, max_seqlen_q, num_heads, num_kv_heads, head_dim, scale,
+                       soft_cap, out, out_tok_stride, out_head_stride, workspace, workspace_bytes, stream);
+}
+
+extern "C" int pa_prefill_fp8(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_stride,
+                              const uint8_t* k_cache, const uint8_t* v_cache,
+                              const float* k_scales, const float* v_scales,
+                              int32_t num_pages, int32_t page_size,
+                              int64_t page_stride, int64_t slot_stride, int64_t head_stride,
+                              int64_t scale_page_stride, int64_t scale_head_stride,
+                              const int32_t* block_tables, int64_t bt_stride, int32_t pages_per_seq,
+                              const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k,
+                              const int32_t* input_positions,
+                              int32_t batch, int32_t num_tokens, int32_t max_seqlen_q,
+                              int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                              float scale, float soft_cap,
+                              uint16_t* out, int64_t out_tok_stride, int64_t out_head_stride,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  return prefill_quant("pa_prefill_fp8", kCodeE4M3, q, q_tok_stride, q_head_stride, k_cache, v_cache, k_scales,
+                       v_scales, num_pages, page_size, page_stride, slot_stride, head_stride, scale_page_stride,
+                       scale_head_stride, block_tables, bt_stride, pages_per_seq, cu_seqlens_q, cu_seqlens_k,
+                       input_positions, batch, num_tokens, max_seqlen_q, num_heads, num_kv_heads, head_dim, scale,
+                       soft_cap, out, out_tok_stride, out_head_stride, workspace, workspace_bytes, stream);
 }
 
 #ifdef PA_PREFILL_PHASES

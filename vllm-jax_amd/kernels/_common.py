@@ -54,12 +54,19 @@ def pages_strides(k_pages: torch.Tensor):
     return ps, ss, hs
 
 
-def check_quantized_pages(k_pages: torch.Tensor, v_pages: torch.Tensor, k_scales_pages, v_scales_pages) -> bool:
-    """Validate float8 pages with per-token scales (the k_scales_pages /
+# dtype of quantized pages -> code type of pa_decode_quant / pa_prefill_quant
+_CODE_TYPES = {torch.float8_e4m3fn: 0, torch.int8: 1, torch.uint8: 2}
+
+
+def check_quantized_pages(k_pages: torch.Tensor, v_pages: torch.Tensor, k_scales_pages, v_scales_pages):
+    """Validate quantized pages with per-token scales (the k_scales_pages /
     v_scales_pages arguments of the reference kernels, decode...:206-217 and
-    prefill...:255-266); returns whether the pages are quantized."""
+    prefill...:255-266).  Returns None for unquantized pages, else the code
+    type of the pages: float8_e4m3fn codes, or int8 / uint8 integers, which
+    the reference casts to q's dtype as integers (decode...:72-75,
+    prefill...:84-85)."""
     if k_scales_pages is None and v_scales_pages is None:
-        return False
+        return None
     if k_scales_pages is None or v_scales_pages is None:
         raise ValueError("k_scales_pages and v_scales_pages must be given together")
     num_kv_heads, total_num_pages, page_size = k_pages.shape[:3]
@@ -74,14 +81,15 @@ def check_quantized_pages(k_pages: torch.Tensor, v_pages: torch.Tensor, k_scales
     if tuple(k_scales_pages.stride()) != tuple(v_scales_pages.stride()):
         raise ValueError("k_scales_pages and v_scales_pages must share strides")
     for name, t in (("k_pages", k_pages), ("v_pages", v_pages)):
-        if t.dtype != torch.float8_e4m3fn:
+        if t.dtype not in _CODE_TYPES:
             # The reference casts pages of any dtype to q's dtype before the
-            # dot (decode...:72-75, prefill...:84-85), so integer pages would
-            # mean integer values: refuse them rather than read their bytes
-            # as float8 codes.
-            raise NotImplementedError(f"{name} of quantized pages must be float8_e4m3fn, got {t.dtype}")
+            # dot; the kernels take 1-byte codes only.
+            raise NotImplementedError(f"{name} of quantized pages must be float8_e4m3fn, int8 or uint8, "
+                                      f"got {t.dtype}")
         if t.stride(-1) != 1:
             raise ValueError(f"{name} must be contiguous in its last dimension")
+    if k_pages.dtype != v_pages.dtype:
+        raise ValueError(f"k_pages and v_pages must have the same dtype, got {k_pages.dtype} and {v_pages.dtype}")
     require_device("k_scales_pages", k_scales_pages)
     require_device("v_scales_pages", v_scales_pages)
-    return True
+    return _CODE_TYPES[k_pages.dtype]

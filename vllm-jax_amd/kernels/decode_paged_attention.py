@@ -4,7 +4,8 @@
 Same arguments, shapes and ``ValueError`` checks as the reference entry
 (decode_paged_attention.py:300-372).  Quantized pages
 (``k_scales_pages`` / ``v_scales_pages``, decode...:158-159,206-217) are float8
-e4m3fn codes with float32 per-token scales ``[Hkv, NB, BS]``.  As in the reference, q is expected to
+e4m3fn codes, or int8 / uint8 integers, with float32 per-token scales
+``[Hkv, NB, BS]``.  As in the reference, q is expected to
 be pre-scaled (the caller divides by sqrt(d), qwen3.py:207) and no scale is
 applied inside; the extra keyword ``scale`` lets a caller fold the scale into
 the kernel instead.  ``lengths=None`` attends to every slot of the block
@@ -77,7 +78,8 @@ def decode_paged_attention(
             raise ValueError(f"The dtype of `lengths` must be int32. Got {lengths.dtype}")
     if block_h % 16:
         raise ValueError(f"block_h must divisible by 16, but is {block_h}.")
-    quantized = check_quantized_pages(k_pages, v_pages, k_scales_pages, v_scales_pages)
+    code_type = check_quantized_pages(k_pages, v_pages, k_scales_pages, v_scales_pages)
+    quantized = code_type is not None
 
     for name, t in (("q", q), ("k_pages", k_pages), ("v_pages", v_pages), ("block_tables", block_tables)):
         require_device(name, t)
@@ -109,7 +111,7 @@ def decode_paged_attention(
     ps, ss, hs = pages_strides(k_pages)
     if quantized:
         _lib.call(
-            "pa_decode_fp8",
+            "pa_decode_quant", code_type,
             q.data_ptr(), q.stride(0), q.stride(1),
             k_pages.data_ptr(), v_pages.data_ptr(), k_scales_pages.data_ptr(), v_scales_pages.data_ptr(),
             total_num_pages, page_size, ps, ss, hs,

@@ -60,8 +60,8 @@ def prefill_paged_attention(
       * ``out`` -- preallocated output;
       * ``workspace`` -- device bytes for the work list that orders the
         kernel's items by kv length (``pa_prefill_workspace_size``) and, for
-        quantized pages (float8 e4m3fn codes with float32 ``[Hkv, NB, BS]``
-        per-token scales), the pages widened to bf16 ahead of it
+        quantized pages (float8 e4m3fn codes, or int8 / uint8 integers, with
+        float32 ``[Hkv, NB, BS]`` per-token scales), the pages widened to bf16 ahead of it
         (``pa_prefill_fp8_workspace_size``); allocated when absent or too small.
     """
     del slot_mapping, block_m, pages_per_compute_block, k_splits, num_warps, num_stages
@@ -90,7 +90,8 @@ def prefill_paged_attention(
     if cu_seqlens_k is not None and tuple(cu_seqlens_k.shape) != (batch + 1,):
         raise ValueError("cu_seqlens_k must have shape [batch + 1]")
 
-    quantized = check_quantized_pages(k_pages, v_pages, k_scales_pages, v_scales_pages)
+    code_type = check_quantized_pages(k_pages, v_pages, k_scales_pages, v_scales_pages)
+    quantized = code_type is not None
     for name, t in (("q", q), ("k_pages", k_pages), ("v_pages", v_pages), ("block_tables", block_tables),
                     ("cu_seqlens", cu_seqlens), ("input_positions", input_positions)):
         require_device(name, t)
@@ -126,7 +127,7 @@ def prefill_paged_attention(
     ws_bytes = workspace.numel() * workspace.element_size()
     if quantized:
         _lib.call(
-            "pa_prefill_fp8",
+            "pa_prefill_quant", code_type,
             q.data_ptr(), q.stride(0), q.stride(1),
             k_pages.data_ptr(), v_pages.data_ptr(), k_scales_pages.data_ptr(), v_scales_pages.data_ptr(),
             total_num_pages, page_size, ps, ss, hs,
