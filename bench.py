@@ -332,6 +332,7 @@ def run_gpu(args):
     if prefix is not None:
         res["prefix_prefill"] = prefix
     if pre8 is not None:
+        pre8["roofline"]["traffic"] = traffic.get("prefill_fp8_path")
         res["prefill_fp8"] = pre8
     if dec8 is not None:
         dec8["roofline"]["traffic"] = traffic.get("decode_fp8_split_kernel")
