@@ -326,7 +326,13 @@ prefill_any_zero_kernel(PrefillParams p, int head_dim) {
 // The chunk's partial (O unnormalised, the log2 max and the sum per head)
 // goes to the workspace; decode_any_merge_kernel combines the chunks of
 // every sequence.
-template <int D, bool kSoftCap>
+// Whole 128-byte lines per K / V row (head sizes multiple of 64): the
+// generic decode can stream its K / V loads past the caches.
+__host__ __device__ constexpr bool any_decode_streamable(int d) { return d % 64 == 0; }
+
+// kStream: K / V loads non-temporal (rows of whole 128-byte lines, each
+// read by one item: one block of q heads per kv head).
+template <int D, bool kSoftCap, bool kStream>
 __global__ void __launch_bounds__(64)
 decode_any_kernel(DecodeParams p) {
   using A = AnyDims<D>;
@@ -347,7 +353,9 @@ decode_any_kernel(DecodeParams p) {
   const int h = lane >> 5;
   const int hkv = p.num_kv_heads;
   const int vheads = hkv * p.hblocks;
-  const int item = blockIdx.x;
+  // contiguous item ranges per XCD: the kv heads of a (sequence, chunk),
+  // adjacent slices of each token row, are read by one XCD together
+  const int item = xcd_grouped_item(blockIdx.x, gridDim.x);
   const int vh = item % vheads;
   const int rest = item / vheads;
   const int kvh = vh / p.hblocks;
@@ -383,8 +391,13 @@ decode_any_kernel(DecodeParams p) {
       const int j = min(j0 + t, t1 - 1);
       const int64_t off = (int64_t)safe_page(bt_row, j / p.page_size, p.num_pages) * p.page_stride +
                           (int64_t)(j % p.page_size) * p.slot_stride + head_off + 8 * e;
-      kr[i] = ld16(p.k_cache + off);
-      vr[i] = ld16(p.v_cache + off);
+      if constexpr (kStream) {
+        kr[i] = ld16_stream(p.k_cache + off);
+        vr[i] = ld16_stream(p.v_cache + off);
+      } else {
+        kr[i] = ld16(p.k_cache + off);
+        vr[i] = ld16(p.v_cache + off);
+      }
     }
   };
 
@@ -549,11 +562,15 @@ int decode_any_launch(const char* name, const DecodeParams& prm, int head_dim, h
   if (items > 0) {
     const dim3 g((unsigned)items), blk(64);
     const bool cap = p.soft_cap > 0.f;
+    // one block of q heads per kv head: every K / V row is read once
+    const bool stream = p.hblocks == 1;
     switch (head_dim) {
-#define PA_ANY_LAUNCH(d)                                           \
-  case d:                                                          \
-    if (cap) decode_any_kernel<d, true><<<g, blk, 0, s>>>(p);      \
-    else decode_any_kernel<d, false><<<g, blk, 0, s>>>(p);         \
+#define PA_ANY_LAUNCH(d)                                                                    \
+  case d:                                                                                   \
+    if (cap && stream) decode_any_kernel<d, true, any_decode_streamable(d)><<<g, blk, 0, s>>>(p);   \
+    else if (cap) decode_any_kernel<d, true, false><<<g, blk, 0, s>>>(p);                    \
+    else if (stream) decode_any_kernel<d, false, any_decode_streamable(d)><<<g, blk, 0, s>>>(p);    \
+    else decode_any_kernel<d, false, false><<<g, blk, 0, s>>>(p);                            \
     break;
       PA_ANY_DIMS(PA_ANY_LAUNCH)
 #undef PA_ANY_LAUNCH
