@@ -27,9 +27,10 @@
  *
  * Supported shapes: num_heads % num_kv_heads == 0, and
  *   - head_dim 128 in every entry (the tuned kernels); pa_prefill, pa_decode,
- *     pa_decode_noalloc and pa_mixed also take any multiple of 16 from 16 to
- *     256 (generic kernels, same arithmetic, lower throughput); float8 pages
- *     take 128 only;
+ *     pa_decode_noalloc, pa_mixed and the quantized-page entries
+ *     (pa_kv_store_fp8, pa_decode_fp8 / _quant, pa_prefill_fp8 / _quant)
+ *     also take any multiple of 16 from 16 to 256 (generic kernels, same
+ *     arithmetic, lower throughput);
  *   - q heads per kv head: any number for decode, up to 256 for prefill and
  *     pa_mixed (up to 128 for prefill at head sizes from 144 on).
  */

@@ -261,9 +261,10 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
 
 def test_generic_head_sizes_at_the_boundary():
     """Head sizes other than 128: multiples of 16 up to 256 are taken by
-    pa_prefill / pa_decode / pa_mixed (they then fail here only on their null
-    pointers), float8 pages keep refusing them, and the mixed workspace of a
-    generic size holds the decode partials of every chunk after 256 bytes."""
+    pa_prefill / pa_decode / pa_mixed and by the quantized-page entries
+    (they then fail here only on their null pointers), other sizes are
+    refused, and the mixed workspace of a generic size holds the decode
+    partials of every chunk after 256 bytes."""
     lib = PKG._lib.load()
     r256 = lambda n: (n + 255) // 256 * 256
     # 2 decodes, 16 heads, 40-page tables of 256-token pages: 3 chunks of 4096 tokens
@@ -271,8 +272,36 @@ def test_generic_head_sizes_at_the_boundary():
     assert lib.pa_mixed_workspace_size(5, 0, 300, 16, 8, 96, 40, 256) == 256          # no decode sequence
     assert lib.pa_mixed_workspace_size(5, 2, 300, 16, 8, 100, 40, 256) == 0           # not a multiple of 16
     assert lib.pa_mixed_workspace_size(5, 2, 300, 16, 8, 272, 40, 256) == 0           # above 256
-    # float8 decode: head size 64 is refused before any pointer is looked at
+    # quantized decode: head size 64 is taken (then the null pointers fail),
+    # 100 and 272 are refused before any pointer is looked at
     fp8 = [None, 2048, 64, None, None, None, None, 16, 256, 131072, 512, 64, 4096, 256, None, 4, 4, None, 2,
            32, 8, 64, 1.0, 0.0, None, 2048, 64, None, 0, None]
-    assert lib.pa_decode_fp8(*fp8) == -2
-    assert "head_dim" in lib.pa_last_error().decode()
+    assert lib.pa_decode_fp8(*fp8) == -1
+    assert "null pointer" in lib.pa_last_error().decode()
+    for code in (0, 1, 2):
+        assert lib.pa_decode_quant(code, *fp8) == -1
+    for d in (100, 272):
+        bad = list(fp8)
+        bad[21] = d
+        assert lib.pa_decode_fp8(*bad) == -2
+        assert "head_dim" in lib.pa_last_error().decode()
+    # quantized prefill: the same sizes
+    pre = [None, 2048, 64, None, None, None, None, 16, 256, 131072, 512, 64, 4096, 256, None, 4, 4, None, None, None,
+           2, 100, 64, 32, 8, 64, 0.125, 0.0, None, 2048, 64, None, 0, None]
+    assert lib.pa_prefill_fp8(*pre) == -1
+    assert "null pointer" in lib.pa_last_error().decode()
+    for d in (100, 272):
+        bad = list(pre)
+        bad[25] = d
+        assert lib.pa_prefill_quant(1, *bad) == -2
+        assert "head_dim" in lib.pa_last_error().decode()
+    # the quantising store: multiples of 16 from 16 to 256
+    st = [None, 512, 64, None, 512, 64, None, 4, 8, 64, None, None, None, None, 16, 256, 131072, 512, 64,
+          4096, 1, 256, None]
+    assert lib.pa_kv_store_fp8(*st) == -1
+    assert "null pointer" in lib.pa_last_error().decode()
+    for d in (8, 100, 272):
+        bad = list(st)
+        bad[9] = d
+        assert lib.pa_kv_store_fp8(*bad) == -2
+        assert "head_dim" in lib.pa_last_error().decode()

@@ -420,3 +420,120 @@ def test_prefill_integer_pages_match_oracle(pkg, dev, kind, lens, prefix, h, hkv
     err = np.abs(ora.bf16_to_f32(u16(out)) - ora.bf16_to_f32(want)).max()
     print(f"{kind} prefill max-abs err {err:.3e}", flush=True)
     assert err <= TOL
+
+
+# ---- quantized pages at head sizes other than 128 (the generic kernels)
+
+def _code_pool(rng, nb, bs, hkv, d, kind):
+    """Codes ``[NB, BS, Hkv, d]`` of `kind` with ``[Hkv, NB, BS]`` scales:
+    e4m3 from the library's quantiser over 0.5 * N(0, 1) rows, integers
+    uniform over their range with scales that keep code * scale near it."""
+    if kind == "e4m3":
+        kf, vf = _bf16(rng, (nb, bs, hkv, d)), _bf16(rng, (nb, bs, hkv, d))
+        kq, ks = ora.quantize_fp8_rows(kf)
+        vq, vs = ora.quantize_fp8_rows(vf)
+        return kq, vq, np.ascontiguousarray(ks.transpose(2, 0, 1)), np.ascontiguousarray(vs.transpose(2, 0, 1))
+    lo, hi, dt = (-128, 128, np.int8) if kind == "int8" else (0, 256, np.uint8)
+    kq = rng.integers(lo, hi, (nb, bs, hkv, d)).astype(dt)
+    vq = rng.integers(lo, hi, (nb, bs, hkv, d)).astype(dt)
+    ks = (rng.uniform(0.5, 1.5, (hkv, nb, bs)) / 128).astype(np.float32)
+    vs = (rng.uniform(0.5, 1.5, (hkv, nb, bs)) / 256).astype(np.float32)
+    return kq, vq, ks, vs
+
+
+def _code_pages(codes, kind, dev):
+    """Device pages ``[Hkv, NB, BS, d]`` (a view of the [NB, BS, Hkv, d] pool)
+    in the torch dtype of `kind`."""
+    import torch
+    t = torch.from_numpy(codes).to(dev)
+    if kind == "e4m3":
+        t = t.view(torch.float8_e4m3fn)
+    return t.permute(2, 0, 1, 3)
+
+
+@pytest.mark.parametrize("d,nb,bs,hkv,t", [(16, 8, 32, 4, 200), (64, 16, 256, 8, 700), (96, 40, 16, 2, 300),
+                                           (256, 6, 64, 2, 333)])
+def test_kv_store_fp8_head_dims_bit_exact(pkg, dev, d, nb, bs, hkv, t):
+    """The quantising store at head sizes other than 128 (16 lanes per row up
+    to 128, 32 above): codes and scales bit-exact against the oracle."""
+    import torch
+    rng = np.random.default_rng(d + t)
+    k = _bf16(rng, (t, hkv, d), 2.0)
+    v = _bf16(rng, (t, hkv, d), 0.1)
+    k[3, 0] = 0                                       # an all-zero row: scale 1, zero codes
+    v[5, hkv - 1, : d // 2] = 0                       # half a row zero
+    slots = rng.permutation(nb * bs)[:t].astype(np.int32)
+    slots[::7] = -1
+    codes0 = rng.integers(0, 256, (2, nb, bs, hkv, d)).astype(np.uint8)
+    scales0 = rng.standard_normal((2, hkv, nb, bs)).astype(np.float32)
+    codes = torch.from_numpy(codes0).to(dev).view(torch.float8_e4m3fn)
+    scales = torch.from_numpy(scales0).to(dev)
+    pkg.update_kv_cache_fp8(codes, scales, torch.as_tensor(slots, device=dev), from_u16(k, dev), from_u16(v, dev))
+    torch.cuda.synchronize()
+    kc, vc, ks, vs = ora.kv_store_fp8(codes0[0], codes0[1], scales0[0], scales0[1], k, v, slots)
+    assert np.array_equal(_u8(codes[0]), kc) and np.array_equal(_u8(codes[1]), vc)
+    assert np.array_equal(scales[0].cpu().numpy(), ks) and np.array_equal(scales[1].cpu().numpy(), vs)
+
+
+@pytest.mark.parametrize("kind", ["e4m3", "int8", "uint8"])
+@pytest.mark.parametrize("lens,h,hkv,bs,d,cap", [
+    ([1, 15, 300, 0, 2049], 32, 8, 256, 64, None),   # two chunks, length 0
+    ([70, 500, 33], 16, 16, 32, 96, 30.0),           # MHA, soft cap
+    ([17, 1100, 2050], 32, 2, 16, 256, None),        # G = 16, 16-token pages
+    ([5, 260], 48, 1, 64, 48, None),                 # G = 48: two blocks of q heads
+])
+def test_decode_quantized_pages_head_dims(pkg, dev, kind, lens, h, hkv, bs, d, cap):
+    """Decode over quantized pages at head sizes other than 128 (the generic
+    kernel widening codes as it stages them) against the oracle over the
+    same codes and scales, every sequence."""
+    import torch
+    rng = np.random.default_rng(sum(lens) + h + d + len(kind))
+    nb = sum((n + bs - 1) // bs for n in lens) + 2
+    kq, vq, ks, vs = _code_pool(rng, nb, bs, hkv, d, kind)
+    bt = _tables_for(rng, lens, bs, nb, pow2_width=True)
+    q = _bf16(rng, (len(lens), h, d))
+    out = pkg.decode_paged_attention(from_u16(q, dev), _code_pages(kq, kind, dev), _code_pages(vq, kind, dev),
+                                     torch.as_tensor(bt, device=dev),
+                                     torch.as_tensor(np.asarray(lens, np.int32), device=dev),
+                                     k_scales_pages=torch.from_numpy(ks).to(dev),
+                                     v_scales_pages=torch.from_numpy(vs).to(dev), attn_logits_soft_cap=cap)
+    torch.cuda.synchronize()
+    got = u16(out)
+    want = ora.decode_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, np.asarray(lens),
+                                soft_cap=cap, k_scales_pages=ks, v_scales_pages=vs, code_type=kind)
+    err = np.abs(ora.bf16_to_f32(got) - ora.bf16_to_f32(want)).max()
+    print(f"{kind} decode d={d} max-abs err {err:.3e}", flush=True)
+    assert err <= TOL
+    assert not got[np.asarray(lens) == 0].any()
+
+
+@pytest.mark.parametrize("kind", ["e4m3", "int8", "uint8"])
+@pytest.mark.parametrize("lens,prefix,h,hkv,bs,d", [
+    ([17, 128, 300, 511], [0, 0, 0, 0], 16, 8, 256, 64),   # the Qwen3-0.6B-sized batch at d = 64
+    ([5, 40, 130], [0, 20, 300], 32, 8, 16, 96),            # cached prefixes, small pages
+    ([200, 77], [64, 0], 16, 2, 64, 256),                   # G = 8, d = 256
+])
+def test_prefill_quantized_pages_head_dims(pkg, dev, kind, lens, prefix, h, hkv, bs, d):
+    """Prefill over quantized pages at head sizes other than 128 (pages
+    widened once, then the generic prefill) against the oracle, every row."""
+    import torch
+    rng = np.random.default_rng(sum(lens) + h + d + 3 * len(kind))
+    kv = [p + n for p, n in zip(prefix, lens)]
+    nb = sum((n + bs - 1) // bs for n in kv) + 2
+    kq, vq, ks, vs = _code_pool(rng, nb, bs, hkv, d, kind)
+    bt = _tables_for(rng, kv, bs, nb)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cuk = np.concatenate([[0], np.cumsum(kv)]).astype(np.int32)
+    pos = np.concatenate([np.arange(p, p + n) for p, n in zip(prefix, lens)]).astype(np.int32)
+    q = _bf16(rng, (int(cu[-1]), h, d))
+    i32 = lambda x: torch.as_tensor(np.ascontiguousarray(x, dtype=np.int32), device=dev)
+    out = pkg.prefill_paged_attention(from_u16(q, dev), _code_pages(kq, kind, dev), _code_pages(vq, kind, dev),
+                                      i32(bt), i32(cu), None, i32(pos), max_seqlen_bucket=max(lens),
+                                      cu_seqlens_k=i32(cuk), k_scales_pages=torch.from_numpy(ks).to(dev),
+                                      v_scales_pages=torch.from_numpy(vs).to(dev))
+    torch.cuda.synchronize()
+    want = ora.prefill_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, cu, pos,
+                                 cu_seqlens_k=cuk, k_scales_pages=ks, v_scales_pages=vs, code_type=kind)
+    err = np.abs(ora.bf16_to_f32(u16(out)) - ora.bf16_to_f32(want)).max()
+    print(f"{kind} prefill d={d} max-abs err {err:.3e}", flush=True)
+    assert err <= TOL

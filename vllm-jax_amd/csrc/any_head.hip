@@ -23,6 +23,7 @@
 // column lives in the two lanes (n, 0) and (n, 1), exactly where O^T's
 // column n lives, so the rescale needs no exchange.
 #include <climits>
+#include <type_traits>
 
 #include "any_head.h"
 #include "decode_impl.h"
@@ -113,9 +114,11 @@ constexpr float kAnySlack = 8.f;  // lazy rescale: the reference max moves when 
 // kLazy: move the reference only past the slack (prefill, where the VALU
 // work of the softmax wave bounds the step); otherwise every step (decode,
 // bound by memory, where the branch costs registers at the large sizes).
-template <int kDt, int kRowBytes, bool kLazy>
+// kVs: quantized V pages, vs[i] the V scale of s[i]'s token: P is rounded to
+// bf16 as p * vs for PV, while the row sum takes p itself.
+template <int kDt, int kRowBytes, bool kLazy, bool kVs = false>
 __device__ __forceinline__ void any_softmax_pv(const f32x16& s, float& m_run, float& l_run, f32x16 (&acc)[kDt],
-                                               const lds_char* v, int lane) {
+                                               const lds_char* v, int lane, const f32x16& vs = f32x16{}) {
   float mx = s[0];
 #pragma unroll
   for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
@@ -147,7 +150,8 @@ __device__ __forceinline__ void any_softmax_pv(const f32x16& s, float& m_run, fl
     for (int e = 0; e < 4; ++e) {
       const float a = fast_exp2(s[8 * u + 2 * e] - ms);
       const float b = fast_exp2(s[8 * u + 2 * e + 1] - ms);
-      pw[u][e] = pack_bf16x2(a, b);
+      if constexpr (kVs) pw[u][e] = pack_bf16x2(a * vs[8 * u + 2 * e], b * vs[8 * u + 2 * e + 1]);
+      else pw[u][e] = pack_bf16x2(a, b);
       ls += a + b;
     }
   l_run = kLazy ? l_run + ls : l_run * corr + ls;
@@ -330,11 +334,24 @@ prefill_any_zero_kernel(PrefillParams p, int head_dim) {
 // generic decode can stream its K / V loads past the caches.
 __host__ __device__ constexpr bool any_decode_streamable(int d) { return d % 64 == 0; }
 
+// Eight 1-byte codes of type `code` (uniform over the launch) to bf16, exactly.
+__device__ __forceinline__ u32x4 codes8_to_bf16x8_rt(const u32x2& c, int code) {
+  if (code == kCodeI8) return codes8_to_bf16x8<kCodeI8>(c);
+  if (code == kCodeU8) return codes8_to_bf16x8<kCodeU8>(c);
+  return codes8_to_bf16x8<kCodeE4M3>(c);
+}
+
 // kStream: K / V loads non-temporal (rows of whole 128-byte lines, each
 // read by one item: one block of q heads per kv head).
-template <int D, bool kSoftCap, bool kStream>
+// kQuant: the pages hold 1-byte codes of type `code` (p.k8 / p.v8, strides in
+// bytes) with per-token scales (p.k_scales / p.v_scales).  Eight codes per
+// lane and chunk are loaded (8 bytes) and widened to bf16 exactly as they are
+// staged, so the tiles and the MFMAs are those of bf16 pages; the step's
+// scales are staged beside them.  As in the tuned decode, the logit of token
+// j is (q . k_j) * k_scale_j, and P is rounded to bf16 as p * v_scale_j.
+template <int D, bool kSoftCap, bool kStream, bool kQuant = false>
 __global__ void __launch_bounds__(64)
-decode_any_kernel(DecodeParams p) {
+decode_any_kernel(DecodeParams p, int code) {
   using A = AnyDims<D>;
   // Up to head size 64 a load batch is two 32-token steps (more bytes in
   // flight per wave for one wave less per SIMD); the next batch is loaded
@@ -346,6 +363,7 @@ decode_any_kernel(DecodeParams p) {
   constexpr bool kPrefetch = kSoftCap ? D <= 192 : D <= 224;
   __shared__ __attribute__((aligned(16))) char k_tile_g[kTok * A::kRow];
   __shared__ __attribute__((aligned(16))) char v_tile_g[kTok * A::kRow + 32];  // V^T operands read 16 bytes past
+  __shared__ __attribute__((aligned(16))) float ksc_g[kQuant ? kTok : 4], vsc_g[kQuant ? kTok : 4];
   lds_char* k_tile = (lds_char*)k_tile_g;
   lds_char* v_tile = (lds_char*)v_tile_g;
   const int lane = threadIdx.x;
@@ -380,7 +398,9 @@ decode_any_kernel(DecodeParams p) {
   }
   const int32_t* bt_row = p.block_tables + (int64_t)b * p.bt_stride;
   const int64_t head_off = (int64_t)kvh * p.head_stride;
-  u32x4 kr[kPer], vr[kPer];
+  using Raw = std::conditional_t<kQuant, u32x2, u32x4>;
+  Raw kr[kPer], vr[kPer];
+  float ksr = 0.f, vsr = 0.f;  // (kQuant) scales of token lane % kTok of the batch
   auto load = [&](int j0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
@@ -391,13 +411,25 @@ decode_any_kernel(DecodeParams p) {
       const int j = min(j0 + t, t1 - 1);
       const int64_t off = (int64_t)safe_page(bt_row, j / p.page_size, p.num_pages) * p.page_stride +
                           (int64_t)(j % p.page_size) * p.slot_stride + head_off + 8 * e;
-      if constexpr (kStream) {
+      if constexpr (kQuant) {
+        kr[i] = *reinterpret_cast<const u32x2*>(p.k8 + off);
+        vr[i] = *reinterpret_cast<const u32x2*>(p.v8 + off);
+      } else if constexpr (kStream) {
         kr[i] = ld16_stream(p.k_cache + off);
         vr[i] = ld16_stream(p.v_cache + off);
       } else {
         kr[i] = ld16(p.k_cache + off);
         vr[i] = ld16(p.v_cache + off);
       }
+    }
+    if constexpr (kQuant) {
+      // past the chunk: the scales of its last token (a real one; those
+      // tokens are masked, so their p is 0)
+      const int j = min(j0 + (lane & (kTok - 1)), t1 - 1);
+      const int64_t si = (int64_t)safe_page(bt_row, j / p.page_size, p.num_pages) * p.sc_page_stride +
+                         (int64_t)kvh * p.sc_head_stride + j % p.page_size;
+      ksr = p.k_scales[si];
+      vsr = p.v_scales[si];
     }
   };
 
@@ -414,8 +446,19 @@ decode_any_kernel(DecodeParams p) {
       const int c = lane + 64 * i;
       const int t = c / A::kChunks;
       const int e = c - t * A::kChunks;
-      lds_st16(k_tile + t * A::kRow + 16 * e, kr[i]);
-      lds_st16(v_tile + t * A::kRow + 16 * e, vr[i]);
+      if constexpr (kQuant) {
+        lds_st16(k_tile + t * A::kRow + 16 * e, codes8_to_bf16x8_rt(kr[i], code));
+        lds_st16(v_tile + t * A::kRow + 16 * e, codes8_to_bf16x8_rt(vr[i], code));
+      } else {
+        lds_st16(k_tile + t * A::kRow + 16 * e, kr[i]);
+        lds_st16(v_tile + t * A::kRow + 16 * e, vr[i]);
+      }
+    }
+    if constexpr (kQuant) {
+      if (lane < kTok) {
+        ksc_g[lane] = ksr;
+        vsc_g[lane] = vsr;
+      }
     }
     __syncthreads();
     if constexpr (kPrefetch) {
@@ -430,12 +473,29 @@ decode_any_kernel(DecodeParams p) {
         for (int ks = 0; ks < A::kKs; ++ks)
           s = mfma32(as_bf16x8(lds_ld16(k_tile + (kAnyStep * sub + n) * A::kRow + 2 * (16 * ks + 8 * h))), qb[ks],
                      s);
+        // (kQuant) scales of the lane's 16 tokens 8(i/4) + 4h + i%4 of the step
+        f32x16 ksc = {}, vsc = {};
+        if constexpr (kQuant) {
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const int o = kAnyStep * sub + 8 * q4 + 4 * h;
+            const f32x4 a = __builtin_bit_cast(f32x4, lds_ld16((const lds_char*)ksc_g + 4 * o));
+            const f32x4 c = __builtin_bit_cast(f32x4, lds_ld16((const lds_char*)vsc_g + 4 * o));
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              ksc[4 * q4 + r] = a[r];
+              vsc[4 * q4 + r] = c[r];
+            }
+          }
+        }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int j = js + 8 * (i >> 2) + 4 * h + (i & 3);
-          s[i] = j < t1 ? any_logit_f32<kSoftCap>(s[i], p.logit_scale, p.soft_cap) : -INFINITY;
+          s[i] = j < t1 ? any_logit_f32<kSoftCap>(kQuant ? s[i] * ksc[i] : s[i], p.logit_scale, p.soft_cap)
+                        : -INFINITY;
         }
-        any_softmax_pv<A::kDt, A::kRow, false>(s, m_run, l_run, acc, v_tile + kAnyStep * sub * A::kRow, lane);
+        any_softmax_pv<A::kDt, A::kRow, false, kQuant>(s, m_run, l_run, acc, v_tile + kAnyStep * sub * A::kRow,
+                                                       lane, vsc);
       }
     }
   }
@@ -552,7 +612,7 @@ int prefill_any_launch(const char* name, const PrefillParams& prm, int head_dim,
   return launch_status(name);
 }
 
-int decode_any_launch(const char* name, const DecodeParams& prm, int head_dim, hipStream_t s) {
+int decode_any_launch(const char* name, const DecodeParams& prm, int head_dim, hipStream_t s, int code) {
   DecodeParams p = prm;
   p.plan = nullptr;
   p.hblocks = (p.group + 31) / 32;
@@ -564,13 +624,16 @@ int decode_any_launch(const char* name, const DecodeParams& prm, int head_dim, h
     const bool cap = p.soft_cap > 0.f;
     // one block of q heads per kv head: every K / V row is read once
     const bool stream = p.hblocks == 1;
+    const bool quant = code >= 0;
     switch (head_dim) {
-#define PA_ANY_LAUNCH(d)                                                                    \
-  case d:                                                                                   \
-    if (cap && stream) decode_any_kernel<d, true, any_decode_streamable(d)><<<g, blk, 0, s>>>(p);   \
-    else if (cap) decode_any_kernel<d, true, false><<<g, blk, 0, s>>>(p);                    \
-    else if (stream) decode_any_kernel<d, false, any_decode_streamable(d)><<<g, blk, 0, s>>>(p);    \
-    else decode_any_kernel<d, false, false><<<g, blk, 0, s>>>(p);                            \
+#define PA_ANY_LAUNCH(d)                                                                          \
+  case d:                                                                                         \
+    if (quant && cap) decode_any_kernel<d, true, false, true><<<g, blk, 0, s>>>(p, code);         \
+    else if (quant) decode_any_kernel<d, false, false, true><<<g, blk, 0, s>>>(p, code);          \
+    else if (cap && stream) decode_any_kernel<d, true, any_decode_streamable(d)><<<g, blk, 0, s>>>(p, 0);   \
+    else if (cap) decode_any_kernel<d, true, false><<<g, blk, 0, s>>>(p, 0);                       \
+    else if (stream) decode_any_kernel<d, false, any_decode_streamable(d)><<<g, blk, 0, s>>>(p, 0);  \
+    else decode_any_kernel<d, false, false><<<g, blk, 0, s>>>(p, 0);                               \
     break;
       PA_ANY_DIMS(PA_ANY_LAUNCH)
 #undef PA_ANY_LAUNCH

@@ -215,12 +215,12 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "%s: Number of Q heads must be divisible by number of KV heads. Got %d and %d.", name,
                 num_heads, num_kv_heads);
-  const bool any_d = head_dim != kHeadDim && !fp8 && any_head_dim(head_dim);
+  const bool any_d = head_dim != kHeadDim && any_head_dim(head_dim);
   if (head_dim != kHeadDim && !any_d)
-    return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported (%s)", name, head_dim,
-                fp8 ? "quantized pages: only 128" : "128, or a multiple of 16 from 16 to 256");
+    return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported (128, or a multiple of 16 from 16 to 256)", name,
+                head_dim);
   const int group = num_heads / num_kv_heads;
-  if (fp8 && page_size % kDecodeStep != 0)
+  if (fp8 && !any_d && page_size % kDecodeStep != 0)
     return fail(PA_ERR_UNSUPPORTED, "%s: quantized pages need page_size %% %d == 0 (got %d)", name, kDecodeStep,
                 page_size);
   if (batch == 0) return PA_OK;
@@ -277,7 +277,7 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
   prm.zero_empty = 0;
 
   hipStream_t s = (hipStream_t)stream;
-  if (any_d) return decode_any_launch(name, prm, head_dim, s);
+  if (any_d) return decode_any_launch(name, prm, head_dim, s, fp8 ? code : -1);
   const int64_t pairs = (int64_t)batch * prm.n_chunks;
   const int64_t vheads = (int64_t)num_kv_heads * prm.hblocks;  // work items per (sequence, chunk)
   // The work list pays for its launch once the grid is several waves of

@@ -82,8 +82,9 @@ gather_kv_kernel(const uint16_t* __restrict__ cache, int32_t num_pages, int32_t 
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Quantising KV store: one 16-lane group per (token, kv head) row of d = 128,
-// 8 values per lane.  amax over the row (16-lane butterfly); the stored
+// Quantising KV store: one kLanes-lane group per (token, kv head) row, 8
+// values per lane (lanes past the row's cph = d / 8 chunks hold none; 16
+// lanes up to d = 128, 32 up to 256).  amax over the row (butterfly); the stored
 // scale is the smallest power of two s with amax / s <= 448 (at least
 // 2^-126), and the codes are e4m3(x / s) with round-to-nearest-even
 // (v_cvt_pk_fp8_f32), x / s exact; an all-zero row stores scale 1.  A power
@@ -91,29 +92,33 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // conversion (v_cvt_scalef32_pk_bf16_fp8 scales by a power of two).  Codes
 // go to the (page, slot, head) byte pool, scales to a [Hkv, NB, BS]-strided
 // float pool.
+template <int kLanes>
 __global__ void __launch_bounds__(256)
 kv_store_fp8_kernel(const uint16_t* __restrict__ k, int64_t k_ts, int64_t k_hs,
                     const uint16_t* __restrict__ v, int64_t v_ts, int64_t v_hs,
-                    const int32_t* __restrict__ slot_mapping, int32_t num_tokens, int32_t num_kv_heads,
+                    const int32_t* __restrict__ slot_mapping, int32_t num_tokens, int32_t num_kv_heads, int32_t cph,
                     uint8_t* __restrict__ k_cache, uint8_t* __restrict__ v_cache,
                     float* __restrict__ k_scales, float* __restrict__ v_scales,
                     int64_t num_slots, int32_t page_size,
                     int64_t page_stride, int64_t slot_stride, int64_t head_stride,
                     int64_t sc_page_stride, int64_t sc_slot_stride, int64_t sc_head_stride) {
-  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 4;  // (token, head)
-  const int i16 = threadIdx.x & 15;
+  static_assert(kLanes == 16 || kLanes == 32, "row group");
+  const int64_t row = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / kLanes;  // (token, head)
+  const int i16 = threadIdx.x & (kLanes - 1);
   const int64_t t = row / num_kv_heads;
-  if (t >= num_tokens) return;  // whole 16-lane group
+  if (t >= num_tokens) return;  // whole group
   const int h = (int)(row - t * num_kv_heads);
   const int64_t slot = slot_mapping[t];
   if (slot < 0 || slot >= num_slots) return;
   const int64_t page = slot / page_size;
   const int64_t off = slot - page * page_size;
-  const int64_t dst = page * page_stride + off * slot_stride + h * head_stride + 8 * i16;
+  const bool has = i16 < cph;  // the lane holds a chunk of the row
+  const int ci = has ? i16 : 0;
+  const int64_t dst = page * page_stride + off * slot_stride + h * head_stride + 8 * ci;
   const int64_t sdst = page * sc_page_stride + off * sc_slot_stride + h * sc_head_stride;
 #pragma unroll
   for (int which = 0; which < 2; ++which) {
-    const u32x4 x = ld16(which ? v + t * v_ts + h * v_hs + 8 * i16 : k + t * k_ts + h * k_hs + 8 * i16);
+    const u32x4 x = ld16(which ? v + t * v_ts + h * v_hs + 8 * ci : k + t * k_ts + h * k_hs + 8 * ci);
     float f[8];
     float a = 0.f;
 #pragma unroll
@@ -122,10 +127,9 @@ kv_store_fp8_kernel(const uint16_t* __restrict__ k, int64_t k_ts, int64_t k_hs,
       f[2 * e + 1] = bf16_hi(x[e]);
       a = fmaxf(a, fmaxf(fabsf(f[2 * e]), fabsf(f[2 * e + 1])));
     }
-    a = fmaxf(a, __shfl_xor(a, 1, 16));
-    a = fmaxf(a, __shfl_xor(a, 2, 16));
-    a = fmaxf(a, __shfl_xor(a, 4, 16));
-    a = fmaxf(a, __shfl_xor(a, 8, 16));
+    if (!has) a = 0.f;
+#pragma unroll
+    for (int m = 1; m < kLanes; m <<= 1) a = fmaxf(a, __shfl_xor(a, m, kLanes));
     // a = 1.m * 2^E: a / 2^(E-8) = 1.m * 256 <= 448 iff 1.m <= 1.75, else
     // 2^(E-7) is the smallest; exponent fields below 1 are raised to 1
     const uint32_t ab = __float_as_uint(a);
@@ -139,7 +143,7 @@ kv_store_fp8_kernel(const uint16_t* __restrict__ k, int64_t k_ts, int64_t k_hs,
     lo = __builtin_amdgcn_cvt_pk_fp8_f32(f[2] * inv, f[3] * inv, lo, true);
     hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[4] * inv, f[5] * inv, hi, false);
     hi = __builtin_amdgcn_cvt_pk_fp8_f32(f[6] * inv, f[7] * inv, hi, true);
-    *reinterpret_cast<u32x2*>((which ? v_cache : k_cache) + dst) = u32x2{(uint32_t)lo, (uint32_t)hi};
+    if (has) *reinterpret_cast<u32x2*>((which ? v_cache : k_cache) + dst) = u32x2{(uint32_t)lo, (uint32_t)hi};
     if (i16 == 0) (which ? v_scales : k_scales)[sdst] = sc;
   }
 }
@@ -265,7 +269,9 @@ extern "C" int pa_kv_store_fp8(const uint16_t* k, int64_t k_tok_stride, int64_t 
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "pa_kv_store_fp8: bad sizes (num_tokens=%d, num_kv_heads=%d, num_pages=%d, page_size=%d)",
                 num_tokens, num_kv_heads, num_pages, page_size);
-  if (head_dim != 128) return fail(PA_ERR_UNSUPPORTED, "pa_kv_store_fp8: head_dim %d not supported (only 128)", head_dim);
+  if (head_dim % 16 != 0 || head_dim < 16 || head_dim > 256)
+    return fail(PA_ERR_UNSUPPORTED, "pa_kv_store_fp8: head_dim %d not supported (a multiple of 16 from 16 to 256)",
+                head_dim);
   if (num_tokens == 0) return PA_OK;
   if (!k || !v || !slot_mapping || !k_cache || !v_cache || !k_scales || !v_scales)
     return fail(PA_ERR_INVALID_ARGUMENT, "pa_kv_store_fp8: null pointer");
@@ -274,10 +280,19 @@ extern "C" int pa_kv_store_fp8(const uint16_t* k, int64_t k_tok_stride, int64_t 
       (k_tok_stride | k_head_stride | v_tok_stride | v_head_stride) % 8 || (page_stride | slot_stride | head_stride) % 8)
     return fail(PA_ERR_UNSUPPORTED, "pa_kv_store_fp8: bf16 rows must be 16-byte and code rows 8-byte aligned");
   const int64_t groups = (int64_t)num_tokens * num_kv_heads;
-  const int64_t blocks = (groups * 16 + 255) / 256;
-  kv_store_fp8_kernel<<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(
-      k, k_tok_stride, k_head_stride, v, v_tok_stride, v_head_stride, slot_mapping, num_tokens, num_kv_heads,
-      k_cache, v_cache, k_scales, v_scales, (int64_t)num_pages * page_size, page_size, page_stride, slot_stride,
-      head_stride, scale_page_stride, scale_slot_stride, scale_head_stride);
+  const int32_t cph = head_dim / 8;
+  const int lanes = cph <= 16 ? 16 : 32;
+  const int64_t blocks = (groups * lanes + 255) / 256;
+  if (blocks > 0x7fffffff) return fail(PA_ERR_UNSUPPORTED, "pa_kv_store_fp8: %d tokens too many", num_tokens);
+  if (lanes == 16)
+    kv_store_fp8_kernel<16><<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(
+        k, k_tok_stride, k_head_stride, v, v_tok_stride, v_head_stride, slot_mapping, num_tokens, num_kv_heads, cph,
+        k_cache, v_cache, k_scales, v_scales, (int64_t)num_pages * page_size, page_size, page_stride, slot_stride,
+        head_stride, scale_page_stride, scale_slot_stride, scale_head_stride);
+  else
+    kv_store_fp8_kernel<32><<<dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream>>>(
+        k, k_tok_stride, k_head_stride, v, v_tok_stride, v_head_stride, slot_mapping, num_tokens, num_kv_heads, cph,
+        k_cache, v_cache, k_scales, v_scales, (int64_t)num_pages * page_size, page_size, page_stride, slot_stride,
+        head_stride, scale_page_stride, scale_slot_stride, scale_head_stride);
   return launch_status("pa_kv_store_fp8");
 }

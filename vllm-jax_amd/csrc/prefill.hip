@@ -283,23 +283,24 @@ fp8_pages_widen_kernel(const uint8_t* __restrict__ k8, const uint8_t* __restrict
                        int64_t bt_stride, int32_t pages_per_seq, const int32_t* __restrict__ cu_q,
                        const int32_t* __restrict__ cu_k, int32_t num_kv_heads, const int32_t* __restrict__ owner,
                        const int32_t* __restrict__ count, uint16_t* __restrict__ wk, uint16_t* __restrict__ wv,
-                       int32_t code) {
+                       int32_t code, int32_t head_dim) {
   const int32_t sl = blockIdx.x / kWidenSplit;
   const int part_w = blockIdx.x - sl * kWidenSplit;
   if (sl >= *count) return;
   const int64_t page =
       fp8_entry_page(bt, bt_stride, pages_per_seq, page_size, num_pages, cu_q, cu_k, owner[sl]);  // in use
-  const int rows = page_size * num_kv_heads;  // (slot, head) rows of 128 codes
-  const int64_t wbase = (int64_t)sl * rows * kPHeadDim;
-  const int c_lo = (int)((int64_t)rows * 8 * part_w / kWidenSplit);
-  const int c_hi = (int)((int64_t)rows * 8 * (part_w + 1) / kWidenSplit);
+  const int rows = page_size * num_kv_heads;  // (slot, head) rows of head_dim codes
+  const int parts = head_dim >> 4;            // 16 codes per part
+  const int64_t wbase = (int64_t)sl * rows * head_dim;
+  const int c_lo = (int)((int64_t)rows * parts * part_w / kWidenSplit);
+  const int c_hi = (int)((int64_t)rows * parts * (part_w + 1) / kWidenSplit);
 #pragma unroll 4
   for (int c = c_lo + threadIdx.x; c < c_hi; c += 256) {
-    const int r = c >> 3, part = c & 7;  // 16 codes of row r
+    const int r = c / parts, part = c - r * parts;  // 16 codes of row r
     const int slot = r / num_kv_heads, h = r - slot * num_kv_heads;
     const int64_t src = page * page_stride + (int64_t)slot * slot_stride + (int64_t)h * head_stride + 16 * part;
     const int64_t sidx = page * sc_page_stride + (int64_t)h * sc_head_stride + slot;
-    const int64_t dst = wbase + (int64_t)r * kPHeadDim + 16 * part;
+    const int64_t dst = wbase + (int64_t)r * head_dim + 16 * part;
 #pragma unroll
     for (int which = 0; which < 2; ++which) {
       const u32x4 x = ld16((which ? v8 : k8) + src);
@@ -542,8 +543,9 @@ static int prefill_quant(const char* name, int32_t code, const uint16_t* q, int6
   if (batch < 0 || num_pages <= 0 || page_size <= 0 || pages_per_seq < 0 || num_kv_heads <= 0)
     return fail(PA_ERR_INVALID_ARGUMENT, "%s: bad sizes (batch=%d, num_pages=%d, page_size=%d, "
                 "pages_per_seq=%d, num_kv_heads=%d)", name, batch, num_pages, page_size, pages_per_seq, num_kv_heads);
-  if (head_dim != kPHeadDim)
-    return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported (only %d)", name, head_dim, kPHeadDim);
+  if (head_dim != kPHeadDim && !any_head_dim(head_dim))
+    return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported (128, or a multiple of 16 from 16 to 256)", name,
+                head_dim);
   if (batch == 0 || pages_per_seq == 0 || num_tokens == 0)  // nothing to widen: zero rows only
     return prefill_launch(name, q, q_tok_stride, q_head_stride, nullptr, nullptr, 1, page_size,
                           (int64_t)page_size * num_kv_heads * head_dim, (int64_t)num_kv_heads * head_dim, head_dim,
@@ -589,7 +591,7 @@ static int prefill_quant(const char* name, int32_t code, const uint16_t* q, int6
   fp8_pages_widen_kernel<<<dim3((unsigned)(entries * kWidenSplit)), dim3(256), 0, s>>>(
       k_cache, v_cache, k_scales, v_scales, num_pages, page_size, page_stride, slot_stride, head_stride,
       scale_page_stride, scale_head_stride, block_tables, bt_stride, pages_per_seq, cu_seqlens_q, cu_seqlens_k,
-      num_kv_heads, owner, n_slots, wk, wv, code);
+      num_kv_heads, owner, n_slots, wk, wv, code, head_dim);
   rc = launch_status(name);
   if (rc) return rc;
   return prefill_launch(name, q, q_tok_stride, q_head_stride, wk, wv, (int32_t)std::min<int64_t>(entries, 0x7fffffff),
