@@ -371,9 +371,22 @@ decode_any_kernel(DecodeParams p, int code) {
   const int h = lane >> 5;
   const int hkv = p.num_kv_heads;
   const int vheads = hkv * p.hblocks;
-  // contiguous item ranges per XCD: the kv heads of a (sequence, chunk),
-  // adjacent slices of each token row, are read by one XCD together
-  const int item = xcd_grouped_item(blockIdx.x, gridDim.x);
+  int item;
+  if (p.plan) {
+    // the decode work list (pairs by token count, most first): XCD x = bid
+    // % 8 takes ranks x, x + 8, ..., all kv heads (and q-head blocks) of a
+    // rank in a row, so the XCDs get near-equal work and the kv heads of a
+    // token row are read by one XCD together
+    const int k = blockIdx.x >> 3;
+    const int kr = k / vheads;
+    const int r = 8 * kr + (blockIdx.x & 7);
+    if (r >= p.plan[0]) return;
+    item = p.plan[kDecodePlanHeader + r] * vheads + (k - kr * vheads);
+  } else {
+    // contiguous item ranges per XCD: the kv heads of a (sequence, chunk),
+    // adjacent slices of each token row, are read by one XCD together
+    item = xcd_grouped_item(blockIdx.x, gridDim.x);
+  }
   const int vh = item % vheads;
   const int rest = item / vheads;
   const int kvh = vh / p.hblocks;
@@ -614,9 +627,11 @@ int prefill_any_launch(const char* name, const PrefillParams& prm, int head_dim,
 
 int decode_any_launch(const char* name, const DecodeParams& prm, int head_dim, hipStream_t s, int code) {
   DecodeParams p = prm;
-  p.plan = nullptr;
   p.hblocks = (p.group + 31) / 32;
-  const int64_t items = (int64_t)p.batch * p.n_chunks * p.num_kv_heads * p.hblocks;
+  const int64_t pairs = (int64_t)p.batch * p.n_chunks;
+  const int64_t vheads = (int64_t)p.num_kv_heads * p.hblocks;
+  // with the work list (p.plan, from pa_decode), XCD x runs ranks x, x + 8, ...
+  const int64_t items = p.plan ? (pairs + 7) / 8 * 8 * vheads : pairs * vheads;
   if (items > 0x7fffffff)
     return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)items);
   if (items > 0) {
@@ -643,9 +658,9 @@ int decode_any_launch(const char* name, const DecodeParams& prm, int head_dim, h
     const int rc = launch_status(name);
     if (rc) return rc;
   }
-  const int64_t pairs = (int64_t)p.batch * p.num_heads;
-  if (pairs > 0) {
-    decode_any_merge_kernel<<<dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s>>>(p, head_dim);
+  const int64_t rows = (int64_t)p.batch * p.num_heads;  // (sequence, q head) pairs
+  if (rows > 0) {
+    decode_any_merge_kernel<<<dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s>>>(p, head_dim);
     return launch_status(name);
   }
   return PA_OK;

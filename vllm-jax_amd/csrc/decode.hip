@@ -277,9 +277,10 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
   prm.zero_empty = 0;
 
   hipStream_t s = (hipStream_t)stream;
-  if (any_d) return decode_any_launch(name, prm, head_dim, s, fp8 ? code : -1);
   const int64_t pairs = (int64_t)batch * prm.n_chunks;
-  const int64_t vheads = (int64_t)num_kv_heads * prm.hblocks;  // work items per (sequence, chunk)
+  // work items per (sequence, chunk): one per kv head and block of q heads
+  // (16 per item here, 32 in the generic kernels)
+  const int64_t vheads = (int64_t)num_kv_heads * (any_d ? (group + 31) / 32 : prm.hblocks);
   // The work list pays for its launch once the grid is several waves of
   // workgroups deep (two per CU, 256 CUs).
   const bool planned = pairs > 0 && pairs * vheads >= kDecodePlanMinItems;
@@ -294,6 +295,7 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
     if (rc) return rc;
     prm.plan = plan;
   }
+  if (any_d) return decode_any_launch(name, prm, head_dim, s, fp8 ? code : -1);
   if (blocks > 0) {  // no table pages: every row is zero, only the merge pass runs
     const bool aligned = page_size % kDecodeStep == 0;
     const bool cap = prm.soft_cap > 0.f;
