@@ -35,6 +35,12 @@ namespace {
 // Prefill waves per workgroup (32 q rows each): 8 while the registers allow
 // two waves per SIMD (head sizes up to 112), else 4.
 __host__ __device__ constexpr int any_prefill_waves(int d) { return d <= 112 ? 8 : 4; }
+// Up to head size 64 the prefill's registers are capped at 128 per lane
+// (four waves per SIMD), so two workgroups share a CU; from 80 on the cap
+// would spill.  With one workgroup per CU (four waves, from head size 144
+// on) the page ids of a step are read a step ahead (see prefill_any_kernel).
+__host__ __device__ constexpr int any_prefill_wpe(int d) { return d <= 64 ? 4 : 1; }
+__host__ __device__ constexpr bool any_pages_ahead(int d) { return any_prefill_waves(d) == 4; }
 constexpr int kAnyStep = 32;                 // kv tokens per step (the MFMA's M)
 
 template <int D>
@@ -43,10 +49,24 @@ struct AnyDims {
   static constexpr int kKs = D / 16;         // k-steps of S = K Q^T
   static constexpr int kDt = (D + 31) / 32;  // 32-row blocks of O^T
   static constexpr int kChunks = D / 8;      // 16-byte chunks of a K / V row
-  static constexpr int kRow = 2 * D + 16;    // bytes per K / V row in LDS (16 bytes of padding)
-  // the V tile: the last rows' V^T operands of a partial 32-row block read
-  // up to 16 bytes past the tile
-  static constexpr int kVTile = kAnyStep * kRow + 32;
+  // Bytes per K row in LDS: 16 bytes of padding put the 16 rows a K read
+  // serves per pass (16 bytes each) on distinct banks.
+  static constexpr int kRow = 2 * D + 16;
+  // Bytes per V row: a transposing V^T read serves 32 lanes per pass, 4 rows
+  // x 8 columns x 2 bytes wide and two 16-column groups; with a row stride of
+  // 64 or 192 mod 256 bytes the 4 rows land on 4 disjoint quarters of the 64
+  // banks (a stride of 2D + 16 put 2 to 4 lanes on a bank).  The smallest
+  // padding of 0 / 32 / 64 / 96 bytes that gives it, which also keeps the
+  // widest V^T operand (64 * kDt bytes from a row's start) inside its row.
+  static constexpr int vpad() {
+    for (int pad = 0; pad <= 96; pad += 32)
+      if ((2 * D + pad) % 256 == 64 || (2 * D + pad) % 256 == 192) return pad;
+    return 32;  // D = 16 (32-byte rows)
+  }
+  static constexpr int kVRow = 2 * D + vpad();
+  static_assert(64 * kDt <= kVRow, "V^T operands stay inside their row");
+  // the V tile, with 32 bytes of slack past its last row
+  static constexpr int kVTile = kAnyStep * kVRow + 32;
 };
 
 typedef char __attribute__((address_space(3))) lds_char;
@@ -170,7 +190,7 @@ __device__ __forceinline__ void any_softmax_pv(const f32x16& s, float& m_run, fl
 // waves share the step's K and V tiles (row-major); the next step's
 // K / V chunks are loaded into registers while this step computes.
 template <int D, bool kSoftCap>
-__global__ void __launch_bounds__(64 * any_prefill_waves(D))
+__global__ void __launch_bounds__(64 * any_prefill_waves(D)) __attribute__((amdgpu_waves_per_eu(any_prefill_wpe(D))))
 prefill_any_kernel(PrefillParams p) {
   using A = AnyDims<D>;
   constexpr int kAnyWaves = any_prefill_waves(D);
@@ -224,6 +244,23 @@ prefill_any_kernel(PrefillParams p) {
   const int32_t* bt_row = p.block_tables + (int64_t)w.b * p.bt_stride;
   const int64_t head_off = (int64_t)w.kvh * p.head_stride;
   u32x4 kr[kPer], vr[kPer];
+  // kAhead: the page ids of a step's chunks are read one step before its K /
+  // V loads (pages()), so that no K / V load waits on its block-table read:
+  // with a single workgroup per CU nothing else hides that second latency.
+  // Otherwise load() reads them itself (fewer live registers).
+  constexpr bool kAhead = any_pages_ahead(D);
+  int32_t pg[kAhead ? kPer : 1];
+  auto pages = [&](int j0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = tid + kThreads * i;
+      if (c < kStepChunks) {
+        // tokens past the kv length read the last valid one (masked below)
+        const int j = min(j0 + c / A::kChunks, w.lk - 1);
+        pg[i] = safe_page(bt_row, j / p.page_size, p.num_pages);
+      }
+    }
+  };
   auto load = [&](int j0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
@@ -233,8 +270,11 @@ prefill_any_kernel(PrefillParams p) {
         const int e = c - t * A::kChunks;
         // tokens past the kv length read the last valid one (masked below)
         const int j = min(j0 + t, w.lk - 1);
-        const int64_t off = (int64_t)safe_page(bt_row, j / p.page_size, p.num_pages) * p.page_stride +
-                            (int64_t)(j % p.page_size) * p.slot_stride + head_off + 8 * e;
+        int32_t page;
+        if constexpr (kAhead) page = pg[i];
+        else page = safe_page(bt_row, j / p.page_size, p.num_pages);
+        const int64_t off =
+            (int64_t)page * p.page_stride + (int64_t)(j % p.page_size) * p.slot_stride + head_off + 8 * e;
         kr[i] = ld16(p.k_cache + off);
         vr[i] = ld16(p.v_cache + off);
       }
@@ -248,7 +288,7 @@ prefill_any_kernel(PrefillParams p) {
         const int t = c / A::kChunks;
         const int e = c - t * A::kChunks;
         lds_st16(k_tile + t * A::kRow + 16 * e, kr[i]);
-        lds_st16(v_tile + t * A::kRow + 16 * e, vr[i]);
+        lds_st16(v_tile + t * A::kVRow + 16 * e, vr[i]);
       }
     }
   };
@@ -257,13 +297,26 @@ prefill_any_kernel(PrefillParams p) {
 #pragma unroll
   for (int dt = 0; dt < A::kDt; ++dt) acc[dt] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
-  if (n_steps > 0) load(0);
+  // kAhead: every step loads the next step's K / V and the page ids of the
+  // one after, also past the last step (the token index is clamped, so those
+  // loads read real rows, never used): loads under a branch would make the
+  // compiler wait for them where the branch joins.
+  if (n_steps > 0) {
+    if constexpr (kAhead) pages(0);
+    load(0);
+    if constexpr (kAhead) pages(kAnyStep);
+  }
   for (int st = 0; st < n_steps; ++st) {
     __syncthreads();  // every wave is done with the previous step's tiles
     store();
     __syncthreads();
     const int j0 = st * kAnyStep;
-    if (st + 1 < n_steps) load(j0 + kAnyStep);
+    if constexpr (kAhead) {
+      load(j0 + kAnyStep);
+      pages(j0 + 2 * kAnyStep);
+    } else if (st + 1 < n_steps) {
+      load(j0 + kAnyStep);
+    }
     f32x16 s = {};
 #pragma unroll
     for (int ks = 0; ks < A::kKs; ++ks)
@@ -278,7 +331,7 @@ prefill_any_kernel(PrefillParams p) {
         s[i] = j < w.lk && (int64_t)j + w.kv_pos_off <= qpos ? s[i] : -INFINITY;
       }
     }
-    any_softmax_pv<A::kDt, A::kRow, true>(s, m_run, l_run, acc, v_tile, lane);
+    any_softmax_pv<A::kDt, A::kVRow, true>(s, m_run, l_run, acc, v_tile, lane);
   }
   // a row that sees no key (its position precedes the sequence's first kv
   // position) is written as zeros
@@ -362,7 +415,7 @@ decode_any_kernel(DecodeParams p, int code) {
   constexpr int kPer = kTok * A::kChunks / 64;      // chunks of K (and of V) per lane and batch
   constexpr bool kPrefetch = kSoftCap ? D <= 192 : D <= 224;
   __shared__ __attribute__((aligned(16))) char k_tile_g[kTok * A::kRow];
-  __shared__ __attribute__((aligned(16))) char v_tile_g[kTok * A::kRow + 32];  // V^T operands read 16 bytes past
+  __shared__ __attribute__((aligned(16))) char v_tile_g[kTok * A::kVRow + 32];
   __shared__ __attribute__((aligned(16))) float ksc_g[kQuant ? kTok : 4], vsc_g[kQuant ? kTok : 4];
   lds_char* k_tile = (lds_char*)k_tile_g;
   lds_char* v_tile = (lds_char*)v_tile_g;
@@ -461,10 +514,10 @@ decode_any_kernel(DecodeParams p, int code) {
       const int e = c - t * A::kChunks;
       if constexpr (kQuant) {
         lds_st16(k_tile + t * A::kRow + 16 * e, codes8_to_bf16x8_rt(kr[i], code));
-        lds_st16(v_tile + t * A::kRow + 16 * e, codes8_to_bf16x8_rt(vr[i], code));
+        lds_st16(v_tile + t * A::kVRow + 16 * e, codes8_to_bf16x8_rt(vr[i], code));
       } else {
         lds_st16(k_tile + t * A::kRow + 16 * e, kr[i]);
-        lds_st16(v_tile + t * A::kRow + 16 * e, vr[i]);
+        lds_st16(v_tile + t * A::kVRow + 16 * e, vr[i]);
       }
     }
     if constexpr (kQuant) {
@@ -507,7 +560,7 @@ decode_any_kernel(DecodeParams p, int code) {
           s[i] = j < t1 ? any_logit_f32<kSoftCap>(kQuant ? s[i] * ksc[i] : s[i], p.logit_scale, p.soft_cap)
                         : -INFINITY;
         }
-        any_softmax_pv<A::kDt, A::kRow, false, kQuant>(s, m_run, l_run, acc, v_tile + kAnyStep * sub * A::kRow,
+        any_softmax_pv<A::kDt, A::kVRow, false, kQuant>(s, m_run, l_run, acc, v_tile + kAnyStep * sub * A::kVRow,
                                                        lane, vsc);
       }
     }
