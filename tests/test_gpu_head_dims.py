@@ -35,6 +35,9 @@ TOL = 2e-2
     ([90, 300], 40, 2, 32, 16),               # G = 20, d = 16
     ([70, 33], 64, 1, 48, 48),                # G = 64 (one kv head), d = 48
     ([120], 8, 8, 128, 240),                  # MHA, d = 240
+    ([100, 45], 16, 8, 8, 64),                # 8-token pages: paged per lane (below 16)
+    ([77, 130], 16, 4, 4, 256),               # 4-token pages at d = 256
+    ([50, 200], 32, 8, 17, 96),               # 17-token pages: a 32-token step spans up to 3 pages
 ])
 def test_prefill_head_dims(pkg, dev, lens, h, hkv, bs, d):
     pb = wl.make_prefill(lens, num_heads=h, num_kv_heads=hkv, page_size=bs, head_dim=d,

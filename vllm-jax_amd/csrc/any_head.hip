@@ -189,7 +189,10 @@ __device__ __forceinline__ void any_softmax_pv(const f32x16& s, float& m_run, fl
 // of wave w is token row / G, head row % G of the kv head's group.  All
 // waves share the step's K and V tiles (row-major); the next step's
 // K / V chunks are loaded into registers while this step computes.
-template <int D, bool kSoftCap>
+// kPaged3: pages of at least 16 tokens, so a 32-token step (clamped to the
+// kv length) lies in at most three consecutive table entries: the step is
+// paged once, with uniform values, instead of per lane and chunk.
+template <int D, bool kSoftCap, bool kPaged3>
 __global__ void __launch_bounds__(64 * any_prefill_waves(D)) __attribute__((amdgpu_waves_per_eu(any_prefill_wpe(D))))
 prefill_any_kernel(PrefillParams p) {
   using A = AnyDims<D>;
@@ -244,9 +247,48 @@ prefill_any_kernel(PrefillParams p) {
   const int32_t* bt_row = p.block_tables + (int64_t)w.b * p.bt_stride;
   const int64_t head_off = (int64_t)w.kvh * p.head_stride;
   u32x4 kr[kPer], vr[kPer];
-  // kAhead: the page ids of a step's chunks are read one step before its K /
-  // V loads (pages()), so that no K / V load waits on its block-table read:
-  // with a single workgroup per CU nothing else hides that second latency.
+  // kPaged3: step_pages() reads the step's (up to) three page ids with
+  // scalar loads, a step before its K / V loads, and turns them into scalar
+  // row bases; a lane then finds its row with two compares and a select
+  // (per chunk: no division by the page size, no block-table load, no 64-bit
+  // multiply by the page stride).  For the next step to load: the in-page
+  // offset of its first (clamped) token, and the element offsets of table
+  // entries lp0 .. lp0 + 2 for this kv head; plain scalars, so that nothing
+  // is placed in an array in memory.
+  int sp_off0 = 0;
+  int64_t sp_b0 = 0, sp_b1 = 0, sp_b2 = 0;
+  auto step_pages = [&](int j0) __attribute__((always_inline)) {
+    const int jc0 = min(j0, w.lk - 1);
+    const int lp0 = __builtin_amdgcn_readfirstlane(jc0 / p.page_size);
+    sp_off0 = __builtin_amdgcn_readfirstlane(jc0 - lp0 * p.page_size);
+    // entries past the table row are never selected: the index is clamped
+    const int last = p.pages_per_seq - 1;
+    sp_b0 = (int64_t)safe_page_scalar(bt_row, min(lp0, last), p.num_pages) * p.page_stride + head_off;
+    sp_b1 = (int64_t)safe_page_scalar(bt_row, min(lp0 + 1, last), p.num_pages) * p.page_stride + head_off;
+    sp_b2 = (int64_t)safe_page_scalar(bt_row, min(lp0 + 2, last), p.num_pages) * p.page_stride + head_off;
+  };
+  auto load3 = [&](int j0, int off0, int64_t b0, int64_t b1, int64_t b2) __attribute__((always_inline)) {
+    const int jc0 = min(j0, w.lk - 1);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int c = tid + kThreads * i;
+      if (c < kStepChunks) {
+        const int t = c / A::kChunks;
+        const int e = c - t * A::kChunks;
+        // token min(j0 + t, lk - 1) = lp0 * page_size + x, x < 3 * page_size
+        const int x = off0 + (min(j0 + t, w.lk - 1) - jc0);
+        const int q = (x >= p.page_size ? 1 : 0) + (x >= 2 * p.page_size ? 1 : 0);
+        const int64_t base = q == 0 ? b0 : (q == 1 ? b1 : b2);
+        const int64_t off = base + (int64_t)(x - q * p.page_size) * p.slot_stride + 8 * e;
+        kr[i] = ld16(p.k_cache + off);
+        vr[i] = ld16(p.v_cache + off);
+      }
+    }
+  };
+  // Page sizes below 16 (!kPaged3): per lane and chunk.  kAhead: the page
+  // ids of a step's chunks are read one step before its K / V loads
+  // (pages()), so that no K / V load waits on its block-table read: with a
+  // single workgroup per CU nothing else hides that second latency.
   // Otherwise load() reads them itself (fewer live registers).
   constexpr bool kAhead = any_pages_ahead(D);
   int32_t pg[kAhead ? kPer : 1];
@@ -297,21 +339,30 @@ prefill_any_kernel(PrefillParams p) {
 #pragma unroll
   for (int dt = 0; dt < A::kDt; ++dt) acc[dt] = f32x16{};
   float m_run = -INFINITY, l_run = 0.f;
-  // kAhead: every step loads the next step's K / V and the page ids of the
-  // one after, also past the last step (the token index is clamped, so those
-  // loads read real rows, never used): loads under a branch would make the
-  // compiler wait for them where the branch joins.
+  // kPaged3 and kAhead: every step loads the next step's K / V and the page
+  // ids of the one after, also past the last step (the token index is
+  // clamped, so those loads read real rows, never used): loads under a
+  // branch would make the compiler wait for them where the branch joins.
   if (n_steps > 0) {
-    if constexpr (kAhead) pages(0);
-    load(0);
-    if constexpr (kAhead) pages(kAnyStep);
+    if constexpr (kPaged3) {
+      step_pages(0);
+      load3(0, sp_off0, sp_b0, sp_b1, sp_b2);
+      step_pages(kAnyStep);
+    } else {
+      if constexpr (kAhead) pages(0);
+      load(0);
+      if constexpr (kAhead) pages(kAnyStep);
+    }
   }
   for (int st = 0; st < n_steps; ++st) {
     __syncthreads();  // every wave is done with the previous step's tiles
     store();
     __syncthreads();
     const int j0 = st * kAnyStep;
-    if constexpr (kAhead) {
+    if constexpr (kPaged3) {
+      load3(j0 + kAnyStep, sp_off0, sp_b0, sp_b1, sp_b2);
+      step_pages(j0 + 2 * kAnyStep);
+    } else if constexpr (kAhead) {
       load(j0 + kAnyStep);
       pages(j0 + 2 * kAnyStep);
     } else if (st + 1 < n_steps) {
@@ -664,11 +715,14 @@ int prefill_any_launch(const char* name, const PrefillParams& prm, int head_dim,
     return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)items);
   const dim3 g((unsigned)items), blk(64 * waves);
   const bool cap = p.soft_cap > 0.f;
+  const bool paged3 = p.page_size >= 16;
   switch (head_dim) {
-#define PA_ANY_LAUNCH(d)                                             \
-  case d:                                                            \
-    if (cap) prefill_any_kernel<d, true><<<g, blk, 0, s>>>(p);       \
-    else prefill_any_kernel<d, false><<<g, blk, 0, s>>>(p);          \
+#define PA_ANY_LAUNCH(d)                                                              \
+  case d:                                                                             \
+    if (cap && paged3) prefill_any_kernel<d, true, true><<<g, blk, 0, s>>>(p);        \
+    else if (cap) prefill_any_kernel<d, true, false><<<g, blk, 0, s>>>(p);            \
+    else if (paged3) prefill_any_kernel<d, false, true><<<g, blk, 0, s>>>(p);         \
+    else prefill_any_kernel<d, false, false><<<g, blk, 0, s>>>(p);                    \
     break;
     PA_ANY_DIMS(PA_ANY_LAUNCH)
 #undef PA_ANY_LAUNCH
