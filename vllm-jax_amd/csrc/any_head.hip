@@ -437,6 +437,9 @@ prefill_any_zero_kernel(PrefillParams p, int head_dim) {
 // Whole 128-byte lines per K / V row (head sizes multiple of 64): the
 // generic decode can stream its K / V loads past the caches.
 __host__ __device__ constexpr bool any_decode_streamable(int d) { return d % 64 == 0; }
+// Tokens per load batch of the generic decode: up to head size 64 two
+// 32-token steps (more bytes in flight per wave for one wave less per SIMD).
+__host__ __device__ constexpr int any_decode_batch(int d) { return d <= 64 ? 2 * kAnyStep : kAnyStep; }
 
 // Eight 1-byte codes of type `code` (uniform over the launch) to bf16, exactly.
 __device__ __forceinline__ u32x4 codes8_to_bf16x8_rt(const u32x2& c, int code) {
@@ -453,7 +456,10 @@ __device__ __forceinline__ u32x4 codes8_to_bf16x8_rt(const u32x2& c, int code) {
 // staged, so the tiles and the MFMAs are those of bf16 pages; the step's
 // scales are staged beside them.  As in the tuned decode, the logit of token
 // j is (q . k_j) * k_scale_j, and P is rounded to bf16 as p * v_scale_j.
-template <int D, bool kSoftCap, bool kStream, bool kQuant = false>
+// kPaged3: pages of at least half a load batch (any_decode_batch), so a
+// batch (clamped to the chunk) lies in at most three consecutive table
+// entries, paged once per batch with scalar loads as in the prefill.
+template <int D, bool kSoftCap, bool kStream, bool kQuant, bool kPaged3>
 __global__ void __launch_bounds__(64)
 decode_any_kernel(DecodeParams p, int code) {
   using A = AnyDims<D>;
@@ -461,8 +467,8 @@ decode_any_kernel(DecodeParams p, int code) {
   // flight per wave for one wave less per SIMD); the next batch is loaded
   // while this one computes, up to the head size whose registers still allow
   // it without spills.
-  constexpr int kSub = D <= 64 ? 2 : 1;
-  constexpr int kTok = kAnyStep * kSub;             // tokens per load batch
+  constexpr int kTok = any_decode_batch(D);         // tokens per load batch
+  constexpr int kSub = kTok / kAnyStep;
   constexpr int kPer = kTok * A::kChunks / 64;      // chunks of K (and of V) per lane and batch
   constexpr bool kPrefetch = kSoftCap ? D <= 192 : D <= 224;
   __shared__ __attribute__((aligned(16))) char k_tile_g[kTok * A::kRow];
@@ -519,6 +525,28 @@ decode_any_kernel(DecodeParams p, int code) {
   Raw kr[kPer], vr[kPer];
   float ksr = 0.f, vsr = 0.f;  // (kQuant) scales of token lane % kTok of the batch
   auto load = [&](int j0) __attribute__((always_inline)) {
+    // (kPaged3) the batch's first (clamped) token is table entry lp0, offset
+    // off0; entries lp0 .. lp0 + 2 as scalar element (and scale) offsets
+    const int jc0 = min(j0, t1 - 1);
+    int off0 = 0;
+    int64_t b0 = 0, b1 = 0, b2 = 0, s0 = 0, s1 = 0, s2 = 0;
+    if constexpr (kPaged3) {
+      const int lp0 = __builtin_amdgcn_readfirstlane(jc0 / p.page_size);
+      off0 = __builtin_amdgcn_readfirstlane(jc0 - lp0 * p.page_size);
+      const int last = p.pages_per_seq - 1;  // entries past the row are never selected
+      const int64_t g0 = safe_page_scalar(bt_row, min(lp0, last), p.num_pages);
+      const int64_t g1 = safe_page_scalar(bt_row, min(lp0 + 1, last), p.num_pages);
+      const int64_t g2 = safe_page_scalar(bt_row, min(lp0 + 2, last), p.num_pages);
+      b0 = g0 * p.page_stride + head_off;
+      b1 = g1 * p.page_stride + head_off;
+      b2 = g2 * p.page_stride + head_off;
+      if constexpr (kQuant) {
+        const int64_t sh = (int64_t)kvh * p.sc_head_stride;
+        s0 = g0 * p.sc_page_stride + sh;
+        s1 = g1 * p.sc_page_stride + sh;
+        s2 = g2 * p.sc_page_stride + sh;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int c = lane + 64 * i;
@@ -526,8 +554,15 @@ decode_any_kernel(DecodeParams p, int code) {
       const int e = c - t * A::kChunks;
       // tokens past the chunk read its last token (masked below)
       const int j = min(j0 + t, t1 - 1);
-      const int64_t off = (int64_t)safe_page(bt_row, j / p.page_size, p.num_pages) * p.page_stride +
-                          (int64_t)(j % p.page_size) * p.slot_stride + head_off + 8 * e;
+      int64_t off;
+      if constexpr (kPaged3) {
+        const int x = off0 + (j - jc0);  // j = lp0 * page_size + x, x < 3 * page_size
+        const int q = (x >= p.page_size ? 1 : 0) + (x >= 2 * p.page_size ? 1 : 0);
+        off = (q == 0 ? b0 : (q == 1 ? b1 : b2)) + (int64_t)(x - q * p.page_size) * p.slot_stride + 8 * e;
+      } else {
+        off = (int64_t)safe_page(bt_row, j / p.page_size, p.num_pages) * p.page_stride +
+              (int64_t)(j % p.page_size) * p.slot_stride + head_off + 8 * e;
+      }
       if constexpr (kQuant) {
         kr[i] = *reinterpret_cast<const u32x2*>(p.k8 + off);
         vr[i] = *reinterpret_cast<const u32x2*>(p.v8 + off);
@@ -543,8 +578,15 @@ decode_any_kernel(DecodeParams p, int code) {
       // past the chunk: the scales of its last token (a real one; those
       // tokens are masked, so their p is 0)
       const int j = min(j0 + (lane & (kTok - 1)), t1 - 1);
-      const int64_t si = (int64_t)safe_page(bt_row, j / p.page_size, p.num_pages) * p.sc_page_stride +
-                         (int64_t)kvh * p.sc_head_stride + j % p.page_size;
+      int64_t si;
+      if constexpr (kPaged3) {
+        const int x = off0 + (j - jc0);
+        const int q = (x >= p.page_size ? 1 : 0) + (x >= 2 * p.page_size ? 1 : 0);
+        si = (q == 0 ? s0 : (q == 1 ? s1 : s2)) + (x - q * p.page_size);
+      } else {
+        si = (int64_t)safe_page(bt_row, j / p.page_size, p.num_pages) * p.sc_page_stride +
+             (int64_t)kvh * p.sc_head_stride + j % p.page_size;
+      }
       ksr = p.k_scales[si];
       vsr = p.v_scales[si];
     }
@@ -747,18 +789,27 @@ int decode_any_launch(const char* name, const DecodeParams& prm, int head_dim, h
     // one block of q heads per kv head: every K / V row is read once
     const bool stream = p.hblocks == 1;
     const bool quant = code >= 0;
+    // a load batch spans at most three pages
+    const bool paged3 = 2 * p.page_size >= any_decode_batch(head_dim);
     switch (head_dim) {
-#define PA_ANY_LAUNCH(d)                                                                          \
-  case d:                                                                                         \
-    if (quant && cap) decode_any_kernel<d, true, false, true><<<g, blk, 0, s>>>(p, code);         \
-    else if (quant) decode_any_kernel<d, false, false, true><<<g, blk, 0, s>>>(p, code);          \
-    else if (cap && stream) decode_any_kernel<d, true, any_decode_streamable(d)><<<g, blk, 0, s>>>(p, 0);   \
-    else if (cap) decode_any_kernel<d, true, false><<<g, blk, 0, s>>>(p, 0);                       \
-    else if (stream) decode_any_kernel<d, false, any_decode_streamable(d)><<<g, blk, 0, s>>>(p, 0);  \
-    else decode_any_kernel<d, false, false><<<g, blk, 0, s>>>(p, 0);                               \
+#define PA_ANY_DECODE(d, P)                                                                              \
+    if (quant && cap) decode_any_kernel<d, true, false, true, P><<<g, blk, 0, s>>>(p, code);             \
+    else if (quant) decode_any_kernel<d, false, false, true, P><<<g, blk, 0, s>>>(p, code);              \
+    else if (cap && stream) decode_any_kernel<d, true, any_decode_streamable(d), false, P><<<g, blk, 0, s>>>(p, 0);  \
+    else if (cap) decode_any_kernel<d, true, false, false, P><<<g, blk, 0, s>>>(p, 0);                   \
+    else if (stream) decode_any_kernel<d, false, any_decode_streamable(d), false, P><<<g, blk, 0, s>>>(p, 0); \
+    else decode_any_kernel<d, false, false, false, P><<<g, blk, 0, s>>>(p, 0);
+#define PA_ANY_LAUNCH(d)     \
+  case d:                    \
+    if (paged3) {            \
+      PA_ANY_DECODE(d, true) \
+    } else {                 \
+      PA_ANY_DECODE(d, false)\
+    }                        \
     break;
       PA_ANY_DIMS(PA_ANY_LAUNCH)
 #undef PA_ANY_LAUNCH
+#undef PA_ANY_DECODE
       default:
         return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported", name, head_dim);
     }
