@@ -71,6 +71,17 @@ struct AnyDims {
 
 typedef char __attribute__((address_space(3))) lds_char;
 
+// Whether chunk c = tid + kThreads * i (i < kPer) of a step's kChunks
+// exists.  Only the last i can fail, and none does when kChunks is a
+// multiple of kThreads: a plain c < kChunks would leave a divergent branch
+// around every chunk's load and LDS write (the compiler does not know the
+// thread index is below kThreads), which keeps it from scheduling across
+// them.
+template <int kChunks, int kThreads, int kPer>
+__device__ __forceinline__ bool any_chunk_live(int i, int c) {
+  return kChunks % kThreads == 0 || i + 1 < kPer || c < kChunks;
+}
+
 // A operand of V^T for rows d0 .. d0 + 31 and k-step u from the row-major
 // V tile (rows of `row` bytes): lane (m, h) takes d = d0 + m of the tokens
 // 16u + 4h + {0,1,2,3} and 16u + 8 + 4h + {0,1,2,3}, in two transposing
@@ -272,7 +283,7 @@ prefill_any_kernel(PrefillParams p) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int c = tid + kThreads * i;
-      if (c < kStepChunks) {
+      if (any_chunk_live<kStepChunks, kThreads, kPer>(i, c)) {
         const int t = c / A::kChunks;
         const int e = c - t * A::kChunks;
         // token min(j0 + t, lk - 1) = lp0 * page_size + x, x < 3 * page_size
@@ -296,7 +307,7 @@ prefill_any_kernel(PrefillParams p) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int c = tid + kThreads * i;
-      if (c < kStepChunks) {
+      if (any_chunk_live<kStepChunks, kThreads, kPer>(i, c)) {
         // tokens past the kv length read the last valid one (masked below)
         const int j = min(j0 + c / A::kChunks, w.lk - 1);
         pg[i] = safe_page(bt_row, j / p.page_size, p.num_pages);
@@ -307,7 +318,7 @@ prefill_any_kernel(PrefillParams p) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int c = tid + kThreads * i;
-      if (c < kStepChunks) {
+      if (any_chunk_live<kStepChunks, kThreads, kPer>(i, c)) {
         const int t = c / A::kChunks;
         const int e = c - t * A::kChunks;
         // tokens past the kv length read the last valid one (masked below)
@@ -326,7 +337,7 @@ prefill_any_kernel(PrefillParams p) {
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
       const int c = tid + kThreads * i;
-      if (c < kStepChunks) {
+      if (any_chunk_live<kStepChunks, kThreads, kPer>(i, c)) {
         const int t = c / A::kChunks;
         const int e = c - t * A::kChunks;
         lds_st16(k_tile + t * A::kRow + 16 * e, kr[i]);
@@ -759,12 +770,12 @@ int prefill_any_launch(const char* name, const PrefillParams& prm, int head_dim,
   const bool cap = p.soft_cap > 0.f;
   const bool paged3 = p.page_size >= 16;
   switch (head_dim) {
-#define PA_ANY_LAUNCH(d)                                                              \
-  case d:                                                                             \
-    if (cap && paged3) prefill_any_kernel<d, true, true><<<g, blk, 0, s>>>(p);        \
-    else if (cap) prefill_any_kernel<d, true, false><<<g, blk, 0, s>>>(p);            \
-    else if (paged3) prefill_any_kernel<d, false, true><<<g, blk, 0, s>>>(p);         \
-    else prefill_any_kernel<d, false, false><<<g, blk, 0, s>>>(p);                    \
+#define PA_ANY_LAUNCH(d)                                                                       \
+  case d:                                                                                      \
+    if (cap && paged3) prefill_any_kernel<d, true, true><<<g, blk, 0, s>>>(p);                 \
+    else if (cap) prefill_any_kernel<d, true, false><<<g, blk, 0, s>>>(p);                     \
+    else if (paged3) prefill_any_kernel<d, false, true><<<g, blk, 0, s>>>(p);                  \
+    else prefill_any_kernel<d, false, false><<<g, blk, 0, s>>>(p);                             \
     break;
     PA_ANY_DIMS(PA_ANY_LAUNCH)
 #undef PA_ANY_LAUNCH
