@@ -140,6 +140,46 @@ __device__ __forceinline__ float any_logit_f32(float x, float logit_scale, float
 
 constexpr float kAnySlack = 8.f;  // lazy rescale: the reference max moves when a row max exceeds it by more
 
+// The lazy reference max of the prefill: the column's reference m_run
+// moves (and O and l are rescaled) only when some column of the wave
+// exceeds its own by more than the slack; called when that holds for the
+// step's row max mx.
+template <int kDt>
+__device__ __forceinline__ void any_lazy_rescale(float mx, float& m_run, float& l_run, f32x16 (&acc)[kDt]) {
+  const float m_new = fmaxf(m_run, mx);
+  const float corr = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
+  m_run = m_new;
+  l_run *= corr;
+#pragma unroll
+  for (int dt = 0; dt < kDt; ++dt) acc[dt] = acc[dt] * corr;
+}
+
+// P of one step's logits relative to the reference max (lazy form: l and O
+// already at m_run), its row sum into l_run, and O^T += V^T P^T from the
+// staged V tile.
+template <int kDt, int kRowBytes>
+__device__ __forceinline__ void any_p_pv(const f32x16& s, float m_run, float& l_run, f32x16 (&acc)[kDt],
+                                         const lds_char* v, int lane) {
+  const float ms = m_run == -INFINITY ? 0.f : m_run;  // a column that has seen no key yet keeps P = 0
+  float ls = 0.f;
+  u32x4 pw[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float a = fast_exp2(s[8 * u + 2 * e] - ms);
+      const float b = fast_exp2(s[8 * u + 2 * e + 1] - ms);
+      pw[u][e] = pack_bf16x2(a, b);
+      ls += a + b;
+    }
+  l_run = l_run + ls;
+#pragma unroll
+  for (int dt = 0; dt < kDt; ++dt)
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      acc[dt] = mfma32(as_bf16x8(vt_operand<kRowBytes>(v, 32 * dt, u, lane)), as_bf16x8(pw[u]), acc[dt]);
+}
+
 // Online softmax of one step's logits `s` (masked ones -inf) for the lane's
 // column, then O^T += V^T P^T from the staged V tile.
 // kLazy: move the reference only past the slack (prefill, where the VALU
@@ -266,19 +306,31 @@ prefill_any_kernel(PrefillParams p) {
   // offset of its first (clamped) token, and the element offsets of table
   // entries lp0 .. lp0 + 2 for this kv head; plain scalars, so that nothing
   // is placed in an array in memory.
+  // The raw table entries are clamped and turned into row bases only when
+  // the step is loaded (a step later): used at once, the scalar loads would
+  // be waited for where they are issued.
   int sp_off0 = 0;
-  int64_t sp_b0 = 0, sp_b1 = 0, sp_b2 = 0;
+  int32_t sp_g0 = 0, sp_g1 = 0, sp_g2 = 0;  // raw table entries lp0 .. lp0 + 2
   auto step_pages = [&](int j0) __attribute__((always_inline)) {
     const int jc0 = min(j0, w.lk - 1);
     const int lp0 = __builtin_amdgcn_readfirstlane(jc0 / p.page_size);
     sp_off0 = __builtin_amdgcn_readfirstlane(jc0 - lp0 * p.page_size);
     // entries past the table row are never selected: the index is clamped
     const int last = p.pages_per_seq - 1;
-    sp_b0 = (int64_t)safe_page_scalar(bt_row, min(lp0, last), p.num_pages) * p.page_stride + head_off;
-    sp_b1 = (int64_t)safe_page_scalar(bt_row, min(lp0 + 1, last), p.num_pages) * p.page_stride + head_off;
-    sp_b2 = (int64_t)safe_page_scalar(bt_row, min(lp0 + 2, last), p.num_pages) * p.page_stride + head_off;
+    const __attribute__((address_space(4))) int32_t* c = (const __attribute__((address_space(4))) int32_t*)bt_row;
+    sp_g0 = c[min(lp0, last)];
+    sp_g1 = c[min(lp0 + 1, last)];
+    sp_g2 = c[min(lp0 + 2, last)];
   };
-  auto load3 = [&](int j0, int off0, int64_t b0, int64_t b1, int64_t b2) __attribute__((always_inline)) {
+  // (the entries come in by value: a select among captured references
+  // became an indexed access to the closure, which put it in scratch memory)
+  auto load3 = [&](int j0, int off0, int32_t g0, int32_t g1, int32_t g2) __attribute__((always_inline)) {
+    // the entries clamped into the pool, as safe_page does
+    auto base = [&](int32_t g) __attribute__((always_inline)) {
+      const int32_t pg = g < 0 ? 0 : (g >= p.num_pages ? p.num_pages - 1 : g);
+      return (int64_t)pg * p.page_stride + head_off;
+    };
+    const int64_t b0 = base(g0), b1 = base(g1), b2 = base(g2);
     const int jc0 = min(j0, w.lk - 1);
 #pragma unroll
     for (int i = 0; i < kPer; ++i) {
@@ -357,7 +409,7 @@ prefill_any_kernel(PrefillParams p) {
   if (n_steps > 0) {
     if constexpr (kPaged3) {
       step_pages(0);
-      load3(0, sp_off0, sp_b0, sp_b1, sp_b2);
+      load3(0, sp_off0, sp_g0, sp_g1, sp_g2);
       step_pages(kAnyStep);
     } else {
       if constexpr (kAhead) pages(0);
@@ -365,13 +417,16 @@ prefill_any_kernel(PrefillParams p) {
       if constexpr (kAhead) pages(kAnyStep);
     }
   }
-  for (int st = 0; st < n_steps; ++st) {
+  // A step: step_head() stages its tiles, issues the next loads, computes its
+  // masked logits into s and returns their row max; step_tail() takes P and PV.
+  f32x16 s;
+  auto step_head = [&](int st) __attribute__((always_inline)) {
     __syncthreads();  // every wave is done with the previous step's tiles
     store();
     __syncthreads();
     const int j0 = st * kAnyStep;
     if constexpr (kPaged3) {
-      load3(j0 + kAnyStep, sp_off0, sp_b0, sp_b1, sp_b2);
+      load3(j0 + kAnyStep, sp_off0, sp_g0, sp_g1, sp_g2);
       step_pages(j0 + 2 * kAnyStep);
     } else if constexpr (kAhead) {
       load(j0 + kAnyStep);
@@ -379,10 +434,21 @@ prefill_any_kernel(PrefillParams p) {
     } else if (st + 1 < n_steps) {
       load(j0 + kAnyStep);
     }
-    f32x16 s = {};
+    s = f32x16{};
 #pragma unroll
     for (int ks = 0; ks < A::kKs; ++ks)
       s = mfma32(as_bf16x8(lds_ld16(k_tile + n * A::kRow + 2 * (16 * ks + 8 * h))), qb[ks], s);
+    if constexpr (kAnyWaves == 4) {
+      // each K read four MFMAs ahead of the MFMA it feeds (left to itself
+      // the compiler issued them one or two ahead: nothing else on the SIMD
+      // hides the LDS latency)
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 4, 0);
+#pragma unroll
+      for (int i = 0; i < A::kKs; ++i) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+        if (i + 4 < A::kKs) __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 16; ++i) s[i] = any_logit<kSoftCap>(s[i], p.logit_scale, p.soft_cap);
     // a step below the length and below every row's causal limit needs no mask
@@ -393,7 +459,35 @@ prefill_any_kernel(PrefillParams p) {
         s[i] = j < w.lk && (int64_t)j + w.kv_pos_off <= qpos ? s[i] : -INFINITY;
       }
     }
-    any_softmax_pv<A::kDt, A::kVRow, true>(s, m_run, l_run, acc, v_tile, lane);
+    float mx = s[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+    return max_xor32(mx);
+  };
+  auto step_tail = [&]() __attribute__((always_inline)) { any_p_pv<A::kDt, A::kVRow>(s, m_run, l_run, acc, v_tile, lane); };
+  if constexpr (kAnyWaves == 4) {
+    // O lives in AGPRs here (with one wave per SIMD the registers allow it),
+    // and a rescale inside the loop made the compiler copy all of O into
+    // VGPRs on every step; the loop is left for the (rare) rescale instead.
+    int st = 0;
+    while (st < n_steps) {
+      float mx = step_head(st);
+      while (!__any(mx > m_run + kAnySlack)) {
+        step_tail();
+        if (++st >= n_steps) break;
+        mx = step_head(st);
+      }
+      if (st >= n_steps) break;
+      any_lazy_rescale(mx, m_run, l_run, acc);
+      step_tail();
+      ++st;
+    }
+  } else {
+    for (int st = 0; st < n_steps; ++st) {
+      const float mx = step_head(st);
+      if (__any(mx > m_run + kAnySlack)) any_lazy_rescale(mx, m_run, l_run, acc);
+      step_tail();
+    }
   }
   // a row that sees no key (its position precedes the sequence's first kv
   // position) is written as zeros
