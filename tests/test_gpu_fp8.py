@@ -507,6 +507,34 @@ def test_decode_quantized_pages_head_dims(pkg, dev, kind, lens, h, hkv, bs, d, c
     assert not got[np.asarray(lens) == 0].any()
 
 
+@pytest.mark.parametrize("kind", ["e4m3", "uint8"])
+def test_decode_quantized_pages_head_dim_work_list(pkg, dev, kind):
+    """Quantized pages at head size 96 in a batch that takes the decode work
+    list (640 sequences x 4 kv heads); every sequence against the oracle."""
+    import torch
+    rng = np.random.default_rng(77 + len(kind))
+    lens = rng.integers(0, 600, size=640)
+    lens[:4] = [0, 1, 64, 599]
+    bs, hkv, h, d = 64, 4, 16, 96
+    nb = sum((int(n) + bs - 1) // bs for n in lens) + 2
+    kq, vq, ks, vs = _code_pool(rng, nb, bs, hkv, d, kind)
+    bt = _tables_for(rng, lens, bs, nb, pow2_width=True)
+    q = _bf16(rng, (len(lens), h, d))
+    out = pkg.decode_paged_attention(from_u16(q, dev), _code_pages(kq, kind, dev), _code_pages(vq, kind, dev),
+                                     torch.as_tensor(bt, device=dev),
+                                     torch.as_tensor(np.asarray(lens, np.int32), device=dev),
+                                     k_scales_pages=torch.from_numpy(ks).to(dev),
+                                     v_scales_pages=torch.from_numpy(vs).to(dev))
+    torch.cuda.synchronize()
+    got = u16(out)
+    want = ora.decode_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, np.asarray(lens),
+                                k_scales_pages=ks, v_scales_pages=vs, code_type=kind)
+    err = np.abs(ora.bf16_to_f32(got) - ora.bf16_to_f32(want)).max()
+    print(f"{kind} decode d=96, work list: max-abs err {err:.3e}", flush=True)
+    assert err <= TOL
+    assert not got[lens == 0].any()
+
+
 @pytest.mark.parametrize("kind", ["e4m3", "int8", "uint8"])
 @pytest.mark.parametrize("lens,prefix,h,hkv,bs,d", [
     ([17, 128, 300, 511], [0, 0, 0, 0], 16, 8, 256, 64),   # the Qwen3-0.6B-sized batch at d = 64

@@ -104,6 +104,21 @@ def test_decode_head_dims(pkg, dev, lens, h, hkv, bs, d):
     assert not got[np.asarray(lens) == 0].any()
 
 
+@pytest.mark.parametrize("d", [64, 96, 256])
+def test_decode_head_dims_work_list(pkg, dev, d):
+    """A batch large enough for pa_decode's work list (640 sequences x 4 kv
+    heads: 2 560 items), which the generic decode then follows, ranks dealt
+    over the XCDs; every sequence against the oracle."""
+    rng = np.random.default_rng(40 + d)
+    lens = rng.integers(0, 700, size=640)
+    lens[:6] = [0, 1, 63, 64, 65, 699]
+    width = 1 << (max(-(-int(n) // 64) for n in lens) - 1).bit_length()
+    db = wl.make_decode(lens, num_heads=16, num_kv_heads=4, page_size=64, head_dim=d,
+                        rng=np.random.default_rng(41 + d), table_width=width)
+    out, _ = _run_and_check(pkg, dev, db, seed=6)
+    assert not ora.bf16_to_f32(u16(out))[lens == 0].any()
+
+
 def test_decode_head_dim_soft_cap(pkg, dev):
     db = wl.make_decode([40, 300, 2700], num_heads=16, num_kv_heads=8, page_size=256, head_dim=64,
                         rng=np.random.default_rng(4), table_width=16)
