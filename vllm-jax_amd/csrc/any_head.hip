@@ -37,8 +37,9 @@ namespace {
 __host__ __device__ constexpr int any_prefill_waves(int d) { return d <= 112 ? 8 : 4; }
 // Up to head size 64 the prefill's registers are capped at 128 per lane
 // (four waves per SIMD), so two workgroups share a CU; from 80 on the cap
-// would spill.  With one workgroup per CU (four waves, from head size 144
-// on) the page ids of a step are read a step ahead (see prefill_any_kernel).
+// would spill.  Pages below 16 tokens are paged per chunk, and their page
+// ids are read a step ahead only with one workgroup per CU (four waves,
+// from head size 144 on; see prefill_any_kernel).
 __host__ __device__ constexpr int any_prefill_wpe(int d) { return d <= 64 ? 4 : 1; }
 __host__ __device__ constexpr bool any_pages_ahead(int d) { return any_prefill_waves(d) == 4; }
 constexpr int kAnyStep = 32;                 // kv tokens per step (the MFMA's M)
