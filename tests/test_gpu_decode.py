@@ -150,9 +150,11 @@ def test_decode_work_list_all_sequences(pkg, dev):
 
 
 def test_decode_work_list_many_q_heads_per_kv_head(pkg, dev):
-    """G = 64 (blocks of 16 q heads as separate work items) on a launch large
-    enough for the work list (64 sequences, 131 (sequence, chunk) pairs x 4 kv
-    heads x 4 blocks = 2096 items); every sequence against the oracle."""
+    """G = 64 (blocks of 32 q heads as separate work items, in the generic
+    kernel that takes more than 16 q heads per kv head over bf16 pages) on a
+    launch large enough for the work list (64 sequences x 4 chunks of the
+    widest table row x 4 kv heads x 2 blocks = 2048 items); every sequence
+    against the oracle."""
     rng = np.random.default_rng(57)
     lens = rng.integers(1, 6000, 64)
     lens[:4] = [0, 1, 2048, 4097]

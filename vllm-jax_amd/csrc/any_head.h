@@ -20,7 +20,9 @@ int prefill_any_launch(const char* name, const PrefillParams& p, int head_dim, h
 
 // Split kernel and merge of `p` (filled as for the tuned kernel, with
 // head_dim-wide partials in the workspace and, optionally, the decode work
-// list of pa_decode in p.plan) with `head_dim`-wide rows.  `code` < 0: bf16 pages; else the pages hold 1-byte codes of that
+// list of pa_decode in p.plan) with `head_dim`-wide rows: the head sizes of
+// any_head_dim, and 128 (which pa_decode sends here for bf16 pages with more
+// than 16 q heads per kv head).  `code` < 0: bf16 pages; else the pages hold 1-byte codes of that
 // type (kCodeE4M3, kCodeI8, kCodeU8) with per-token scales, as p.k8 / p.v8 /
 // p.k_scales / p.v_scales give them.  Returns a PA_* code.
 int decode_any_launch(const char* name, const DecodeParams& p, int head_dim, hipStream_t s, int code = -1);

@@ -914,6 +914,7 @@ int decode_any_launch(const char* name, const DecodeParams& prm, int head_dim, h
     }                        \
     break;
       PA_ANY_DIMS(PA_ANY_LAUNCH)
+      PA_ANY_LAUNCH(128)  // more than 16 q heads per kv head over bf16 pages (pa_decode)
 #undef PA_ANY_LAUNCH
 #undef PA_ANY_DECODE
       default:

@@ -215,11 +215,17 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
     return fail(PA_ERR_INVALID_ARGUMENT,
                 "%s: Number of Q heads must be divisible by number of KV heads. Got %d and %d.", name,
                 num_heads, num_kv_heads);
-  const bool any_d = head_dim != kHeadDim && any_head_dim(head_dim);
-  if (head_dim != kHeadDim && !any_d)
+  if (head_dim != kHeadDim && !any_head_dim(head_dim))
     return fail(PA_ERR_UNSUPPORTED, "%s: head_dim %d not supported (128, or a multiple of 16 from 16 to 256)", name,
                 head_dim);
   const int group = num_heads / num_kv_heads;
+  // The generic kernels (any_head.hip) take every head size but 128, and
+  // also 128 over bf16 pages with more than 16 q heads per kv head: their
+  // items cover 32 q heads (one 32-wide MFMA column block), where this
+  // kernel's cover 16, so each kv head's K/V is read half as often (32 q
+  // heads per kv head: 261 -> 236 us for the Qwen3-8B batch's contexts).
+  // Over float8 pages this kernel stays faster (177 vs 284 us).
+  const bool any_d = head_dim != kHeadDim || (!fp8 && group > 16);
   if (fp8 && !any_d && page_size % kDecodeStep != 0)
     return fail(PA_ERR_UNSUPPORTED, "%s: quantized pages need page_size %% %d == 0 (got %d)", name, kDecodeStep,
                 page_size);
@@ -300,13 +306,13 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
     const bool aligned = page_size % kDecodeStep == 0;
     const bool cap = prm.soft_cap > 0.f;
     const dim3 grid((unsigned)blocks), block(64 * kDecodeWaves);
-    // more than 16 q heads per kv head: several items read each kv head's
-    // K/V, so the loads stay cacheable (the soft cap keeps the streaming form)
+    // (quantized pages) more than 16 q heads per kv head: several items read
+    // each kv head's K/V, so the loads stay cacheable (the soft cap keeps the
+    // streaming form); bf16 pages with more than 16 went to the generic kernel
     const bool shared = prm.hblocks > 1;
     if (fp8 && code == kCodeI8) launch_decode_codes<kCodeI8>(prm, cap, shared, grid, block, s);
     else if (fp8 && code == kCodeU8) launch_decode_codes<kCodeU8>(prm, cap, shared, grid, block, s);
     else if (fp8) launch_decode_codes<kCodeE4M3>(prm, cap, shared, grid, block, s);
-    else if (aligned && !cap && shared) decode_split_kernel<true, false, false, true><<<grid, block, 0, s>>>(prm);
     else if (aligned && !cap) decode_split_kernel<true, false><<<grid, block, 0, s>>>(prm);
     else if (aligned) decode_split_kernel<true, true><<<grid, block, 0, s>>>(prm);
     else if (!cap) decode_split_kernel<false, false><<<grid, block, 0, s>>>(prm);
