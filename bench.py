@@ -447,16 +447,7 @@ def run_decode_fp8(args, torch, pkg, db, dt_, ws, dscale, bf16_ms):
                                    k_scales_pages=scales[0], v_scales_pages=scales[1], scale=dscale,
                                    workspace=ws, out=out)
 
-    for _ in range(args.warmup):
-        call()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(max(args.steps, 10)):
-        call()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / max(args.steps, 10)
+    ms = _time_ms_warm(torch, call, args)
     ctx = int(db.context_lens.sum())
     pages = int(np.ceil(db.context_lens / db.page_size).sum())
     nbytes = ctx * hkv * (2 * d + 8) + 2 * db.batch * db.num_heads * d * 2 + 4 * pages + 4 * db.batch

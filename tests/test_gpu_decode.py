@@ -136,9 +136,11 @@ def test_decode_through_attention_seam(pkg, dev):
 
 
 def test_decode_work_list_all_sequences(pkg, dev):
-    """A launch large enough for the decode work list (96 sequences x 3 chunks
-    x 8 kv heads = 2304 workgroups), every sequence against the oracle:
-    lengths 0 and 1, chunk boundaries, ragged rest."""
+    """A launch large enough for the decode work list (96 sequences x 4
+    chunks of 2048 tokens x 8 kv heads = 3072 workgroups; with 4096-token
+    chunks it would hold only 1536, so it keeps the 2048-token ones), every
+    sequence against the oracle: lengths 0 and 1, chunk boundaries, ragged
+    rest."""
     rng = np.random.default_rng(31)
     lens = rng.integers(2, 6000, 96)
     lens[:8] = [0, 1, 2047, 2048, 2049, 4096, 4097, 6000]
@@ -146,6 +148,21 @@ def test_decode_work_list_all_sequences(pkg, dev):
     db = wl.make_decode(lens.tolist(), num_heads=32, num_kv_heads=8, page_size=256, rng=rng, table_width=width)
     print(f"decode work list: {db.batch} sequences, table width {width}", flush=True)
     out, _ = _run_and_check(pkg, dev, db, seed=31)
+    assert not u16(out)[0].any()
+
+
+def test_decode_long_chunks_all_sequences(pkg, dev):
+    """A launch that still holds 2048 items of 4096 tokens (160 sequences x 4
+    chunks of the widest table row x 8 kv heads = 5120), so the split kernel
+    runs 4096-token chunks; every sequence against the oracle: lengths 0 and
+    1 and both sides of the 4096 and 8192 chunk boundaries."""
+    rng = np.random.default_rng(37)
+    lens = rng.integers(2, 16384, 160)
+    lens[:10] = [0, 1, 4095, 4096, 4097, 8191, 8192, 8193, 12289, 16384]
+    width = 64  # 16 384 tokens of 256-token pages
+    db = wl.make_decode(lens.tolist(), num_heads=32, num_kv_heads=8, page_size=256, rng=rng, table_width=width)
+    print(f"decode long chunks: {db.batch} sequences, table width {width}", flush=True)
+    out, _ = _run_and_check(pkg, dev, db, seed=37)
     assert not u16(out)[0].any()
 
 

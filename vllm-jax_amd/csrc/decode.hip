@@ -124,6 +124,21 @@ static int decode_chunks(int32_t pages_per_seq, int32_t page_size) {
   return (int)((max_tokens + chunk - 1) / chunk);
 }
 
+constexpr int kDecodeLongChunk = 4096;  // tokens per item of the split kernel on large launches
+
+// Tokens per work item of decode_split_kernel.  An item pays a fixed cost
+// (q, the chunk's page ids, the waves' combine, a partial and its merge),
+// so on launches that still hold kDecodePlanMinItems items of 4096 tokens
+// the chunk is 4096 (pages of 64+ tokens keep it within 64 page ids); else
+// decode_chunk_tokens.  The workspace is sized for the shorter chunks, so
+// either fits it.
+static int decode_split_chunk(int32_t page_size, int32_t batch, int32_t pages_per_seq, int64_t vheads) {
+  const int base = decode_chunk_tokens(page_size);
+  if (page_size < 64) return base;
+  const int64_t chunks = ((int64_t)pages_per_seq * page_size + kDecodeLongChunk - 1) / kDecodeLongChunk;
+  return (int64_t)batch * chunks * vheads >= kDecodePlanMinItems ? kDecodeLongChunk : base;
+}
+
 }  // namespace pa
 
 using namespace pa;
@@ -224,7 +239,7 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
   // items cover 32 q heads (one 32-wide MFMA column block), where this
   // kernel's cover 16, so each kv head's K/V is read half as often (32 q
   // heads per kv head: 261 -> 236 us for the Qwen3-8B batch's contexts).
-  // Over float8 pages this kernel stays faster (177 vs 284 us).
+  // Over float8 pages this kernel stays faster (155 vs 284 us).
   const bool any_d = head_dim != kHeadDim || (!fp8 && group > 16);
   if (fp8 && !any_d && page_size % kDecodeStep != 0)
     return fail(PA_ERR_UNSUPPORTED, "%s: quantized pages need page_size %% %d == 0 (got %d)", name, kDecodeStep,
@@ -268,8 +283,15 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
   prm.num_kv_heads = num_kv_heads;
   prm.group = group;
   prm.hblocks = (group + 15) / 16;
-  prm.chunk = decode_chunk_tokens(page_size);
-  prm.n_chunks = pages_per_seq > 0 ? decode_chunks(pages_per_seq, page_size) : 0;
+  // work items per (sequence, chunk): one per kv head and block of q heads
+  // (16 per item here, 32 in the generic kernels)
+  const int64_t vheads = (int64_t)num_kv_heads * (any_d ? (group + 31) / 32 : prm.hblocks);
+  // The generic kernels run an item on one wave and keep the shorter chunks:
+  // 4096-token items made head sizes 64 and 96 and 32 q heads per kv head
+  // 4-9 % slower there (fewer items in flight).
+  prm.chunk = any_d ? decode_chunk_tokens(page_size) : decode_split_chunk(page_size, batch, pages_per_seq, vheads);
+  prm.n_chunks =
+      pages_per_seq > 0 ? (int)(((int64_t)pages_per_seq * page_size + prm.chunk - 1) / prm.chunk) : 0;
   prm.soft_cap = soft_cap > 0.f ? soft_cap : 0.f;
   prm.logit_scale = prm.soft_cap > 0.f ? scale : scale * kLog2e;
   const size_t parts = (size_t)batch * num_heads * prm.n_chunks;
@@ -284,9 +306,6 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
 
   hipStream_t s = (hipStream_t)stream;
   const int64_t pairs = (int64_t)batch * prm.n_chunks;
-  // work items per (sequence, chunk): one per kv head and block of q heads
-  // (16 per item here, 32 in the generic kernels)
-  const int64_t vheads = (int64_t)num_kv_heads * (any_d ? (group + 31) / 32 : prm.hblocks);
   // The work list pays for its launch once the grid is several waves of
   // workgroups deep (two per CU, 256 CUs).
   const bool planned = pairs > 0 && pairs * vheads >= kDecodePlanMinItems;

@@ -1,8 +1,9 @@
 // Split-K paged GQA decode for gfx950.
 //
-// Workgroup = (sequence b, kv head, chunk of 2048 context tokens; 1024 when
-// pages hold 16 tokens), four wavefronts.  The chunk is cut into 16-token steps dealt round-robin to
-// the waves (wave w takes steps w, w+4, ...), so the four waves stream
+// Workgroup = (sequence b, kv head, chunk of context tokens: 4096 on large
+// launches with pages of 64+ tokens, else 2048, 1024 when pages hold 16
+// tokens), four wavefronts.  The chunk is cut into 16-token steps dealt
+// round-robin to the waves (wave w takes steps w, w+4, ...), so the four waves stream
 // adjacent token rows and finish together.  Each wave keeps kDecodeBufs steps
 // of K and V in flight in VGPRs: the loads of step i+kDecodeBufs are issued as
 // soon as step i has been consumed, so HBM always sees several 8 KiB requests
@@ -158,7 +159,8 @@ __device__ __forceinline__ int xcd_grouped_item(int bid, int nb) {
   return x * q8 + min(x, r8) + k;
 }
 
-// Tokens per workgroup: the aligned path keeps the chunk's page ids in one
+// Tokens per workgroup (the shorter chunks; large launches with pages of
+// 64+ tokens take 4096): the aligned path keeps the chunk's page ids in one
 // VGPR (one per lane), so a chunk spans at most 64 pages.
 __host__ __device__ inline int decode_chunk_tokens(int page_size) { return page_size >= 32 ? 2048 : 1024; }
 
