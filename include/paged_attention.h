@@ -104,9 +104,10 @@ size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_d
  * with k_j / v_j of kv head h / (num_heads / num_kv_heads) read through
  * block_tables[b].  lengths[b] == 0 gives a zero row.  soft_cap > 0 applies
  * soft_cap * tanh(logit / soft_cap).  Any number of q heads per kv head: a
- * work item takes them 16 at a time (the reference pads the group to its
- * block_h, decode_paged_attention.py:188-197), so above 16 each block of 16
- * q heads reads its kv head's K/V once.
+ * work item takes them 16 at a time (32 at a time over bf16 pages above 16
+ * per kv head, and at head sizes other than 128; the reference pads the
+ * group to its block_h, decode_paged_attention.py:188-197), so each block
+ * of q heads reads its kv head's K/V once.
  * Replaces decode_paged_attention (decode_paged_attention.py:300-397); that
  * entry expects q pre-scaled (qwen3.py:207), i.e. scale = 1.
  * q: [batch, H, d] strides (q_batch_stride, q_head_stride, 1);
