@@ -182,37 +182,21 @@ __device__ __forceinline__ void any_p_pv(const f32x16& s, float m_run, float& l_
 }
 
 // Online softmax of one step's logits `s` (masked ones -inf) for the lane's
-// column, then O^T += V^T P^T from the staged V tile.
-// kLazy: move the reference only past the slack (prefill, where the VALU
-// work of the softmax wave bounds the step); otherwise every step (decode,
-// bound by memory, where the branch costs registers at the large sizes).
+// column, then O^T += V^T P^T from the staged V tile (decode).  The running
+// max moves every step: decode is bound by memory, and a lazy reference's
+// branch costs registers at the large head sizes.
 // kVs: quantized V pages, vs[i] the V scale of s[i]'s token: P is rounded to
 // bf16 as p * vs for PV, while the row sum takes p itself.
-template <int kDt, int kRowBytes, bool kLazy, bool kVs = false>
+template <int kDt, int kRowBytes, bool kVs = false>
 __device__ __forceinline__ void any_softmax_pv(const f32x16& s, float& m_run, float& l_run, f32x16 (&acc)[kDt],
                                                const lds_char* v, int lane, const f32x16& vs = f32x16{}) {
   float mx = s[0];
 #pragma unroll
   for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
   mx = max_xor32(mx);
-  // m_run is the column's reference max: it moves (and O and l are rescaled)
-  // only when some column of the wave exceeds its own by more than the
-  // slack, so P stays below 2^kAnySlack
-  float corr = 1.f;
-  if constexpr (kLazy) {
-    if (__any(mx > m_run + kAnySlack)) {  // uniform over the wave
-      const float m_new = fmaxf(m_run, mx);
-      corr = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
-      m_run = m_new;
-      l_run *= corr;
-#pragma unroll
-      for (int dt = 0; dt < kDt; ++dt) acc[dt] = acc[dt] * corr;
-    }
-  } else {
-    const float m_new = fmaxf(m_run, mx);
-    corr = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
-    m_run = m_new;
-  }
+  const float m_new = fmaxf(m_run, mx);
+  const float corr = fast_exp2(m_run - (m_new == -INFINITY ? 0.f : m_new));
+  m_run = m_new;
   const float ms = m_run == -INFINITY ? 0.f : m_run;  // a column that has seen no key yet keeps P = 0
   float ls = 0.f;
   u32x4 pw[2];
@@ -226,10 +210,10 @@ __device__ __forceinline__ void any_softmax_pv(const f32x16& s, float& m_run, fl
       else pw[u][e] = pack_bf16x2(a, b);
       ls += a + b;
     }
-  l_run = kLazy ? l_run + ls : l_run * corr + ls;
+  l_run = l_run * corr + ls;
 #pragma unroll
   for (int dt = 0; dt < kDt; ++dt) {
-    if constexpr (!kLazy) acc[dt] = acc[dt] * corr;
+    acc[dt] = acc[dt] * corr;
 #pragma unroll
     for (int u = 0; u < 2; ++u)
       acc[dt] = mfma32(as_bf16x8(vt_operand<kRowBytes>(v, 32 * dt, u, lane)), as_bf16x8(pw[u]), acc[dt]);
@@ -759,7 +743,7 @@ decode_any_kernel(DecodeParams p, int code) {
           s[i] = j < t1 ? any_logit_f32<kSoftCap>(kQuant ? s[i] * ksc[i] : s[i], p.logit_scale, p.soft_cap)
                         : -INFINITY;
         }
-        any_softmax_pv<A::kDt, A::kVRow, false, kQuant>(s, m_run, l_run, acc, v_tile + kAnyStep * sub * A::kVRow,
+        any_softmax_pv<A::kDt, A::kVRow, kQuant>(s, m_run, l_run, acc, v_tile + kAnyStep * sub * A::kVRow,
                                                        lane, vsc);
       }
     }
