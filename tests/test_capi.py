@@ -199,6 +199,9 @@ def test_decode_workspace_size():
     assert lib.pa_decode_workspace_size(4, 8, 128, 100, 16) == r256(4 * 8 * 2 * (128 + 2) * 4) + 256 + 4 * r8(8)
     assert lib.pa_decode_workspace_size(3, 8, 128, 100, 16) == r256(3 * 8 * 2 * (128 + 2) * 4) + 256 + 4 * r8(6)
     assert lib.pa_decode_workspace_size(0, 32, 128, 32, 256) == 0
+    # the generic decode's 1024-token items at head sizes below 128 other than 64
+    assert lib.pa_decode_workspace_size(4, 8, 96, 32, 256) == r256(4 * 8 * 8 * (96 + 2) * 4) + 256 + 4 * r8(32)
+    assert lib.pa_decode_workspace_size(4, 8, 64, 32, 256) == r256(4 * 8 * 4 * (64 + 2) * 4) + 256 + 4 * r8(16)
 
 
 def test_mixed_workspace_size():

@@ -118,13 +118,23 @@ void launch_decode_merge(const DecodeParams& p, hipStream_t s) {
 
 constexpr int64_t kDecodePlanMinItems = 2048;  // workgroups from which pa_decode builds a work list
 
-static int decode_chunks(int32_t pages_per_seq, int32_t page_size) {
+constexpr int kDecodeLongChunk = 4096;  // tokens per item on large launches
+constexpr int kDecodeShortChunk = 1024;  // tokens per item of the generic decode at small head sizes
+
+// The generic decode (one wave per item) at head sizes below 128 other than
+// 64 runs best with 1024-token items; same-process A/B on the Qwen3-8B
+// batch's contexts, 1024 against 2048 tokens: 48 -5.6 %, 80 -0.2 %, 96
+// -1.3 %, 112 -1.2 %; 64 +1.6 %, 160 +1.6 %, 192 +3.6 %, 224 +1.9 %.
+static bool decode_any_short_chunk(int head_dim) { return head_dim < 128 && head_dim != 64; }
+
+// Chunks of the widest table row at the shortest chunk a launch can take:
+// the workspace holds one partial per (sequence, q head, chunk) for them.
+static int decode_chunks(int32_t pages_per_seq, int32_t page_size, int32_t head_dim) {
   const int64_t max_tokens = (int64_t)pages_per_seq * page_size;
-  const int chunk = decode_chunk_tokens(page_size);
+  int chunk = decode_chunk_tokens(page_size);
+  if (head_dim != kHeadDim && decode_any_short_chunk(head_dim)) chunk = min(chunk, kDecodeShortChunk);
   return (int)((max_tokens + chunk - 1) / chunk);
 }
-
-constexpr int kDecodeLongChunk = 4096;  // tokens per item of the split kernel on large launches
 
 // Tokens per work item of decode_split_kernel.  An item pays a fixed cost
 // (q, the chunk's page ids, the waves' combine, a partial and its merge),
@@ -137,6 +147,19 @@ static int decode_split_chunk(int32_t page_size, int32_t batch, int32_t pages_pe
   if (page_size < 64) return base;
   const int64_t chunks = ((int64_t)pages_per_seq * page_size + kDecodeLongChunk - 1) / kDecodeLongChunk;
   return (int64_t)batch * chunks * vheads >= kDecodePlanMinItems ? kDecodeLongChunk : base;
+}
+
+// Tokens per work item of the generic decode (decode_any_kernel, one wave
+// per item): 1024 at the head sizes of decode_any_short_chunk; 4096 at head
+// size 256 on launches that still hold kDecodePlanMinItems such items (-1.7 %
+// there, where 4096 cost 4-9 % at 64, 96 and 32 q heads per kv head); else
+// decode_chunk_tokens.
+static int decode_any_chunk(int32_t head_dim, int32_t page_size, int32_t batch, int32_t pages_per_seq,
+                            int64_t vheads) {
+  const int base = decode_chunk_tokens(page_size);
+  if (decode_any_short_chunk(head_dim)) return min(base, kDecodeShortChunk);
+  if (head_dim == 256) return decode_split_chunk(page_size, batch, pages_per_seq, vheads);
+  return base;
 }
 
 }  // namespace pa
@@ -193,7 +216,7 @@ static size_t decode_partials_bytes(int32_t batch, int32_t num_heads, int32_t he
 extern "C" size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_dim,
                                            int32_t pages_per_seq, int32_t page_size) {
   if (batch <= 0 || num_heads <= 0 || head_dim <= 0 || pages_per_seq <= 0 || page_size <= 0) return 0;
-  const int n_chunks = decode_chunks(pages_per_seq, page_size);
+  const int n_chunks = decode_chunks(pages_per_seq, page_size, head_dim);
   const size_t pairs8 = ((size_t)batch * n_chunks + 7) / 8 * 8;
   return decode_partials_bytes(batch, num_heads, head_dim, n_chunks) + (kDecodePlanHeader + pairs8) * sizeof(int32_t);
 }
@@ -286,10 +309,8 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
   // work items per (sequence, chunk): one per kv head and block of q heads
   // (16 per item here, 32 in the generic kernels)
   const int64_t vheads = (int64_t)num_kv_heads * (any_d ? (group + 31) / 32 : prm.hblocks);
-  // The generic kernels run an item on one wave and keep the shorter chunks:
-  // 4096-token items made head sizes 64 and 96 and 32 q heads per kv head
-  // 4-9 % slower there (fewer items in flight).
-  prm.chunk = any_d ? decode_chunk_tokens(page_size) : decode_split_chunk(page_size, batch, pages_per_seq, vheads);
+  prm.chunk = any_d ? decode_any_chunk(head_dim, page_size, batch, pages_per_seq, vheads)
+                    : decode_split_chunk(page_size, batch, pages_per_seq, vheads);
   prm.n_chunks =
       pages_per_seq > 0 ? (int)(((int64_t)pages_per_seq * page_size + prm.chunk - 1) / prm.chunk) : 0;
   prm.soft_cap = soft_cap > 0.f ? soft_cap : 0.f;
