@@ -352,3 +352,57 @@ def test_prefill_rows_past_max_seqlen_are_zero(pkg, dev, with_list):
     err = float(np.abs(got[kept] - ora.bf16_to_f32(ref)[kept]).max())
     print(f"truncated prefill max-abs err {err:.3e}")
     assert err <= TOL
+
+
+@pytest.mark.parametrize("prefix", [False, True])
+def test_prefill_page_sizes_bit_identical(pkg, dev, prefix):
+    """The same tokens over 16-, 32-, 48-, 64- and 256-token pages: the three
+    ways the tile loads find their pages (per lane at 48, one base per wave
+    and tile at 16 and 32, one per tile at 64 and 256) read the same K / V
+    rows, so the outputs are bit-identical; the 16-token one is also checked
+    against the oracle.  With cached prefixes the kv ranges end inside pages
+    and tiles, and rows past a kv length take the clamped last row."""
+    import torch
+    pre = [0, 5, 300, 1111, 64] if prefix else [0] * 6
+    new = [700, 1, 129, 64, 333] if prefix else [1, 63, 64, 65, 700, 1500]
+    gen = np.random.default_rng(74)
+    bf = lambda *shape: torch.as_tensor(ora.round_bf16(0.5 * gen.standard_normal(shape).astype(np.float32)),
+                                        device=dev).to(torch.bfloat16)
+    doc_k, doc_v = bf(max(pre) + 1, 8, 128), bf(max(pre) + 1, 8, 128)   # the cached document's K / V
+    q, k, v = bf(sum(new), 32, 128), bf(sum(new), 8, 128), bf(sum(new), 8, 128)
+    outs = {}
+    for bs in (16, 32, 48, 64, 256):
+        rng = np.random.default_rng(71)
+        if prefix:
+            pb = wl.make_prefix_prefill(pre, new, num_heads=32, num_kv_heads=8, page_size=bs, rng=rng,
+                                        shared_prefix_tokens=max(pre) + 1)
+        else:
+            pb = wl.make_prefill(new, num_heads=32, num_kv_heads=8, page_size=bs, rng=rng)
+        kv = torch.zeros((2, pb.num_pages, bs, 8, 128), dtype=torch.bfloat16, device=dev)
+        # the cached tokens: every prefix slot once (shared pages hold the same document tokens)
+        slots = {}
+        for b, p in enumerate(pre):
+            for j in range(p):
+                slots.setdefault(int(pb.block_tables[b, j // bs]) * bs + j % bs, j)
+        if slots:
+            sl = torch.as_tensor(list(slots), dtype=torch.int32, device=dev)
+            pos = torch.as_tensor(list(slots.values()), dtype=torch.long, device=dev)
+            kv = pkg.update_kv_cache(kv, sl, doc_k[pos], doc_v[pos])
+        kv = pkg.update_kv_cache(kv, torch.as_tensor(pb.slot_mapping, dtype=torch.int32, device=dev), k, v)
+        i32 = lambda a: torch.as_tensor(np.ascontiguousarray(a), dtype=torch.int32, device=dev)
+        out = pkg.prefill_paged_attention(q, kv[0].permute(2, 0, 1, 3), kv[1].permute(2, 0, 1, 3),
+                                          i32(pb.block_tables), i32(pb.cu_seqlens_q), i32(pb.slot_mapping),
+                                          i32(pb.input_positions), max_seqlen_bucket=pb.max_seqlen_bucket,
+                                          cu_seqlens_k=i32(pb.cu_seqlens_k))
+        torch.cuda.synchronize()
+        outs[bs] = u16(out)
+        if bs == 16:
+            kvh = u16(kv)
+            ref = ora.prefill_attention(u16(q), kvh[0].transpose(2, 0, 1, 3), kvh[1].transpose(2, 0, 1, 3),
+                                        pb.block_tables, pb.cu_seqlens_q, pb.input_positions,
+                                        cu_seqlens_k=pb.cu_seqlens_k)
+            err = float(np.abs(ora.bf16_to_f32(outs[16]) - ora.bf16_to_f32(ref)).max())
+            print(f"16-token pages vs oracle: max-abs err {err:.3e}", flush=True)
+            assert err <= TOL
+    for bs in (32, 48, 64, 256):
+        assert np.array_equal(outs[bs], outs[16]), bs

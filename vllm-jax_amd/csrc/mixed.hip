@@ -187,7 +187,7 @@ mixed_plan_kernel(MixedParams m, int32_t* __restrict__ plan) {
   if (tid == 0) plan[0] = count;
 }
 
-template <bool kSoftCap, bool kAlignedP, bool kAlignedD>
+template <bool kSoftCap, int kPagingP, bool kAlignedD>
 __global__ void __launch_bounds__(kThreads, 1)
 mixed_kernel(MixedParams m) {
   const int bid = blockIdx.x;
@@ -249,7 +249,7 @@ mixed_kernel(MixedParams m) {
     decode_item<kMixedDecodeWaves, kAlignedD, kSoftCap>(m.dec, dec, red_o, red_m, red_m + 16 * kMixedDecodeWaves);
     return;
   }
-  if (pre) prefill_run<kSoftCap, kAlignedP>(m.pre, w);
+  if (pre) prefill_run<kSoftCap, kPagingP>(m.pre, w);
 }
 
 static_assert(sizeof(float) * kMixedDecodeWaves * 16 * kPHeadDim <= sizeof(uint16_t) * kStages * kTileElems,
@@ -502,16 +502,18 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
     m.plan = plan;
   }
   const dim3 grid((unsigned)r4), block(kThreads);
-  const bool aligned_p = page_size % kTileN == 0;
-  const bool aligned_d = page_size % kDecodeStep == 0;
+  const int paging_p = prefill_paging(page_size, slot_stride);
+  const bool aligned_d = page_size % kDecodeStep == 0;  // every kPageTile / kPageWave size is
   if (cap > 0.f) {
-    if (aligned_p) mixed_kernel<true, true, true><<<grid, block, 0, s>>>(m);
-    else if (aligned_d) mixed_kernel<true, false, true><<<grid, block, 0, s>>>(m);
-    else mixed_kernel<true, false, false><<<grid, block, 0, s>>>(m);
+    if (paging_p == kPageTile) mixed_kernel<true, kPageTile, true><<<grid, block, 0, s>>>(m);
+    else if (paging_p == kPageWave) mixed_kernel<true, kPageWave, true><<<grid, block, 0, s>>>(m);
+    else if (aligned_d) mixed_kernel<true, kPageLane, true><<<grid, block, 0, s>>>(m);
+    else mixed_kernel<true, kPageLane, false><<<grid, block, 0, s>>>(m);
   } else {
-    if (aligned_p) mixed_kernel<false, true, true><<<grid, block, 0, s>>>(m);
-    else if (aligned_d) mixed_kernel<false, false, true><<<grid, block, 0, s>>>(m);
-    else mixed_kernel<false, false, false><<<grid, block, 0, s>>>(m);
+    if (paging_p == kPageTile) mixed_kernel<false, kPageTile, true><<<grid, block, 0, s>>>(m);
+    else if (paging_p == kPageWave) mixed_kernel<false, kPageWave, true><<<grid, block, 0, s>>>(m);
+    else if (aligned_d) mixed_kernel<false, kPageLane, true><<<grid, block, 0, s>>>(m);
+    else mixed_kernel<false, kPageLane, false><<<grid, block, 0, s>>>(m);
   }
   int rc = launch_status("pa_mixed");
   if (rc || partials == 0 || num_decodes == 0) return rc;

@@ -8,10 +8,10 @@
 
 namespace pa {
 
-template <bool kSoftCap, bool kAligned>
+template <bool kSoftCap, int kPaging>
 __global__ void __launch_bounds__(kThreads, 1)
 prefill_kernel(PrefillParams p) {
-  prefill_body<kSoftCap, kAligned>(p, blockIdx.x);
+  prefill_body<kSoftCap, kPaging>(p, blockIdx.x);
 }
 
 // The item of workgroup `bid` with the pools: every XCD walks the whole list
@@ -40,7 +40,7 @@ __device__ __forceinline__ int prefill_pooled_item(const PrefillParams& p, int b
   return -1;
 }
 
-template <bool kSoftCap, bool kAligned>
+template <bool kSoftCap, int kPaging>
 __global__ void __launch_bounds__(kThreads, 1)
 prefill_kernel_pooled(PrefillParams p) {
   __shared__ int32_t s_item;
@@ -48,7 +48,7 @@ prefill_kernel_pooled(PrefillParams p) {
   __syncthreads();
   const int item = __builtin_amdgcn_readfirstlane(s_item);  // the same in every lane
   if (item < 0) return;
-  prefill_body<kSoftCap, kAligned>(p, item);
+  prefill_body<kSoftCap, kPaging>(p, item);
 }
 
 constexpr int kPrepThreads = 1024;
@@ -458,23 +458,22 @@ static int prefill_launch(const char* name, const uint16_t* q, int64_t q_tok_str
   // quarter more workgroups than items lets the XCDs that run ahead take up
   // to twice their share of it
   const int64_t blocks = prm.pool ? std::min<int64_t>(items + (items + 3) / 4, 0x7fffffff) : items;
-  const bool aligned = page_size % kTileN == 0;
+  const int paging = prefill_paging(page_size, slot_stride);
   const dim3 g((unsigned)blocks), b(kThreads);
-  if (prm.pool) {
-    if (prm.soft_cap > 0.f) {
-      if (aligned) prefill_kernel_pooled<true, true><<<g, b, 0, s>>>(prm);
-      else prefill_kernel_pooled<true, false><<<g, b, 0, s>>>(prm);
-    } else {
-      if (aligned) prefill_kernel_pooled<false, true><<<g, b, 0, s>>>(prm);
-      else prefill_kernel_pooled<false, false><<<g, b, 0, s>>>(prm);
-    }
-  } else if (prm.soft_cap > 0.f) {
-    if (aligned) prefill_kernel<true, true><<<g, b, 0, s>>>(prm);
-    else prefill_kernel<true, false><<<g, b, 0, s>>>(prm);
-  } else {
-    if (aligned) prefill_kernel<false, true><<<g, b, 0, s>>>(prm);
-    else prefill_kernel<false, false><<<g, b, 0, s>>>(prm);
-  }
+  // one instance per (soft cap, paging, pool)
+  auto launch = [&](auto cap, auto pg) {
+    constexpr bool kCap = decltype(cap)::value;
+    constexpr int kPg = decltype(pg)::value;
+    if (prm.pool) prefill_kernel_pooled<kCap, kPg><<<g, b, 0, s>>>(prm);
+    else prefill_kernel<kCap, kPg><<<g, b, 0, s>>>(prm);
+  };
+  auto with_paging = [&](auto cap) {
+    if (paging == kPageTile) launch(cap, std::integral_constant<int, kPageTile>{});
+    else if (paging == kPageWave) launch(cap, std::integral_constant<int, kPageWave>{});
+    else launch(cap, std::integral_constant<int, kPageLane>{});
+  };
+  if (prm.soft_cap > 0.f) with_paging(std::true_type{});
+  else with_paging(std::false_type{});
   return launch_status(name);
 }
 

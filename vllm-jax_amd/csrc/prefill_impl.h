@@ -86,6 +86,13 @@ struct PrefillParams {
   int32_t* pool;
 };
 
+// How the tile loads find their pages.  kPageLane: each lane looks up its
+// row's page (any page size).  kPageTile: pages of a multiple of 64 tokens
+// hold whole tiles, one scalar page base per tile.  kPageWave: pages of 16 or
+// 32 tokens; a wave's 8 rows of a tile lie in one page, one scalar page base
+// per wave and tile.
+constexpr int kPageLane = 0, kPageTile = 1, kPageWave = 2;
+
 // One entry of the work list: a (sequence, q tile) pair with the sequence's
 // row range and kv geometry as prefill_body derives them.
 struct PrefillPair {
@@ -295,8 +302,9 @@ __device__ __forceinline__ bool prefill_resolve(const PrefillParams& p, int bid,
 }
 
 // One prefill work item, run by a whole 512-thread workgroup.
-template <bool kSoftCap, bool kAligned>
+template <bool kSoftCap, int kPaging>
 __device__ __forceinline__ void prefill_run(const PrefillParams& p, const PrefillWork& w) {
+  constexpr bool kAligned = kPaging != kPageLane;  // scalar page bases
   PA_PHASE(ph0);
   auto k_stage = [&](auto c) __attribute__((always_inline)) -> uint16_t* { return k_lds[decltype(c)::value]; };
   auto v_stage = [&](auto c) __attribute__((always_inline)) -> uint16_t* { return v_lds[decltype(c)::value]; };
@@ -354,12 +362,21 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   const int qpos = row_ok ? qpos_ld : 0;
   // raw page ids of the first three kv tiles, read while the loads above fly
   int32_t raw_pre[3] = {0, 0, 0};
+  // (kPageWave) log2 of the page size, and the table entry of this wave's
+  // rows of tile T: rows 8w .. 8w + 7, or the tile's last row inside the kv
+  // length when they lie past it (a wave's rows never straddle a page)
+  const int pg_sh = kPaging == kPageWave ? (p.page_size == 16 ? 4 : 5) : 0;
+  auto wave_entry = [&](int T) __attribute__((always_inline)) {
+    const int last = min(max(lk - 1 - T * kTileN, 0), kTileN - 1);
+    return (T * kTileN + min(8 * wave, last)) >> pg_sh;
+  };
   if constexpr (kAligned) {
     if (p.pages_per_seq > 0) {
       const __attribute__((address_space(4))) int32_t* c =
           (const __attribute__((address_space(4))) int32_t*)(p.block_tables + (int64_t)b * p.bt_stride);
 #pragma unroll
-      for (int i = 0; i < 3; ++i) raw_pre[i] = c[min(i * kTileN / p.page_size, p.pages_per_seq - 1)];
+      for (int i = 0; i < 3; ++i)
+        raw_pre[i] = c[min(kPaging == kPageWave ? wave_entry(i) : i * kTileN / p.page_size, p.pages_per_seq - 1)];
     }
   }
 
@@ -431,11 +448,14 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   // this nor the byte offset 2 * ld_off below wraps
   uint32_t ld_off[kBlk];
   uint32_t ld_sw[kBlk];  // its swizzled chunk part alone
+  static_assert(kPaging != kPageWave || kBlk == 2, "a wave's rows of a tile must lie in one 16-token page");
+  // (kPageWave) tile rows are rows of the wave's page: r mod page size
+  const int row_mask = kPaging == kPageWave ? p.page_size - 1 : kTileN - 1;
 #pragma unroll
   for (int i = 0; i < kBlk; ++i) {
     const int r = 4 * (kBlk * wave + i) + ld_r;
     ld_sw[i] = (uint32_t)(8 * swz(r, ld_p));
-    ld_off[i] = (uint32_t)(r * (int32_t)p.slot_stride) + ld_sw[i];
+    ld_off[i] = (uint32_t)((kPaging == kPageWave ? r & row_mask : r) * (int32_t)p.slot_stride) + ld_sw[i];
   }
   // Tile DMA in two steps: tile_addrs() computes this wave's 2*kBlk global
   // addresses (K block 0, V block 0, K block 1, ...), dma_issue() issues one
@@ -450,7 +470,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   // Aligned pages hold tpp whole tiles: tile j0 = 64 (tpp lp + r) is tile r
   // of table entry lp.  The loop walks (lp, r) incrementally, so no division
   // sits on the softmax wave's path.
-  const int tpp = kAligned ? p.page_size / kTileN : 1;
+  const int tpp = kPaging == kPageTile ? p.page_size / kTileN : 1;
   const int64_t tile_stride = (int64_t)kTileN * p.slot_stride;
   auto page_raw_at = [&](int lp) __attribute__((always_inline)) {
     const __attribute__((address_space(4))) int32_t* c = (const __attribute__((address_space(4))) int32_t*)bt_row;
@@ -462,7 +482,8 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   auto tile_addrs = [&](int j0, int32_t raw, int rin) __attribute__((always_inline)) {
     TileAddrs a;
     if constexpr (kAligned) {
-      // page_size % 64 == 0: the whole tile lies in one page
+      // the whole tile (kPageTile) or this wave's rows of it (kPageWave) lie
+      // in one page
       const int32_t page = raw < 0 ? 0 : (raw >= p.num_pages ? p.num_pages - 1 : raw);
       // One scalar base per tile and a per-lane offset: no per-lane 64-bit
       // address arithmetic on the softmax wave's path.
@@ -473,7 +494,8 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
       // never stale); a tile wholly past it reads its row 0.  Selects, no
       // branch.
       const int last = __builtin_amdgcn_readfirstlane(max(lk - 1 - j0, 0));
-      const uint32_t last_off = (uint32_t)(min(last, kTileN - 1) * (int32_t)p.slot_stride);
+      const int last_row = kPaging == kPageWave ? min(last, kTileN - 1) & row_mask : min(last, kTileN - 1);
+      const uint32_t last_off = (uint32_t)(last_row * (int32_t)p.slot_stride);
 #pragma unroll
       for (int i = 0; i < kBlk; ++i) {
         const int r = 4 * (kBlk * wave + i) + ld_r;
@@ -734,12 +756,14 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     const int dstage = grp_b ? (s + 3) % kStages : (s + 2) % kStages;
     TileAddrs ta;
     if constexpr (kPv || kQk) ta = tile_addrs(ti * kTileN, page_next, nx_r);
-    if constexpr (kAligned && (kPv || kQk)) {  // for the next iteration: tile ti + 1
+    if constexpr (kPaging == kPageTile && (kPv || kQk)) {  // for the next iteration: tile ti + 1
       if (++nx_r == tpp) {
         nx_r = 0;
         ++nx_lp;
       }
       page_next = page_raw_at(nx_lp);
+    } else if constexpr (kPaging == kPageWave && (kPv || kQk)) {
+      page_next = page_raw_at(wave_entry(ti + 1));
     }
     // one DMA before each quarter of the softmax: a burst of them would
     // stall on the address queue
@@ -776,10 +800,12 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     if (grp_b) issue_tile_raw(2 * kTileN, raw_pre[2], 2);
   }
   // raw page id of the first tile the loop loads (tile `ahead`)
-  if (kAligned && n_tiles > 0) {
+  if (kPaging == kPageTile && n_tiles > 0) {
     nx_lp = ahead / tpp;
     nx_r = ahead - nx_lp * tpp;
     page_next = page_raw_at(nx_lp);
+  } else if (kPaging == kPageWave && n_tiles > 0) {
+    page_next = page_raw_at(wave_entry(ahead));
   }
   const int issued = n_tiles > 0 ? (grp_b ? 3 : 2) : 0;
   if (issued == 3) wait_vm_lgkm0<2 * kDmaPerTile>();
@@ -860,10 +886,17 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
 }
 
 // The work item numbered `bid`, resolved and run.
-template <bool kSoftCap, bool kAligned>
+template <bool kSoftCap, int kPaging>
 __device__ __forceinline__ void prefill_body(const PrefillParams& p, int bid) {
   PrefillWork w;
-  if (prefill_resolve(p, bid, w)) prefill_run<kSoftCap, kAligned>(p, w);
+  if (prefill_resolve(p, bid, w)) prefill_run<kSoftCap, kPaging>(p, w);
+}
+
+// Tile paging of a launch (kPageLane / kPageTile / kPageWave).
+inline int prefill_paging(int32_t page_size, int64_t slot_stride) {
+  if (page_size % kTileN == 0) return kPageTile;
+  if ((page_size == 16 || page_size == 32) && prefill_offsets_fit(slot_stride)) return kPageWave;
+  return kPageLane;
 }
 
 }  // namespace pa
