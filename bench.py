@@ -142,6 +142,58 @@ def run_head_dims(args):
             "steps": args.steps, "warmup": args.warmup}
 
 
+def run_page_sizes(args):
+    """Prefill and decode over pages of 16, 32, 64 and 256 tokens, the same
+    tokens each time: the Qwen3-8B prefix-cached prefill (seed 3's lengths)
+    and the Qwen3-8B-shaped decode batch (256 sequences, contexts U[512,
+    8192]), 32 q / 8 kv heads, head size 128.  Attention only; timed like
+    the other short lines (`_time_ms_warm`)."""
+    import torch
+    import __graft_entry__ as ge
+    pkg = ge.load_package()
+    import vllm_jax_amd.workloads as wl
+    dev = torch.device("cuda:0")
+    lens_d = np.random.default_rng(2).integers(512, 8193, size=256)
+    rng = np.random.default_rng(3)
+    prefix, new = rng.integers(0, 4097, size=64), rng.integers(128, 1025, size=64)
+    pre, dec = [], []
+    for bs in (256, 64, 32, 16):
+        pb = wl.make_prefix_prefill(prefix, new, num_heads=32, num_kv_heads=8, page_size=bs,
+                                    rng=np.random.default_rng(3), shared_prefix_tokens=4096)
+        t = wl.materialize_prefill(pb, seed=3, device=dev, fill_pool=True)
+        kp, vp = t["kv_cache"][0].permute(2, 0, 1, 3), t["kv_cache"][1].permute(2, 0, 1, 3)
+        out = torch.empty_like(t["q"])
+
+        def attn():
+            pkg.prefill_paged_attention(t["q"], kp, vp, t["block_tables"], t["cu_seqlens_q"], t["slot_mapping"],
+                                        t["input_positions"], max_seqlen_bucket=pb.max_seqlen_bucket,
+                                        cu_seqlens_k=t["cu_seqlens_k"], out=out)
+        ms = _time_ms_warm(torch, attn, args)
+        tf = pb.flops() / (ms * 1e-3) / 1e12
+        pre.append({"page_size": bs, "ms": round(ms, 4), "tflops": round(tf, 1),
+                    "frac_of_mfma_peak": round(tf / MFMA_BF16_PEAK_TFLOPS, 4)})
+        del t, kp, vp, out
+        db = wl.make_decode(lens_d, num_heads=32, num_kv_heads=8, page_size=bs, rng=np.random.default_rng(2))
+        dd = wl.materialize_decode(db, seed=2, device=dev)
+        kv = dd["kv_cache"]
+        kpd, vpd = kv[0].permute(2, 0, 1, 3), kv[1].permute(2, 0, 1, 3)
+        outd = torch.empty_like(dd["q"])
+
+        def dec_call():
+            pkg.decode_paged_attention(dd["q"], kpd, vpd, dd["block_tables"], dd["context_lens"],
+                                       scale=1 / 11.3125, out=outd)
+        ms = _time_ms_warm(torch, dec_call, args)
+        gbs = db.hbm_bytes() / (ms * 1e-3) / 1e9
+        dec.append({"page_size": bs, "ms": round(ms, 4), "gbs": round(gbs, 1),
+                    "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)})
+        del dd, kv, kpd, vpd, outd
+        torch.cuda.empty_cache()
+    return {"metric": "attention over pages of 256 / 64 / 32 / 16 tokens (head size 128, tuned kernels)",
+            "prefill": {"workload": "Qwen3-8B prefix-cached prefill (seed 3's lengths)", "results": pre},
+            "decode": {"workload": "256 sequences, contexts U[512, 8192], 32 q / 8 kv heads", "results": dec},
+            "steps": args.steps, "warmup": args.warmup}
+
+
 def _time_ms(torch, fn, args):
     for _ in range(args.warmup):
         fn()
@@ -839,7 +891,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["prefill", "decode", "rope", "mixed", "decode_fp8", "prefix", "prefill_fp8",
                                        "long8", "g32",
-                                       "copy", "head_dims"],
+                                       "copy", "head_dims", "page_sizes"],
                     default=None,
                     help="profiling aid: run one kernel family only (the JSON line then covers that part)")
     args = ap.parse_args()
@@ -853,6 +905,9 @@ def main():
         return
     if args.only == "head_dims":
         print(json.dumps(run_head_dims(args)), flush=True)
+        return
+    if args.only == "page_sizes":
+        print(json.dumps(run_page_sizes(args)), flush=True)
         return
     res, ctx = run_gpu(args)
     if args.only is not None:
