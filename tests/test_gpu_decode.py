@@ -152,14 +152,18 @@ def test_decode_work_list_all_sequences(pkg, dev):
 
 
 @pytest.mark.parametrize("bs,width,cap", [(256, 64, None), (64, 256, None), (80, 256, None), (8192, 2, None),
-                                          (256, 64, 5.0)])
+                                          (256, 64, 5.0), (16, 1024, None), (32, 512, None), (48, 384, None),
+                                          (16, 1024, 5.0)])
 def test_decode_long_chunks_all_sequences(pkg, dev, bs, width, cap):
     """A launch that still holds 2048 items of 4096 tokens (160 sequences x
     4+ chunks of the widest table row x 8 kv heads), so the split kernel runs
     4096-token chunks; every sequence against the oracle: lengths 0 and 1 and
     both sides of the 4096 and 8192 chunk boundaries.  64-token pages put 64
     page ids in a chunk (one per lane), 80-token ones chunks that start
-    inside a page, 8192-token ones two chunks per page; then the soft cap."""
+    inside a page, 8192-token ones two chunks per page; then the soft cap.
+    16-, 32- and 48-token pages put 256, 128 and up to 87 page ids in a chunk
+    (the kernels that hold four per lane; 48-token chunks start inside a
+    page), with and without the soft cap."""
     rng = np.random.default_rng(37)
     lens = rng.integers(2, 16384, 160)
     lens[:10] = [0, 1, 4095, 4096, 4097, 8191, 8192, 8193, 12289, 16384]

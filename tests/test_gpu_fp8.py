@@ -145,17 +145,19 @@ def test_decode_fp8_qwen3_8b_full_pool(pkg, dev):
     assert err <= TOL
 
 
-def test_decode_fp8_long_chunks_64_token_pages(pkg, dev):
+@pytest.mark.parametrize("bs,width", [(64, 256), (16, 1024), (48, 384)])
+def test_decode_fp8_long_chunks(pkg, dev, bs, width):
     """float8 pages on a launch that takes 4096-token chunks (160 sequences
-    x 4 chunks of the widest row x 8 kv heads), over 64-token pages: 64 page
-    ids per chunk, one per lane.  Every sequence against the oracle over the
-    same codes and scales: lengths 0 and 1 and both sides of the 4096 and
-    8192 boundaries."""
+    x 4 chunks of the widest row x 8 kv heads): over 64-token pages 64 page
+    ids per chunk, one per lane; over 16- and 48-token pages 256 and up to 87
+    (four per lane; 48-token chunks start inside a page).  Every sequence
+    against the oracle over the same codes and scales: lengths 0 and 1 and
+    both sides of the 4096 and 8192 boundaries."""
     import torch
     rng = np.random.default_rng(41)
     lens = rng.integers(2, 16384, 160)
     lens[:10] = [0, 1, 4095, 4096, 4097, 8191, 8192, 8193, 12289, 16384]
-    db = wl.make_decode(lens.tolist(), num_heads=32, num_kv_heads=8, page_size=64, rng=rng, table_width=256)
+    db = wl.make_decode(lens.tolist(), num_heads=32, num_kv_heads=8, page_size=bs, rng=rng, table_width=width)
     t = wl.materialize_decode(db, seed=41, device=dev)
     codes, scales = _quantize_pool_on_device(pkg, t["kv_cache"])
     out = pkg.decode_paged_attention(t["q"], codes[0].permute(2, 0, 1, 3), codes[1].permute(2, 0, 1, 3),
@@ -171,7 +173,7 @@ def test_decode_fp8_long_chunks_64_token_pages(pkg, dev):
         want = ora.decode_attention(qs_all[seqs], kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt,
                                     db.context_lens[seqs], k_scales_pages=ks, v_scales_pages=vs)
         err = max(err, float(np.abs(got[seqs] - ora.bf16_to_f32(want)).max()))
-    print(f"fp8 decode, 4096-token chunks over 64-token pages, all {db.batch} sequences: max-abs err {err:.3e}",
+    print(f"fp8 decode, 4096-token chunks over {bs}-token pages, all {db.batch} sequences: max-abs err {err:.3e}",
           flush=True)
     assert err <= TOL
     assert not got[0].any()

@@ -69,8 +69,9 @@ def test_prefill_graph_replays(pkg, dev):
 
 @pytest.mark.parametrize("bs", [256, 16])
 def test_decode_graph_replays(pkg, dev, bs):
-    """A decode launch with the work list (and, at 256-token pages, the
-    4096-token items), plan and merge kernels inside the graph."""
+    """A decode launch with the work list, 4096-token items (one page id per
+    lane at 256-token pages, four at 16-token ones), plan and merge kernels
+    inside the graph."""
     import torch
     rng = np.random.default_rng(83)
     lens = rng.integers(1, 9000, 160)

@@ -53,7 +53,8 @@ decode_plan_kernel(DecodeParams p, int32_t* __restrict__ plan) {
   if (tid == 0) plan[0] = count;
 }
 
-template <bool kAligned, bool kSoftCap, bool kFp8 = false, bool kShared = false, int kCode = kCodeE4M3>
+template <bool kAligned, bool kSoftCap, bool kFp8 = false, bool kShared = false, int kCode = kCodeE4M3,
+          int kIds = 1>
 __global__ void __launch_bounds__(256, 2)
 decode_split_kernel(DecodeParams p) {
   __shared__ DecodeLds red;
@@ -75,8 +76,8 @@ decode_split_kernel(DecodeParams p) {
   } else {
     item = xcd_grouped_item(blockIdx.x, gridDim.x);
   }
-  decode_item<kDecodeWaves, kAligned, kSoftCap, kFp8, kShared, kCode>(p, item, &red.o[0][0][0], &red.m[0][0],
-                                                                      &red.l[0][0]);
+  decode_item<kDecodeWaves, kAligned, kSoftCap, kFp8, kShared, kCode, kIds>(p, item, &red.o[0][0][0],
+                                                                            &red.m[0][0], &red.l[0][0]);
 }
 
 // One wave per (sequence, q head): out = sum_c o_c 2^(m_c - M) / sum_c l_c 2^(m_c - M).
@@ -139,14 +140,26 @@ static int decode_chunks(int32_t pages_per_seq, int32_t page_size, int32_t head_
 // Tokens per work item of decode_split_kernel.  An item pays a fixed cost
 // (q, the chunk's page ids, the waves' combine, a partial and its merge),
 // so on launches that still hold kDecodePlanMinItems items of 4096 tokens
-// the chunk is 4096 (pages of 64+ tokens keep it within 64 page ids); else
-// decode_chunk_tokens.  The workspace is sized for the shorter chunks, so
+// the chunk is 4096; else decode_chunk_tokens.  Pages of 64+ tokens keep a
+// 4096-token chunk within 64 page ids (one per lane); 16-token aligned pages
+// below 64 tokens span up to 257 and take the four-ids-per-lane kernels
+// (decode_split_ids).  The workspace is sized for the shorter chunks, so
 // either fits it.
 static int decode_split_chunk(int32_t page_size, int32_t batch, int32_t pages_per_seq, int64_t vheads) {
   const int base = decode_chunk_tokens(page_size);
-  if (page_size < 64) return base;
+  if (page_size < 64 && page_size % kDecodeStep != 0) return base;
   const int64_t chunks = ((int64_t)pages_per_seq * page_size + kDecodeLongChunk - 1) / kDecodeLongChunk;
   return (int64_t)batch * chunks * vheads >= kDecodePlanMinItems ? kDecodeLongChunk : base;
+}
+
+// Page ids each lane of decode_split_kernel holds for chunks of `chunk`
+// tokens (aligned pages, chunk <= 4096).  Chunks start at multiples of
+// `chunk`: when page_size divides it a chunk spans chunk / page_size pages,
+// else at most floor((chunk + page_size - 2) / page_size) + 1 (at most 256
+// for pages of 16+ tokens).
+static int decode_split_ids(int32_t page_size, int chunk) {
+  const int span = chunk % page_size == 0 ? chunk / page_size : (chunk + page_size - 2) / page_size + 1;
+  return span > 64 ? 4 : 1;
 }
 
 // Tokens per work item of the generic decode (decode_any_kernel, one wave
@@ -225,12 +238,19 @@ extern "C" size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int
 // arrives with the cache pointers (and scales) set; the rest is filled here.
 // Launch of the split kernel over 1-byte codes of type `code` (kCodeE4M3,
 // kCodeI8, kCodeU8).
-template <int kCode>
+template <int kCode, int kIds>
 static void launch_decode_codes(const DecodeParams& prm, bool cap, bool shared, dim3 grid, dim3 block,
                                 hipStream_t s) {
-  if (!cap && shared) decode_split_kernel<true, false, true, true, kCode><<<grid, block, 0, s>>>(prm);
-  else if (!cap) decode_split_kernel<true, false, true, false, kCode><<<grid, block, 0, s>>>(prm);
-  else decode_split_kernel<true, true, true, false, kCode><<<grid, block, 0, s>>>(prm);
+  if (!cap && shared) decode_split_kernel<true, false, true, true, kCode, kIds><<<grid, block, 0, s>>>(prm);
+  else if (!cap) decode_split_kernel<true, false, true, false, kCode, kIds><<<grid, block, 0, s>>>(prm);
+  else decode_split_kernel<true, true, true, false, kCode, kIds><<<grid, block, 0, s>>>(prm);
+}
+
+template <int kCode>
+static void launch_decode_codes(const DecodeParams& prm, bool cap, bool shared, bool wide, dim3 grid, dim3 block,
+                                hipStream_t s) {
+  if (wide) launch_decode_codes<kCode, 4>(prm, cap, shared, grid, block, s);
+  else launch_decode_codes<kCode, 1>(prm, cap, shared, grid, block, s);
 }
 
 static int decode_common(const char* name, DecodeParams& prm, bool fp8, const uint16_t* q, int64_t q_batch_stride,
@@ -350,9 +370,12 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
     // each kv head's K/V, so the loads stay cacheable (the soft cap keeps the
     // streaming form); bf16 pages with more than 16 went to the generic kernel
     const bool shared = prm.hblocks > 1;
-    if (fp8 && code == kCodeI8) launch_decode_codes<kCodeI8>(prm, cap, shared, grid, block, s);
-    else if (fp8 && code == kCodeU8) launch_decode_codes<kCodeU8>(prm, cap, shared, grid, block, s);
-    else if (fp8) launch_decode_codes<kCodeE4M3>(prm, cap, shared, grid, block, s);
+    const bool wide = aligned && decode_split_ids(page_size, prm.chunk) == 4;
+    if (fp8 && code == kCodeI8) launch_decode_codes<kCodeI8>(prm, cap, shared, wide, grid, block, s);
+    else if (fp8 && code == kCodeU8) launch_decode_codes<kCodeU8>(prm, cap, shared, wide, grid, block, s);
+    else if (fp8) launch_decode_codes<kCodeE4M3>(prm, cap, shared, wide, grid, block, s);
+    else if (wide && !cap) decode_split_kernel<true, false, false, false, kCodeE4M3, 4><<<grid, block, 0, s>>>(prm);
+    else if (wide) decode_split_kernel<true, true, false, false, kCodeE4M3, 4><<<grid, block, 0, s>>>(prm);
     else if (aligned && !cap) decode_split_kernel<true, false><<<grid, block, 0, s>>>(prm);
     else if (aligned) decode_split_kernel<true, true><<<grid, block, 0, s>>>(prm);
     else if (!cap) decode_split_kernel<false, false><<<grid, block, 0, s>>>(prm);

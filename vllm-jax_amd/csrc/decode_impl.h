@@ -169,14 +169,18 @@ __host__ __device__ inline int decode_chunk_tokens(int page_size) { return page_
 // red_m / red_l are LDS arrays of [kWaves][16][d] and [kWaves][16] floats.
 // kAligned: page_size % 16 == 0, so a 16-token step never crosses a page and
 // the chunk's page ids (at most 64) are read once, one per lane.
+// kIds: page ids each lane holds (aligned path): a chunk spans at most
+// 64 kIds pages.
 // kFp8: K/V pages hold 1-byte codes with per-token scales
 // (decode_paged_attention.py:72-81,108-115), float8 e4m3 or integers by
 // kCode: K is widened to bf16 exactly and its logits multiplied by the
 // token's K scale; P is multiplied by the token's V scale before PV.  Half
 // the K/V bytes of the bf16 path.
-template <int kWaves, bool kAligned, bool kSoftCap, bool kFp8 = false, bool kShared = false, int kCode = kCodeE4M3>
+template <int kWaves, bool kAligned, bool kSoftCap, bool kFp8 = false, bool kShared = false, int kCode = kCodeE4M3,
+          int kIds = 1>
 __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, float* red_o, float* red_m,
                                             float* red_l) {
+  static_assert(kIds == 1 || kIds == 4, "one or four page ids per lane");
   static_assert(kWaves == 4 || kWaves == 8, "the combine splits d over the waves");
   static_assert(!kFp8 || kAligned, "float8 pages need 16-token aligned steps");
   constexpr int kBufs = kFp8 ? kDecodeBufsFp8 : kDecodeBufs;
@@ -220,10 +224,26 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
   // Page ids of the chunk, one per lane (aligned path).
   const int lp_first = t_begin / p.page_size;
   int32_t my_page = 0;
+  int32_t my_page_hi[kIds == 4 ? 3 : 1] = {};  // (kIds == 4) page ids lp_first + 64 (j + 1) + lane
   if constexpr (kAligned) {
     const int lp = lp_first + lane;
     if (lp < p.pages_per_seq) my_page = safe_page(bt_row, lp, p.num_pages);
+    if constexpr (kIds == 4) {
+#pragma unroll
+      for (int j = 0; j < 3; ++j)
+        if (lp + 64 * (j + 1) < p.pages_per_seq) my_page_hi[j] = safe_page(bt_row, lp + 64 * (j + 1), p.num_pages);
+    }
   }
+  // the page id of the chunk's page idx (wave-uniform)
+  auto chunk_page = [&](int idx) __attribute__((always_inline)) -> int32_t {
+    if constexpr (kIds == 1) {
+      return __builtin_amdgcn_readlane(my_page, idx);
+    } else {
+      const int k = idx >> 6;
+      const int32_t v = k == 0 ? my_page : (k == 1 ? my_page_hi[0] : (k == 2 ? my_page_hi[1] : my_page_hi[2]));
+      return __builtin_amdgcn_readlane(v, idx & 63);
+    }
+  };
 
   // Q^T operand: k-step s uses d chunk kchunk(s) for both Q and K (any
   // bijection works for a dot product).  bf16 pages: chunk 4s + g.  Float8
@@ -276,7 +296,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
       int64_t rs = 0;
       if (valid) {
         const int lp = t0 / p.page_size;
-        const int32_t page = __builtin_amdgcn_readlane(my_page, lp - lp_first);
+        const int32_t page = chunk_page(lp - lp_first);
         const int off = t0 - lp * p.page_size;
         const int64_t base = (int64_t)page * p.page_stride + (int64_t)off * p.slot_stride + head_off;
         kbase = p.k8 + base;
@@ -301,7 +321,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
       int64_t rs = 0;
       if (valid) {
         const int lp = t0 / p.page_size;
-        const int32_t page = __builtin_amdgcn_readlane(my_page, lp - lp_first);
+        const int32_t page = chunk_page(lp - lp_first);
         const int64_t base = (int64_t)page * p.page_stride +
                              (int64_t)(t0 - lp * p.page_size) * p.slot_stride + head_off;
         kbase = p.k_cache + base;
