@@ -141,9 +141,9 @@ static int decode_chunks(int32_t pages_per_seq, int32_t page_size, int32_t head_
 // (q, the chunk's page ids, the waves' combine, a partial and its merge),
 // so on launches that still hold kDecodePlanMinItems items of 4096 tokens
 // the chunk is 4096; else decode_chunk_tokens.  Pages of 64+ tokens keep a
-// 4096-token chunk within 64 page ids (one per lane); 16-token aligned pages
-// below 64 tokens span up to 257 and take the four-ids-per-lane kernels
-// (decode_split_ids).  The workspace is sized for the shorter chunks, so
+// 4096-token chunk within 64 page ids (one per lane); pages of 16, 32 or 48
+// tokens span 256, 128 or up to 87 and take the four-ids-per-lane kernels
+// (decode_chunk_span).  The workspace is sized for the shorter chunks, so
 // either fits it.
 static int decode_split_chunk(int32_t page_size, int32_t batch, int32_t pages_per_seq, int64_t vheads) {
   const int base = decode_chunk_tokens(page_size);
@@ -152,14 +152,14 @@ static int decode_split_chunk(int32_t page_size, int32_t batch, int32_t pages_pe
   return (int64_t)batch * chunks * vheads >= kDecodePlanMinItems ? kDecodeLongChunk : base;
 }
 
-// Page ids each lane of decode_split_kernel holds for chunks of `chunk`
-// tokens (aligned pages, chunk <= 4096).  Chunks start at multiples of
-// `chunk`: when page_size divides it a chunk spans chunk / page_size pages,
-// else at most floor((chunk + page_size - 2) / page_size) + 1 (at most 256
-// for pages of 16+ tokens).
-static int decode_split_ids(int32_t page_size, int chunk) {
-  const int span = chunk % page_size == 0 ? chunk / page_size : (chunk + page_size - 2) / page_size + 1;
-  return span > 64 ? 4 : 1;
+// Pages a chunk of `chunk` tokens spans at most (aligned pages).  Chunks
+// start at multiples of `chunk`: when page_size divides it a chunk spans
+// chunk / page_size pages, else at most floor((chunk + page_size - 2) /
+// page_size) + 1.  decode_split_kernel holds one page id per lane up to 64
+// pages and four (kIds = 4) up to 256: every chunk of 4096 tokens or less
+// over pages of 16+ tokens.
+static int decode_chunk_span(int32_t page_size, int chunk) {
+  return chunk % page_size == 0 ? chunk / page_size : (chunk + page_size - 2) / page_size + 1;
 }
 
 // Tokens per work item of the generic decode (decode_any_kernel, one wave
@@ -333,6 +333,11 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
                     : decode_split_chunk(page_size, batch, pages_per_seq, vheads);
   prm.n_chunks =
       pages_per_seq > 0 ? (int)(((int64_t)pages_per_seq * page_size + prm.chunk - 1) / prm.chunk) : 0;
+  // (this kernel, aligned pages) the chunk's page ids, one or four per lane
+  const int span = !any_d && page_size % kDecodeStep == 0 ? decode_chunk_span(page_size, prm.chunk) : 0;
+  if (span > 4 * 64)
+    return fail(PA_ERR_UNSUPPORTED, "%s: a %d-token chunk spans %d pages of %d tokens (max 256)", name, prm.chunk,
+                span, page_size);
   prm.soft_cap = soft_cap > 0.f ? soft_cap : 0.f;
   prm.logit_scale = prm.soft_cap > 0.f ? scale : scale * kLog2e;
   const size_t parts = (size_t)batch * num_heads * prm.n_chunks;
@@ -370,7 +375,7 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
     // each kv head's K/V, so the loads stay cacheable (the soft cap keeps the
     // streaming form); bf16 pages with more than 16 went to the generic kernel
     const bool shared = prm.hblocks > 1;
-    const bool wide = aligned && decode_split_ids(page_size, prm.chunk) == 4;
+    const bool wide = span > 64;
     if (fp8 && code == kCodeI8) launch_decode_codes<kCodeI8>(prm, cap, shared, wide, grid, block, s);
     else if (fp8 && code == kCodeU8) launch_decode_codes<kCodeU8>(prm, cap, shared, wide, grid, block, s);
     else if (fp8) launch_decode_codes<kCodeE4M3>(prm, cap, shared, wide, grid, block, s);
