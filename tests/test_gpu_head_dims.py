@@ -119,12 +119,13 @@ def test_decode_head_dims_work_list(pkg, dev, d):
     assert not ora.bf16_to_f32(u16(out))[lens == 0].any()
 
 
-@pytest.mark.parametrize("d,hi,width,edges", [
-    (96, 5000, 32, [1023, 1024, 1025, 2048, 3073]),     # 1024-token items
-    (48, 5000, 32, [1023, 1024, 1025, 2048, 3073]),     # 1024-token items
-    (256, 16384, 64, [4095, 4096, 4097, 8192, 12289]),  # 4096-token items (a launch of 2 048+ of them)
+@pytest.mark.parametrize("d,hi,bs,width,edges", [
+    (96, 5000, 256, 32, [1023, 1024, 1025, 2048, 3073]),     # 1024-token items
+    (48, 5000, 256, 32, [1023, 1024, 1025, 2048, 3073]),     # 1024-token items
+    (256, 16384, 256, 64, [4095, 4096, 4097, 8192, 12289]),  # 4096-token items (a launch of 2 048+ of them)
+    (256, 16384, 16, 1024, [4095, 4096, 4097, 8192, 12289]),  # the same over 16-token pages
 ])
-def test_decode_head_dims_item_lengths(pkg, dev, d, hi, width, edges):
+def test_decode_head_dims_item_lengths(pkg, dev, d, hi, bs, width, edges):
     """The generic decode's item lengths by head size over contexts of
     several items (160 sequences x 8 kv heads, on the work list): lengths 0
     and 1 and both sides of the item boundaries; every sequence against the
@@ -132,9 +133,9 @@ def test_decode_head_dims_item_lengths(pkg, dev, d, hi, width, edges):
     rng = np.random.default_rng(60 + d)
     lens = rng.integers(2, hi, size=160)
     lens[:2 + len(edges)] = [0, 1] + edges
-    db = wl.make_decode(lens.tolist(), num_heads=32, num_kv_heads=8, page_size=256, head_dim=d,
+    db = wl.make_decode(lens.tolist(), num_heads=32, num_kv_heads=8, page_size=bs, head_dim=d,
                         rng=np.random.default_rng(61 + d), table_width=width)
-    print(f"generic decode d={d}: {db.batch} sequences, contexts up to {hi}", flush=True)
+    print(f"generic decode d={d}: {db.batch} sequences, contexts up to {hi}, {bs}-token pages", flush=True)
     out, _ = _run_and_check(pkg, dev, db, seed=9)
     assert not ora.bf16_to_f32(u16(out))[0].any()
 

@@ -165,8 +165,9 @@ static int decode_chunk_span(int32_t page_size, int chunk) {
 // Tokens per work item of the generic decode (decode_any_kernel, one wave
 // per item): 1024 at the head sizes of decode_any_short_chunk; 4096 at head
 // size 256 on launches that still hold kDecodePlanMinItems such items (-1.7 %
-// there, where 4096 cost 4-9 % at 64, 96 and 32 q heads per kv head); else
-// decode_chunk_tokens.
+// there over 256-token pages, -3.4 % over 16-token ones, where 4096 cost
+// 4-9 % at 64, 96 and 32 q heads per kv head; its page ids are scalar loads
+// per step, so any chunk fits); else decode_chunk_tokens.
 static int decode_any_chunk(int32_t head_dim, int32_t page_size, int32_t batch, int32_t pages_per_seq,
                             int64_t vheads) {
   const int base = decode_chunk_tokens(page_size);
