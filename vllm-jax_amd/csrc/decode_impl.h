@@ -159,18 +159,17 @@ __device__ __forceinline__ int xcd_grouped_item(int bid, int nb) {
   return x * q8 + min(x, r8) + k;
 }
 
-// Tokens per workgroup (the shorter chunks; large launches with pages of
-// 64+ tokens take 4096): the aligned path keeps the chunk's page ids in one
-// VGPR (one per lane), so a chunk spans at most 64 pages.
+// Tokens per workgroup (the shorter chunks; large launches over pages of 16+
+// tokens that are a multiple of 16 take 4096): with one page id per lane
+// (one VGPR) a chunk spans at most 64 pages.
 __host__ __device__ inline int decode_chunk_tokens(int page_size) { return page_size >= 32 ? 2048 : 1024; }
 
 // One decode work item (sequence, chunk, kv head) numbered `item`, run by
 // kWaves wavefronts (threads 0 .. 64*kWaves-1 of the workgroup).  red_o /
 // red_m / red_l are LDS arrays of [kWaves][16][d] and [kWaves][16] floats.
 // kAligned: page_size % 16 == 0, so a 16-token step never crosses a page and
-// the chunk's page ids (at most 64) are read once, one per lane.
-// kIds: page ids each lane holds (aligned path): a chunk spans at most
-// 64 kIds pages.
+// the chunk's page ids are read once, kIds per lane (lane l holds the ids of
+// the chunk's pages l, l + 64, ...): a chunk spans at most 64 kIds pages.
 // kFp8: K/V pages hold 1-byte codes with per-token scales
 // (decode_paged_attention.py:72-81,108-115), float8 e4m3 or integers by
 // kCode: K is widened to bf16 exactly and its logits multiplied by the
