@@ -220,6 +220,10 @@ def test_mixed_workspace_size():
     part = r256(2 * 16 * 2 * (128 + 2) * 4)
     assert lib.pa_mixed_workspace_size(4, 2, 100, 16, 8, 128, 1, 8192) == part + 256 + 32 * 8
     assert lib.pa_mixed_workspace_size(4, 2, 100, 16, 8, 128, 1, 4096) == 256 + 32 * 8
+    # 16-token pages: 4096-token chunks too (256 page ids, four per lane): a 400-page
+    # table is 2 chunks; pairs 3 x 2 decode + 2 x 3 prefill (128-token q tiles) = 12
+    part = r256(3 * 16 * 2 * (128 + 2) * 4)
+    assert lib.pa_mixed_workspace_size(5, 3, 300, 16, 8, 128, 400, 16) == part + 256 + 32 * 16
     # G = 32: two decode pairs per (sequence, chunk), one per block of 16 q heads;
     # 8-token q tiles (13 per prefill sequence)
     assert lib.pa_mixed_workspace_size(4, 2, 100, 32, 1, 128, 8, 256) == 256 + 32 * 32

@@ -186,6 +186,7 @@ def test_decode_head_dim_noalloc_matches_pa_decode(pkg, dev):
     ([700, 30], [100, 5], [0, 40], 40, 2, 48, 256, None),                 # G = 20, 48-token pages
     ([], [17, 128, 300], [0, 0, 0], 16, 8, 16, 80, None),                 # no decode sequence
     ([10, 600, 4096], [], [], 16, 4, 80, 112, None),                      # no prefill sequence, 80-token pages
+    ([5000, 2000], [100], [0], 16, 8, 16, 96, None),                       # 16-token pages, 4096-token chunks
 ])
 def test_mixed_head_dims(pkg, dev, dec, pre_q, pre_p, h, hkv, bs, d, cap):
     rng = np.random.default_rng(len(dec) * 100 + h + d)

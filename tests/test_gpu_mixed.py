@@ -64,7 +64,9 @@ def _run(pkg, dev, q, kc, vc, bt, cu, kv, pos, nd, max_q, soft_cap=None, decode_
     ([700, 30], [100], [0], 64, 8, 64, 0),                                 # G = 8
     ([50, 60], [70], [10], 8, 8, 32, 2),                                   # MHA
     ([100, 30], [50, 20], [0, 5], 8, 2, 24, 0),                            # pages not 16-aligned
-    ([3000, 5000, 100], [90], [0], 8, 2, 48, 0),                           # 48-token pages, 3072-token chunks
+    ([3000, 5000, 100], [90], [0], 8, 2, 48, 0),                           # 48-token pages, 4080-token chunks (85 ids)
+    ([5000, 4096, 4097, 1500], [100, 30], [0, 40], 16, 8, 16, 0),          # 16-token pages, 4096-token chunks (256 ids)
+    ([9000, 4100], [64], [0], 32, 8, 32, 0),                               # 32-token pages, 4096-token chunks (128 ids)
     ([], [17, 128, 300], [0, 0, 0], 16, 8, 256, 0),                        # no decode sequence
     ([10, 600, 4096], [], [], 16, 8, 256, 1),                              # no prefill sequence
     ([700, 30, 0], [100, 7], [0, 20], 40, 2, 64, 0),                       # G = 20: a 16 + 4 head split

@@ -187,7 +187,7 @@ mixed_plan_kernel(MixedParams m, int32_t* __restrict__ plan) {
   if (tid == 0) plan[0] = count;
 }
 
-template <bool kSoftCap, int kPagingP, bool kAlignedD>
+template <bool kSoftCap, int kPagingP, bool kAlignedD, int kIdsD>
 __global__ void __launch_bounds__(kThreads, 1)
 mixed_kernel(MixedParams m) {
   const int bid = blockIdx.x;
@@ -246,7 +246,8 @@ mixed_kernel(MixedParams m) {
     // [8 waves][16][d] floats fill the K ring exactly; m and l go to the V ring
     float* red_o = reinterpret_cast<float*>(&k_lds[0][0]);
     float* red_m = reinterpret_cast<float*>(&v_lds[0][0]);
-    decode_item<kMixedDecodeWaves, kAlignedD, kSoftCap>(m.dec, dec, red_o, red_m, red_m + 16 * kMixedDecodeWaves);
+    decode_item<kMixedDecodeWaves, kAlignedD, kSoftCap, false, false, kCodeE4M3, kIdsD>(m.dec, dec, red_o, red_m,
+                                                                                        red_m + 16 * kMixedDecodeWaves);
     return;
   }
   if (pre) prefill_run<kSoftCap, kPagingP>(m.pre, w);
@@ -257,13 +258,15 @@ static_assert(sizeof(float) * kMixedDecodeWaves * 16 * kPHeadDim <= sizeof(uint1
 
 // Tokens per decode item (a multiple of the 16-token step): eight waves take
 // up to twice the chunk of the four-wave decode kernel.  With 16-aligned pages
-// the chunk is whole pages, at most 64 of them (one page id per lane).
-// Pages above 4096 tokens get 4096-token chunks inside one page (the
-// aligned decode item walks a chunk that starts inside a page).
+// the chunk is the whole pages that fit 4096 tokens: up to 64 of them (one
+// page id per lane) from 64-token pages on, up to 256 below (four per lane:
+// 256 pages of 16 tokens, 128 of 32, 85 of 48).  Pages above 4096 tokens get
+// 4096-token chunks inside one page (the aligned decode item walks a chunk
+// that starts inside a page).
 static int mixed_decode_chunk(int page_size) {
   constexpr int kMax = 4096;
   if (page_size % kDecodeStep != 0 || page_size >= kMax) return kMax;
-  return 64 * page_size <= kMax ? 64 * page_size : (kMax / page_size) * page_size;
+  return (kMax / page_size) * page_size;
 }
 
 static int mixed_decode_chunks(int32_t pages_per_seq, int32_t page_size) {
@@ -504,16 +507,22 @@ extern "C" int pa_mixed(const uint16_t* q, int64_t q_tok_stride, int64_t q_head_
   const dim3 grid((unsigned)r4), block(kThreads);
   const int paging_p = prefill_paging(page_size, slot_stride);
   const bool aligned_d = page_size % kDecodeStep == 0;  // every kPageTile / kPageWave size is
+  // (aligned) a decode chunk of more than 64 pages: four page ids per lane
+  // (pages below 64 tokens, so never with whole-tile prefill paging; always
+  // with the per-wave paging of 16- and 32-token pages)
+  const bool wide_d = aligned_d && dp.chunk / page_size > 64;
   if (cap > 0.f) {
-    if (paging_p == kPageTile) mixed_kernel<true, kPageTile, true><<<grid, block, 0, s>>>(m);
-    else if (paging_p == kPageWave) mixed_kernel<true, kPageWave, true><<<grid, block, 0, s>>>(m);
-    else if (aligned_d) mixed_kernel<true, kPageLane, true><<<grid, block, 0, s>>>(m);
-    else mixed_kernel<true, kPageLane, false><<<grid, block, 0, s>>>(m);
+    if (paging_p == kPageTile) mixed_kernel<true, kPageTile, true, 1><<<grid, block, 0, s>>>(m);
+    else if (paging_p == kPageWave) mixed_kernel<true, kPageWave, true, 4><<<grid, block, 0, s>>>(m);
+    else if (wide_d) mixed_kernel<true, kPageLane, true, 4><<<grid, block, 0, s>>>(m);
+    else if (aligned_d) mixed_kernel<true, kPageLane, true, 1><<<grid, block, 0, s>>>(m);
+    else mixed_kernel<true, kPageLane, false, 1><<<grid, block, 0, s>>>(m);
   } else {
-    if (paging_p == kPageTile) mixed_kernel<false, kPageTile, true><<<grid, block, 0, s>>>(m);
-    else if (paging_p == kPageWave) mixed_kernel<false, kPageWave, true><<<grid, block, 0, s>>>(m);
-    else if (aligned_d) mixed_kernel<false, kPageLane, true><<<grid, block, 0, s>>>(m);
-    else mixed_kernel<false, kPageLane, false><<<grid, block, 0, s>>>(m);
+    if (paging_p == kPageTile) mixed_kernel<false, kPageTile, true, 1><<<grid, block, 0, s>>>(m);
+    else if (paging_p == kPageWave) mixed_kernel<false, kPageWave, true, 4><<<grid, block, 0, s>>>(m);
+    else if (wide_d) mixed_kernel<false, kPageLane, true, 4><<<grid, block, 0, s>>>(m);
+    else if (aligned_d) mixed_kernel<false, kPageLane, true, 1><<<grid, block, 0, s>>>(m);
+    else mixed_kernel<false, kPageLane, false, 1><<<grid, block, 0, s>>>(m);
   }
   int rc = launch_status("pa_mixed");
   if (rc || partials == 0 || num_decodes == 0) return rc;
