@@ -259,9 +259,9 @@ def test_prefill_fp8_shared_pages_widened_once(pkg, dev, width):
     prefix held once in the pool).  The widening keeps one bf16 copy per
     distinct page: the slot count it leaves in the workspace (after the
     widened pages, the remapped table and the slots' owner entries) is the
-    number of distinct pages in use.  A table of 3 x 3000 entries is past
-    what the planner's hash holds; then every used entry gets its own slot.
-    Outputs match the oracle over the same codes in both cases."""
+    number of distinct pages in use, also for a table of 3 x 3000 entries
+    (more than 2^13 entries: the planner's largest hash, which holds up to
+    2^13 distinct pages).  Outputs match the oracle over the same codes."""
     import torch
     bs, h, hkv = 16, 8, 2
     rng = np.random.default_rng(width)
@@ -301,11 +301,66 @@ def test_prefill_fp8_shared_pages_widened_once(pkg, dev, width):
     slots = int(ws[at:at + 4].cpu().numpy().view(np.int32)[0])
     used = [int(x) for b in range(3) for x in bt[b, :-(-kv[b] // bs)]]
     print(f"fp8 prefill, {entries} table entries: {slots} widened pages, {len(set(used))} distinct, {len(used)} used")
-    assert slots == (len(set(used)) if entries <= 1 << 13 else len(used))
+    assert slots == len(set(used))
     want = ora.prefill_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, cu, pos,
                                  cu_seqlens_k=cuk, k_scales_pages=ks, v_scales_pages=vs)
     err = np.abs(ora.bf16_to_f32(u16(out)) - ora.bf16_to_f32(want)).max()
     print(f"fp8 prefill shared pages max-abs err {err:.3e}")
+    assert err <= TOL
+
+
+def test_prefill_fp8_more_distinct_pages_than_the_hash_holds(pkg, dev):
+    """Three sequences with long cached contexts of their own, 8 382
+    distinct 16-token pages in use: more than the planner's hash holds
+    (2^13), so every used entry gets its own slot, the four pages sequences
+    0 and 1 share included (the slot count is the number of used entries,
+    not of distinct pages).  Outputs match the oracle over the same codes."""
+    import torch
+    bs, h, hkv = 16, 8, 2
+    rng = np.random.default_rng(88)
+    prefix, lens = [45056, 45056, 44000], [8, 20, 5]
+    shared = 4  # sequence 1's first pages are sequence 0's
+    kv = [p + n for p, n in zip(prefix, lens)]
+    pages = [-(-k // bs) for k in kv]
+    nb = sum(pages) - shared + 3
+    kq, vq, ks, vs = _quantized_pool(rng, nb, bs, hkv)
+    perm = rng.permutation(nb)
+    width = max(pages)
+    bt = np.full((3, width), -1, np.int32)
+    c = 0
+    for b in range(3):
+        start = shared if b == 1 else 0
+        if b == 1:
+            bt[1, :shared] = bt[0, :shared]
+        bt[b, start:pages[b]] = perm[c:c + pages[b] - start]
+        c += pages[b] - start
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    cuk = np.concatenate([[0], np.cumsum(kv)]).astype(np.int32)
+    pos = np.concatenate([np.arange(p, p + n) for p, n in zip(prefix, lens)]).astype(np.int32)
+    q = _bf16(rng, (int(cu[-1]), h, 128))
+    lib = pkg._lib.load()
+    need = lib.pa_prefill_fp8_workspace_size(3, width, bs, hkv, 128, max(lens), h)
+    ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+    i32 = lambda x: torch.as_tensor(np.ascontiguousarray(x, dtype=np.int32), device=dev)
+    kd = torch.from_numpy(kq).to(dev).view(torch.float8_e4m3fn)
+    vd = torch.from_numpy(vq).to(dev).view(torch.float8_e4m3fn)
+    out = pkg.prefill_paged_attention(from_u16(q, dev), kd.permute(2, 0, 1, 3), vd.permute(2, 0, 1, 3), i32(bt),
+                                      i32(cu), None, i32(pos), max_seqlen_bucket=max(lens), cu_seqlens_k=i32(cuk),
+                                      k_scales_pages=torch.from_numpy(ks).to(dev),
+                                      v_scales_pages=torch.from_numpy(vs).to(dev), workspace=ws)
+    torch.cuda.synchronize()
+    entries = 3 * width
+    page_elems = bs * hkv * 128
+    at = 2 * entries * page_elems * 2 + 2 * entries * 4
+    slots = int(ws[at:at + 4].cpu().numpy().view(np.int32)[0])
+    used = [int(x) for b in range(3) for x in bt[b, :pages[b]]]
+    print(f"fp8 prefill, {len(set(used))} distinct pages: {slots} widened, {len(used)} used", flush=True)
+    assert len(set(used)) > 1 << 13
+    assert slots == len(used)
+    want = ora.prefill_attention(q, kq.transpose(2, 0, 1, 3), vq.transpose(2, 0, 1, 3), bt, cu, pos,
+                                 cu_seqlens_k=cuk, k_scales_pages=ks, v_scales_pages=vs)
+    err = np.abs(ora.bf16_to_f32(u16(out)) - ora.bf16_to_f32(want)).max()
+    print(f"fp8 prefill, one slot per entry: max-abs err {err:.3e}", flush=True)
     assert err <= TOL
 
 

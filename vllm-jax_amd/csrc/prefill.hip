@@ -192,9 +192,13 @@ prefill_prep_kernel(PrefillParams p, int32_t* __restrict__ plan) {
 // fp8_pages_plan_kernel (one workgroup) finds the distinct pages with an
 // open-addressing hash in LDS: keys are physical page ids, and the thread
 // whose atomicCAS claims a key takes the next slot from an LDS counter and
-// records its entry as the slot's owner.  Tables with more entries than the
-// hash holds (hbits == 0) get one slot per used entry.
-constexpr int kFp8HashBits = 14;  // LDS hash of 2^14 slots: tables of up to 2^13 entries
+// records its entry as the slot's owner.  The hash has 2^hbits slots, at
+// least twice the table's entries up to 2^kFp8HashBits; a larger table
+// keeps the largest hash, which holds up to 2^(hbits - 1) distinct pages
+// (the table's entries repeat the pages of shared prefixes, and small pages
+// make many entries).  A launch with more distinct pages than that (or
+// hbits == 0) gives every used entry its own slot instead.
+constexpr int kFp8HashBits = 14;  // LDS hash of 2^14 slots: up to 2^13 distinct pages
 
 // Physical page of table entry e, or -1 when the entry is not in use.
 __device__ __forceinline__ int32_t fp8_entry_page(const int32_t* __restrict__ bt, int64_t bt_stride,
@@ -221,60 +225,77 @@ fp8_pages_plan_kernel(const int32_t* __restrict__ bt, int64_t bt_stride, int32_t
   __shared__ int32_t keys[1 << kFp8HashBits];
   __shared__ int32_t slots[1 << kFp8HashBits];
   __shared__ int32_t n_slots;
+  __shared__ int32_t overflow;
   const int tid = threadIdx.x;
   const int64_t entries = (int64_t)batch * pages_per_seq;
   const uint32_t hmask = hbits ? (1u << hbits) - 1u : 0u;
+  const int32_t max_distinct = hbits ? 1 << (hbits - 1) : 0;
   if (hbits)
     for (uint32_t h = tid; h <= hmask; h += blockDim.x) keys[h] = -1;
-  if (tid == 0) n_slots = 0;
-  __syncthreads();
-  for (int64_t e = tid; e < entries; e += blockDim.x) {
-    const int32_t page = fp8_entry_page(bt, bt_stride, pages_per_seq, page_size, num_pages, cu_q, cu_k, e);
-    if (page < 0) continue;
-    if (!hbits) {  // no hash: every used entry is its own slot
-      owner[atomicAdd(&n_slots, 1)] = (int32_t)e;
-      continue;
-    }
-    // the hash has at least twice as many slots as there are entries, so a
-    // free key is always found within the probe
-    uint32_t h = fp8_page_hash(page, hbits);
-    for (;;) {
-      const int32_t prev = atomicCAS(&keys[h], -1, page);
-      if (prev == -1) {
-        const int32_t sl = atomicAdd(&n_slots, 1);
-        slots[h] = sl;
-        owner[sl] = (int32_t)e;
-        break;
-      }
-      if (prev == page) break;
-      h = (h + 1) & hmask;
-    }
+  if (tid == 0) {
+    n_slots = 0;
+    overflow = hbits ? 0 : 1;
   }
   __syncthreads();
-  for (int64_t e = tid; e < entries; e += blockDim.x) {
-    const int32_t page = fp8_entry_page(bt, bt_stride, pages_per_seq, page_size, num_pages, cu_q, cu_k, e);
-    int32_t sl = -1;
-    if (page >= 0 && hbits) {
+  if (hbits) {
+    for (int64_t e = tid; e < entries; e += blockDim.x) {
+      const int32_t page = fp8_entry_page(bt, bt_stride, pages_per_seq, page_size, num_pages, cu_q, cu_k, e);
+      if (page < 0) continue;
+      // at most one pass over the hash: a full hash ends the probe (the
+      // launch then falls back to one slot per entry)
       uint32_t h = fp8_page_hash(page, hbits);
-      while (keys[h] != page) h = (h + 1) & hmask;  // claimed above, so present
-      sl = slots[h];
+      for (uint32_t probe = 0; probe <= hmask; ++probe) {
+        const int32_t prev = atomicCAS(&keys[h], -1, page);
+        if (prev == -1) {
+          const int32_t sl = atomicAdd(&n_slots, 1);
+          slots[h] = sl;
+          if (sl < max_distinct) owner[sl] = (int32_t)e;
+          else overflow = 1;
+          break;
+        }
+        if (prev == page) break;
+        h = (h + 1) & hmask;
+        if (probe == hmask) overflow = 1;
+      }
     }
-    bt_out[e] = sl;
+    __syncthreads();
   }
-  if (!hbits) {  // one slot per used entry: the slot order is the claim order
+  if (!overflow) {
+    // every page in use holds a key, so each lookup ends
+    for (int64_t e = tid; e < entries; e += blockDim.x) {
+      const int32_t page = fp8_entry_page(bt, bt_stride, pages_per_seq, page_size, num_pages, cu_q, cu_k, e);
+      int32_t sl = -1;
+      if (page >= 0) {
+        uint32_t h = fp8_page_hash(page, hbits);
+        while (keys[h] != page) h = (h + 1) & hmask;
+        sl = slots[h];
+      }
+      bt_out[e] = sl;
+    }
+  } else {
+    // one slot per used entry, in claim order
+    __syncthreads();
+    if (tid == 0) n_slots = 0;
+    __syncthreads();
+    for (int64_t e = tid; e < entries; e += blockDim.x) {
+      const int32_t page = fp8_entry_page(bt, bt_stride, pages_per_seq, page_size, num_pages, cu_q, cu_k, e);
+      if (page >= 0) owner[atomicAdd(&n_slots, 1)] = (int32_t)e;
+      else bt_out[e] = -1;
+    }
     __syncthreads();
     for (int32_t sl = tid; sl < n_slots; sl += blockDim.x) bt_out[owner[sl]] = sl;
   }
   if (tid == 0) *count = n_slots;
 }
 
-// Slot i of the compact pool: the page of entry owner[i], widened.
-// kWidenSplit workgroups per possible slot (the table's entry count), each
-// taking a kWidenSplit-th of the page's (slot, head) rows: with one
-// workgroup per page too few loads were in flight (a distinct page is
-// 1 MiB of codes); those past the number of distinct pages return at once.
-// 16 codes per thread and step.
-constexpr int kWidenSplit = 16;
+// Slot i of the compact pool: the page of entry owner[i], widened.  A page
+// is widened in `split` parts, each a split-th of its (slot, head) rows (16
+// codes per thread and step): with one workgroup per page too few loads
+// were in flight (a 256-token page is 1 MiB of codes), so pages take up to
+// kWidenSplit parts of at least one step each.  The grid strides over the
+// (slot, part) units up to the slot count the plan left on the device.
+constexpr int kWidenSplit = 16;        // parts of a page, at most
+constexpr int kWidenMaxBlocks = 8192;  // workgroups of the widening pass, at most
 __global__ void __launch_bounds__(256)
 fp8_pages_widen_kernel(const uint8_t* __restrict__ k8, const uint8_t* __restrict__ v8,
                        const float* __restrict__ ks, const float* __restrict__ vs, int32_t num_pages,
@@ -283,67 +304,69 @@ fp8_pages_widen_kernel(const uint8_t* __restrict__ k8, const uint8_t* __restrict
                        int64_t bt_stride, int32_t pages_per_seq, const int32_t* __restrict__ cu_q,
                        const int32_t* __restrict__ cu_k, int32_t num_kv_heads, const int32_t* __restrict__ owner,
                        const int32_t* __restrict__ count, uint16_t* __restrict__ wk, uint16_t* __restrict__ wv,
-                       int32_t code, int32_t head_dim) {
-  const int32_t sl = blockIdx.x / kWidenSplit;
-  const int part_w = blockIdx.x - sl * kWidenSplit;
-  if (sl >= *count) return;
-  const int64_t page =
-      fp8_entry_page(bt, bt_stride, pages_per_seq, page_size, num_pages, cu_q, cu_k, owner[sl]);  // in use
-  const int rows = page_size * num_kv_heads;  // (slot, head) rows of head_dim codes
-  const int parts = head_dim >> 4;            // 16 codes per part
-  const int64_t wbase = (int64_t)sl * rows * head_dim;
-  const int c_lo = (int)((int64_t)rows * parts * part_w / kWidenSplit);
-  const int c_hi = (int)((int64_t)rows * parts * (part_w + 1) / kWidenSplit);
+                       int32_t code, int32_t head_dim, int32_t split) {
+  const int64_t units = (int64_t)*count * split;
+  for (int64_t u = blockIdx.x; u < units; u += gridDim.x) {
+    const int32_t sl = (int32_t)(u / split);
+    const int part_w = (int)(u - (int64_t)sl * split);
+    const int64_t page =
+        fp8_entry_page(bt, bt_stride, pages_per_seq, page_size, num_pages, cu_q, cu_k, owner[sl]);  // in use
+    const int rows = page_size * num_kv_heads;  // (slot, head) rows of head_dim codes
+    const int parts = head_dim >> 4;            // 16 codes per part
+    const int64_t wbase = (int64_t)sl * rows * head_dim;
+    const int c_lo = (int)((int64_t)rows * parts * part_w / split);
+    const int c_hi = (int)((int64_t)rows * parts * (part_w + 1) / split);
 #pragma unroll 4
-  for (int c = c_lo + threadIdx.x; c < c_hi; c += 256) {
-    const int r = c / parts, part = c - r * parts;  // 16 codes of row r
-    const int slot = r / num_kv_heads, h = r - slot * num_kv_heads;
-    const int64_t src = page * page_stride + (int64_t)slot * slot_stride + (int64_t)h * head_stride + 16 * part;
-    const int64_t sidx = page * sc_page_stride + (int64_t)h * sc_head_stride + slot;
-    const int64_t dst = wbase + (int64_t)r * head_dim + 16 * part;
+    for (int c = c_lo + threadIdx.x; c < c_hi; c += 256) {
+      const int r = c / parts, part = c - r * parts;  // 16 codes of row r
+      const int slot = r / num_kv_heads, h = r - slot * num_kv_heads;
+      const int64_t src = page * page_stride + (int64_t)slot * slot_stride + (int64_t)h * head_stride + 16 * part;
+      const int64_t sidx = page * sc_page_stride + (int64_t)h * sc_head_stride + slot;
+      const int64_t dst = wbase + (int64_t)r * head_dim + 16 * part;
 #pragma unroll
-    for (int which = 0; which < 2; ++which) {
-      const u32x4 x = ld16((which ? v8 : k8) + src);
-      const float sc = (which ? vs : ks)[sidx];
-      u32x4 o[2];
-      // A positive normal power-of-two scale (what pa_kv_store_fp8 writes):
-      // v_cvt_scalef32_pk_bf16_fp8 multiplies by 2^exponent(sc), so one
-      // conversion per pair gives code * sc exactly.  Any other scale:
-      // widen to float32, multiply, round to bf16 once.  The two agree
-      // wherever both apply.
-      const uint32_t sb = __float_as_uint(sc);
-      if (code != kCodeE4M3) {
-        // integer codes (uniform over the launch): the integer times the
-        // scale, rounded to bf16 once
-        const uint32_t flip = code == kCodeI8 ? 0x80808080u : 0u;
-        const float bias = code == kCodeI8 ? 128.f : 0.f;
+      for (int which = 0; which < 2; ++which) {
+        const u32x4 x = ld16((which ? v8 : k8) + src);
+        const float sc = (which ? vs : ks)[sidx];
+        u32x4 o[2];
+        // A positive normal power-of-two scale (what pa_kv_store_fp8 writes):
+        // v_cvt_scalef32_pk_bf16_fp8 multiplies by 2^exponent(sc), so one
+        // conversion per pair gives code * sc exactly.  Any other scale:
+        // widen to float32, multiply, round to bf16 once.  The two agree
+        // wherever both apply.
+        const uint32_t sb = __float_as_uint(sc);
+        if (code != kCodeE4M3) {
+          // integer codes (uniform over the launch): the integer times the
+          // scale, rounded to bf16 once
+          const uint32_t flip = code == kCodeI8 ? 0x80808080u : 0u;
+          const float bias = code == kCodeI8 ? 128.f : 0.f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint32_t c = x[w] ^ flip;
-          o[w >> 1][2 * (w & 1)] = pack_bf16x2(((float)(c & 0xffu) - bias) * sc, ((float)((c >> 8) & 0xffu) - bias) * sc);
-          o[w >> 1][2 * (w & 1) + 1] =
-              pack_bf16x2(((float)((c >> 16) & 0xffu) - bias) * sc, ((float)(c >> 24) - bias) * sc);
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t c = x[w] ^ flip;
+            o[w >> 1][2 * (w & 1)] = pack_bf16x2(((float)(c & 0xffu) - bias) * sc, ((float)((c >> 8) & 0xffu) - bias) * sc);
+            o[w >> 1][2 * (w & 1) + 1] =
+                pack_bf16x2(((float)((c >> 16) & 0xffu) - bias) * sc, ((float)(c >> 24) - bias) * sc);
+          }
+        } else if ((sb & 0x807fffffu) == 0u && sb >= 0x00800000u && sb < 0x7f800000u) {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            o[w >> 1][2 * (w & 1)] =
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[w], sc, false));
+            o[w >> 1][2 * (w & 1) + 1] =
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[w], sc, true));
+          }
+        } else {
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], false);
+            const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], true);
+            o[w >> 1][2 * (w & 1)] = pack_bf16x2(lo[0] * sc, lo[1] * sc);
+            o[w >> 1][2 * (w & 1) + 1] = pack_bf16x2(hi[0] * sc, hi[1] * sc);
+          }
         }
-      } else if ((sb & 0x807fffffu) == 0u && sb >= 0x00800000u && sb < 0x7f800000u) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          o[w >> 1][2 * (w & 1)] =
-              __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[w], sc, false));
-          o[w >> 1][2 * (w & 1) + 1] =
-              __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8((int)x[w], sc, true));
-        }
-      } else {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], false);
-          const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)x[w], true);
-          o[w >> 1][2 * (w & 1)] = pack_bf16x2(lo[0] * sc, lo[1] * sc);
-          o[w >> 1][2 * (w & 1) + 1] = pack_bf16x2(hi[0] * sc, hi[1] * sc);
-        }
+        uint16_t* d = (which ? wv : wk) + dst;
+        st16(d, o[0]);
+        st16(d + 8, o[1]);
       }
-      uint16_t* d = (which ? wv : wk) + dst;
-      st16(d, o[0]);
-      st16(d + 8, o[1]);
     }
   }
 }
@@ -581,16 +604,20 @@ static int prefill_quant(const char* name, int32_t code, const uint16_t* q, int6
   // an LDS hash of at least twice the entries finds the distinct pages
   int hbits = 6;
   while (hbits <= kFp8HashBits && ((int64_t)1 << hbits) < 2 * entries) ++hbits;
-  if (hbits > kFp8HashBits) hbits = 0;
+  if (hbits > kFp8HashBits) hbits = kFp8HashBits;  // the plan falls back past 2^(hbits - 1) distinct pages
   fp8_pages_plan_kernel<<<dim3(1), dim3(1024), 0, s>>>(block_tables, bt_stride, pages_per_seq, batch, page_size,
                                                        num_pages, cu_seqlens_q, cu_seqlens_k, hbits, bt2, owner,
                                                        n_slots);
   int rc = launch_status(name);
   if (rc) return rc;
-  fp8_pages_widen_kernel<<<dim3((unsigned)(entries * kWidenSplit)), dim3(256), 0, s>>>(
+  // parts per page: a step (256 threads x 16 codes) each, at most kWidenSplit
+  const int64_t page_steps = (int64_t)page_size * num_kv_heads * (head_dim / 16) / 256;
+  const int split = (int)std::max<int64_t>(1, std::min<int64_t>(kWidenSplit, page_steps));
+  const int64_t widen_blocks = std::min<int64_t>(entries * split, kWidenMaxBlocks);
+  fp8_pages_widen_kernel<<<dim3((unsigned)widen_blocks), dim3(256), 0, s>>>(
       k_cache, v_cache, k_scales, v_scales, num_pages, page_size, page_stride, slot_stride, head_stride,
       scale_page_stride, scale_head_stride, block_tables, bt_stride, pages_per_seq, cu_seqlens_q, cu_seqlens_k,
-      num_kv_heads, owner, n_slots, wk, wv, code, head_dim);
+      num_kv_heads, owner, n_slots, wk, wv, code, head_dim, split);
   rc = launch_status(name);
   if (rc) return rc;
   return prefill_launch(name, q, q_tok_stride, q_head_stride, wk, wv, (int32_t)std::min<int64_t>(entries, 0x7fffffff),
