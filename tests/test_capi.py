@@ -195,9 +195,15 @@ def test_decode_workspace_size():
     r8 = lambda n: (n + 7) // 8 * 8
     # partials (256-byte aligned), then a 256-byte header and one int per (sequence, chunk) pair
     assert lib.pa_decode_workspace_size(256, 32, 128, 32, 256) == r256(256 * 32 * 4 * (128 + 2) * 4) + 256 + 4 * 1024
-    # 16-token pages: 1024-token items (64 page ids per chunk), ceil(100 * 16 / 1024) = 2 chunks
-    assert lib.pa_decode_workspace_size(4, 8, 128, 100, 16) == r256(4 * 8 * 2 * (128 + 2) * 4) + 256 + 4 * r8(8)
-    assert lib.pa_decode_workspace_size(3, 8, 128, 100, 16) == r256(3 * 8 * 2 * (128 + 2) * 4) + 256 + 4 * r8(6)
+    # a small launch halves its chunk (down to 512 tokens) until it has 64 (sequence, chunk) pairs:
+    # 4 x 1600-token rows of 16-token pages -> 512-token items, ceil(1600 / 512) = 4 chunks
+    assert lib.pa_decode_workspace_size(4, 8, 128, 100, 16) == r256(4 * 8 * 4 * (128 + 2) * 4) + 256 + 4 * r8(16)
+    assert lib.pa_decode_workspace_size(3, 8, 128, 100, 16) == r256(3 * 8 * 4 * (128 + 2) * 4) + 256 + 4 * r8(12)
+    # one 32 768-token row: 2048 -> 512-token items (64 pairs), 64 chunks
+    assert lib.pa_decode_workspace_size(1, 32, 128, 128, 256) == r256(32 * 64 * (128 + 2) * 4) + 256 + 4 * r8(64)
+    # 8 x 8192-token rows: 1024-token items (64 pairs); 16 of them keep 2048-token ones
+    assert lib.pa_decode_workspace_size(8, 32, 128, 32, 256) == r256(8 * 32 * 8 * (128 + 2) * 4) + 256 + 4 * 64
+    assert lib.pa_decode_workspace_size(16, 32, 128, 32, 256) == r256(16 * 32 * 4 * (128 + 2) * 4) + 256 + 4 * 64
     assert lib.pa_decode_workspace_size(0, 32, 128, 32, 256) == 0
     # the generic decode's 1024-token items at head sizes below 128 other than 64
     assert lib.pa_decode_workspace_size(4, 8, 96, 32, 256) == r256(4 * 8 * 8 * (96 + 2) * 4) + 256 + 4 * r8(32)

@@ -47,6 +47,8 @@ def _run_and_check(pkg, dev, db, seed, *, seqs=None, soft_cap=None):
     ([1, 70, 2049, 300], 40, 2, 256),                       # G = 20: two blocks of q heads, the second partial
     ([17, 1100, 2050], 32, 1, 16),                          # G = 32, 16-token pages, several chunks
     ([0, 5, 600], 17, 1, 24),                               # G = 17, unaligned pages, length 0
+    ([32768], 32, 8, 256),                                  # one long sequence: 512-token items, 64 partials
+    ([511, 512, 513, 1025, 9000], 32, 8, 16),               # a few sequences: 512-token items, 16-token pages
 ])
 def test_decode_small(pkg, dev, lens, h, hkv, bs):
     # power-of-two table width: the oracle keeps the reference's split divisibility rules

@@ -73,6 +73,7 @@ def _run(pkg, dev, q, kc, vc, bt, cu, kv, pos, nd, max_q, soft_cap=None, decode_
     ([5000, 300], [90, 1], [0, 0], 32, 1, 256, 0),                         # G = 32 (one kv head), 2 chunks
     ([9000, 4500, 100], [300], [0], 16, 8, 4096, 0),                       # 4096-token pages: chunk = page
     ([9000, 5000, 4097], [100], [0], 16, 8, 8192, 0),                      # 8192-token pages: chunks start mid-page
+    ([20000, 300], [64], [0], 16, 8, 256, 0),                              # 5 decode chunks: the workgroup-wide merge
 ])
 def test_mixed_matches_oracle(pkg, dev, dec, pre_q, pre_p, h, hkv, bs, pad):
     rng = np.random.default_rng(len(dec) * 100 + h + bs)

@@ -112,9 +112,75 @@ decode_merge_kernel(DecodeParams p) {
   *dst = pack_bf16x2(o0 * inv, o1 * inv);
 }
 
+// The merge of launches with many chunks per sequence (a few long
+// sequences): one workgroup per (sequence, q head), so that its partials are
+// read in parallel.  Eight groups of 32 threads take every eighth chunk, a
+// thread four d values of it (16 bytes); the sums of the groups meet in LDS.
+constexpr int kMergeWideChunks = 4;  // launches with more chunks per sequence take the wide merge
+__global__ void __launch_bounds__(256)
+decode_merge_wide_kernel(DecodeParams p) {
+  __shared__ float red[8][kHeadDim];
+  __shared__ float red_m[4], red_l[4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int b = (int)(blockIdx.x / p.num_heads);
+  const int h = (int)(blockIdx.x - (int64_t)b * p.num_heads);
+  if (!decode_has_row(p, b)) return;  // uniform over the workgroup
+  const int kvh = h / p.group;
+  const int qi = h - kvh * p.group;
+  const int len = min(p.lengths[b], p.pages_per_seq * p.page_size);
+  const int nc = len > 0 ? min((len + p.chunk - 1) / p.chunk, p.n_chunks) : 0;
+  if (nc == 1) return;
+  const int64_t base = ((int64_t)b * p.num_kv_heads + kvh) * p.n_chunks;
+  auto ml = [&](int c) __attribute__((always_inline)) { return p.ws_ml + 2 * ((base + c) * p.group + qi); };
+  // M = the largest chunk max; L = sum_c l_c 2^(m_c - M)
+  float mx = -INFINITY;
+  for (int c = tid; c < nc; c += 256) mx = fmaxf(mx, ml(c)[0]);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if (lane == 0) red_m[wave] = mx;
+  __syncthreads();
+  const float mmax = fmaxf(fmaxf(red_m[0], red_m[1]), fmaxf(red_m[2], red_m[3]));
+  float ls = 0.f;
+  for (int c = tid; c < nc; c += 256) ls += ml(c)[1] * fast_exp2(ml(c)[0] - mmax);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ls += __shfl_xor(ls, o);
+  if (lane == 0) red_l[wave] = ls;
+  // O = sum_c o_c 2^(m_c - M): group g = tid / 32 takes chunks g, g + 8, ...
+  const int g = tid >> 5, e = tid & 31;
+  float4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+  for (int c = g; c < nc; c += 8) {
+    const int64_t part = (base + c) * p.group + qi;
+    const float w = fast_exp2(p.ws_ml[2 * part] - mmax);
+    const float4 v = *reinterpret_cast<const float4*>(p.ws_o + part * kHeadDim + 4 * e);
+    o.x += v.x * w;
+    o.y += v.y * w;
+    o.z += v.z * w;
+    o.w += v.w * w;
+  }
+  *reinterpret_cast<float4*>(&red[g][4 * e]) = o;
+  __syncthreads();
+  if (tid >= 32) return;
+  const float lsum = red_l[0] + red_l[1] + red_l[2] + red_l[3];
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  float4 t = *reinterpret_cast<const float4*>(&red[0][4 * e]);
+#pragma unroll
+  for (int k = 1; k < 8; ++k) {
+    const float4 v = *reinterpret_cast<const float4*>(&red[k][4 * e]);
+    t.x += v.x;
+    t.y += v.y;
+    t.z += v.z;
+    t.w += v.w;
+  }
+  uint16_t* dst = p.out + decode_row(p, b) * p.out_bs + (int64_t)h * p.out_hs + 4 * e;
+  *reinterpret_cast<u32x2*>(dst) = u32x2{pack_bf16x2(t.x * inv, t.y * inv), pack_bf16x2(t.z * inv, t.w * inv)};
+}
+
 void launch_decode_merge(const DecodeParams& p, hipStream_t s) {
   const int64_t pairs = (int64_t)p.batch * p.num_heads;
-  decode_merge_kernel<<<dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s>>>(p);
+  if (p.n_chunks > kMergeWideChunks) decode_merge_wide_kernel<<<dim3((unsigned)pairs), dim3(256), 0, s>>>(p);
+  else decode_merge_kernel<<<dim3((unsigned)((pairs + 3) / 4)), dim3(256), 0, s>>>(p);
 }
 
 constexpr int64_t kDecodePlanMinItems = 2048;  // workgroups from which pa_decode builds a work list
@@ -128,12 +194,30 @@ constexpr int kDecodeShortChunk = 1024;  // tokens per item of the generic decod
 // -1.3 %, 112 -1.2 %; 64 +1.6 %, 160 +1.6 %, 192 +3.6 %, 224 +1.9 %.
 static bool decode_any_short_chunk(int head_dim) { return head_dim < 128 && head_dim != 64; }
 
+constexpr int kDecodeMinChunk = 512;        // shortest item of a small launch
+constexpr int64_t kDecodeFillPairs = 64;  // (sequence, chunk) pairs of a launch that fills the CUs
+
+// A small launch (fewer than kDecodeFillPairs pairs over the widest table
+// row: a few long sequences) halves its chunk, down to kDecodeMinChunk
+// tokens, until it has that many: with 8 kv heads, 512 items of four waves,
+// one per workgroup slot (two per CU).  One 32 768-token sequence of the
+// Qwen3-8B heads took 2048-token items, 128 workgroups for 256 CUs: 38.8 ->
+// 29.0 us with 512-token ones (same process).  Halving launches that
+// already hold 512 items cost 1-2 % (16 x 8192 and 64 x 2048 tokens).
+// Depends on the batch and the table only, so the workspace size gives the
+// same chunk.
+static int decode_fill_chunk(int chunk, int32_t batch, int64_t span) {
+  while (chunk > kDecodeMinChunk && (int64_t)batch * ((span + chunk - 1) / chunk) < kDecodeFillPairs) chunk /= 2;
+  return chunk;
+}
+
 // Chunks of the widest table row at the shortest chunk a launch can take:
 // the workspace holds one partial per (sequence, q head, chunk) for them.
-static int decode_chunks(int32_t pages_per_seq, int32_t page_size, int32_t head_dim) {
+static int decode_chunks(int32_t batch, int32_t pages_per_seq, int32_t page_size, int32_t head_dim) {
   const int64_t max_tokens = (int64_t)pages_per_seq * page_size;
   int chunk = decode_chunk_tokens(page_size);
   if (head_dim != kHeadDim && decode_any_short_chunk(head_dim)) chunk = min(chunk, kDecodeShortChunk);
+  if (head_dim == kHeadDim) chunk = decode_fill_chunk(chunk, batch, max_tokens);  // decode_split_kernel
   return (int)((max_tokens + chunk - 1) / chunk);
 }
 
@@ -230,7 +314,7 @@ static size_t decode_partials_bytes(int32_t batch, int32_t num_heads, int32_t he
 extern "C" size_t pa_decode_workspace_size(int32_t batch, int32_t num_heads, int32_t head_dim,
                                            int32_t pages_per_seq, int32_t page_size) {
   if (batch <= 0 || num_heads <= 0 || head_dim <= 0 || pages_per_seq <= 0 || page_size <= 0) return 0;
-  const int n_chunks = decode_chunks(pages_per_seq, page_size, head_dim);
+  const int n_chunks = decode_chunks(batch, pages_per_seq, page_size, head_dim);
   const size_t pairs8 = ((size_t)batch * n_chunks + 7) / 8 * 8;
   return decode_partials_bytes(batch, num_heads, head_dim, n_chunks) + (kDecodePlanHeader + pairs8) * sizeof(int32_t);
 }
@@ -331,7 +415,8 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
   // (16 per item here, 32 in the generic kernels)
   const int64_t vheads = (int64_t)num_kv_heads * (any_d ? (group + 31) / 32 : prm.hblocks);
   prm.chunk = any_d ? decode_any_chunk(head_dim, page_size, batch, pages_per_seq, vheads)
-                    : decode_split_chunk(page_size, batch, pages_per_seq, vheads);
+                    : decode_fill_chunk(decode_split_chunk(page_size, batch, pages_per_seq, vheads), batch,
+                                        (int64_t)pages_per_seq * page_size);
   prm.n_chunks =
       pages_per_seq > 0 ? (int)(((int64_t)pages_per_seq * page_size + prm.chunk - 1) / prm.chunk) : 0;
   // (this kernel, aligned pages) the chunk's page ids, one or four per lane
