@@ -194,6 +194,40 @@ def run_page_sizes(args):
             "steps": args.steps, "warmup": args.warmup}
 
 
+def run_small_decode(args):
+    """Decode of a few long sequences (32 q / 8 kv heads, head size 128,
+    256-token pages): 1 x 32 768, 1 x 131 072, 2 x 16 384, 4 x 32 768 and
+    8 x 8 192 context tokens, the whole entry call (split, merge) timed like
+    the other short lines (`_time_ms_warm`)."""
+    import torch
+    import __graft_entry__ as ge
+    pkg = ge.load_package()
+    import vllm_jax_amd.workloads as wl
+    dev = torch.device("cuda:0")
+    res = []
+    for batch, ctx in ((1, 32768), (1, 131072), (2, 16384), (4, 32768), (8, 8192)):
+        db = wl.make_decode([ctx] * batch, num_heads=32, num_kv_heads=8, page_size=256,
+                            rng=np.random.default_rng(1))
+        d = wl.materialize_decode(db, seed=1, device=dev)
+        kv = d["kv_cache"]
+        kp, vp = kv[0].permute(2, 0, 1, 3), kv[1].permute(2, 0, 1, 3)
+        out = torch.empty_like(d["q"])
+        ws = torch.empty(pkg._lib.load().pa_decode_workspace_size(db.batch, 32, 128, db.block_tables.shape[1], 256),
+                         dtype=torch.uint8, device=dev)
+
+        def call():
+            pkg.decode_paged_attention(d["q"], kp, vp, d["block_tables"], d["context_lens"], scale=1 / 11.3125,
+                                       workspace=ws, out=out)
+        ms = _time_ms_warm(torch, call, args)
+        gbs = db.hbm_bytes() / (ms * 1e-3) / 1e9
+        res.append({"seqs": batch, "context": ctx, "gb": round(db.hbm_bytes() / 1e9, 4), "us": round(ms * 1e3, 1),
+                    "gbs": round(gbs, 1), "frac_of_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)})
+        del d, kv, kp, vp, out, ws
+        torch.cuda.empty_cache()
+    return {"metric": "decode attn GB/s, a few long sequences (head size 128, 32 q / 8 kv heads)",
+            "results": res, "steps": args.steps, "warmup": args.warmup}
+
+
 def _time_ms(torch, fn, args):
     for _ in range(args.warmup):
         fn()
@@ -891,7 +925,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["prefill", "decode", "rope", "mixed", "decode_fp8", "prefix", "prefill_fp8",
                                        "long8", "g32",
-                                       "copy", "head_dims", "page_sizes"],
+                                       "copy", "head_dims", "page_sizes", "small_decode"],
                     default=None,
                     help="profiling aid: run one kernel family only (the JSON line then covers that part)")
     args = ap.parse_args()
@@ -908,6 +942,9 @@ def main():
         return
     if args.only == "page_sizes":
         print(json.dumps(run_page_sizes(args)), flush=True)
+        return
+    if args.only == "small_decode":
+        print(json.dumps(run_small_decode(args)), flush=True)
         return
     res, ctx = run_gpu(args)
     if args.only is not None:
