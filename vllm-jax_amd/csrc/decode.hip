@@ -389,6 +389,9 @@ static int decode_common(const char* name, DecodeParams& prm, bool fp8, const ui
     return fail(PA_ERR_UNSUPPORTED, "%s: operands must be 16-byte aligned with strides multiple of 8", name);
   if ((int64_t)pages_per_seq * page_size > 0x7fffffffLL)
     return fail(PA_ERR_UNSUPPORTED, "%s: block table spans more than 2^31 tokens", name);
+  if ((int64_t)batch * num_heads > 0x7fffffffLL)  // the merge grid: up to one workgroup per (sequence, q head)
+    return fail(PA_ERR_UNSUPPORTED, "%s: %lld (sequence, q head) rows, more than 2^31", name,
+                (long long)batch * num_heads);
   const size_t need = pa_decode_workspace_size(batch, num_heads, head_dim, pages_per_seq, page_size);
   if (pages_per_seq > 0 && (!workspace || workspace_bytes < need || ((uintptr_t)workspace & 255u)))
     return fail(PA_ERR_WORKSPACE, "%s: 256-byte aligned workspace of %zu bytes needed, %zu given", name, need,
