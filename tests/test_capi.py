@@ -91,6 +91,20 @@ def test_decode_rejects_bad_arguments_without_a_device():
     assert lib.pa_decode(*_decode_args(page_size=0)) == -1
 
 
+def test_decode_refuses_a_merge_grid_past_2_31_without_a_device():
+    """The decode merge takes up to one workgroup per (sequence, q head): a
+    launch with more than 2^31 - 1 such rows is refused before anything is
+    launched.  The pointers are placeholders (16-byte aligned, never
+    dereferenced on the host); without a workspace a launch of ordinary
+    size stops at the workspace check instead."""
+    lib = PKG._lib.load()
+    fake = dict(q=0x10000, k=0x10000, v=0x10000, bt=0x10000, lens=0x10000, out=0x10000)
+    rc = lib.pa_decode(*_decode_args(batch=1 << 25, heads=64, kv_heads=8, **fake))
+    assert rc == -2
+    assert "(sequence, q head) rows" in lib.pa_last_error().decode()
+    assert lib.pa_decode(*_decode_args(**fake)) == -3
+
+
 def test_decode_noalloc_refuses_oversized_launch_without_a_device():
     """pa_decode_noalloc checks its workspace need against the static
     scratch (64 MiB) before it touches a device: a launch that would need
