@@ -258,14 +258,17 @@ def test_prefill_work_list(pkg, dev, case):
     if case == "pooled":
         pb = wl.make_prefill([4096] * 16, num_heads=64, num_kv_heads=8, rng=np.random.default_rng(13))
     elif case == "prefix":
-        pb = wl.make_prefix_prefill([0, 300, 512, 40, 1500, 3], [130, 64, 200, 1, 700, 260], num_heads=32,
-                                    num_kv_heads=8, rng=np.random.default_rng(7), shared_prefix_tokens=1600)
+        pb = wl.make_prefix_prefill([0, 300, 512, 40, 1500, 3, 900, 64, 2000, 10, 700, 1200],
+                                    [130, 64, 200, 1, 700, 260, 333, 1000, 45, 600, 17, 400], num_heads=32,
+                                    num_kv_heads=8, rng=np.random.default_rng(7), shared_prefix_tokens=2100)
     elif case == "many":
         rng = np.random.default_rng(23)
         pb = wl.make_prefill(rng.integers(1, 300, 90).tolist(), num_heads=16, num_kv_heads=8, page_size=64, rng=rng)
     else:
-        pb = wl.make_prefill([100, 23, 7], num_heads=16, num_kv_heads=8, page_size=16, num_pages=20,
-                             rng=np.random.default_rng(3), pad_tokens_to=256, pad_batch_to=4)
+        pb = wl.make_prefill([100, 23, 7, 1000, 640, 64, 65, 300, 999, 1, 512, 130], num_heads=32, num_kv_heads=8,
+                             page_size=16, rng=np.random.default_rng(3), pad_tokens_to=8192, pad_batch_to=16)
+    nq = -(-pb.max_seqlen_bucket // (256 // (pb.num_heads // pb.num_kv_heads)))
+    assert pb.batch * nq * pb.num_kv_heads >= 1024, "below the work list's launch size"
     t = wl.materialize_prefill(pb, 11, dev)
     pkg.update_kv_cache(t["kv_cache"], t["slot_mapping"], t["k"], t["v"])
     need = pkg._lib.load().pa_prefill_workspace_size(pb.batch, pb.max_seqlen_bucket, pb.num_heads,

@@ -56,6 +56,13 @@ constexpr int64_t kPoolMinItems = 16384;  // smallest grid that uses prefill_ker
 constexpr int kPlanBins = 4096;       // cost classes of the work list (class + 1, clamped)
 constexpr int kPlanClassTiles = 16;   // kv tiles per cost class
 constexpr int kPlanMaxBatch = 2048;   // sequences whose geometry the planner keeps in LDS
+// Launches below this many items run in grid order (longest q-tile levels
+// first) even with a workspace: the list's one-workgroup build costs a few
+// microseconds ahead of the prefill, which short launches do not earn back
+// (same process, bit-identical: the Qwen3-0.6B single-layer prefill 23.0 ->
+// 20.3 us, 4 x 512 tokens of the Qwen3-8B heads 25.4 -> 23.2 us, 1 x 2048
+// 52.2 -> 49.2 us; 256 x 128 and 64 x 1024 tokens, above it, unchanged).
+constexpr int64_t kPrefillPlanMinItems = 1024;
 
 // Work list of the prefill (run by one workgroup).  A pair (sequence b,
 // q tile qt) is listed when the tile has rows; its cost is the number of kv
@@ -464,7 +471,8 @@ static int prefill_launch(const char* name, const uint16_t* q, int64_t q_tok_str
   if (items > 0x7fffffff)
     return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)items);
   // the work list needs every sequence's geometry in the planner's LDS
-  const bool planned = workspace && batch > 0 && max_seqlen_q > 0 && batch <= kPlanMaxBatch;
+  const bool planned = workspace && batch > 0 && max_seqlen_q > 0 && batch <= kPlanMaxBatch &&
+                       items >= kPrefillPlanMinItems;
   int32_t* plan = planned ? reinterpret_cast<int32_t*>(workspace) : nullptr;
   {
     const int64_t zero_blocks = (num_tokens + kPrepThreads / 64 - 1) / (kPrepThreads / 64) + (planned ? 1 : 0);
