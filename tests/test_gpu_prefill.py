@@ -332,9 +332,13 @@ def test_prefill_rows_past_max_seqlen_are_zero(pkg, dev, with_list):
     """max_seqlen_q below a sequence's length: its rows at offset >=
     max_seqlen_q are written as zeros (the reference's scatter covers only
     the first max_seqlen_bucket rows, prefill...:384-388); the rows before
-    are unchanged by the truncation (causal rows see only earlier kv)."""
+    are unchanged by the truncation (causal rows see only earlier kv).  128
+    sequences of one 128-token q tile x 8 kv heads = 1024 items: with a
+    workspace the launch builds its work list and the list's launch zeroes
+    the rows; without, the prefill kernel's last workgroups do."""
     import torch
-    pb = wl.make_prefill([100, 300, 40], num_heads=16, num_kv_heads=8, page_size=64, rng=np.random.default_rng(51))
+    pb = wl.make_prefill([100, 300, 40] + [50] * 125, num_heads=16, num_kv_heads=8, page_size=64,
+                         rng=np.random.default_rng(51))
     t = wl.materialize_prefill(pb, 51, dev)
     kv = pkg.update_kv_cache(t["kv_cache"], t["slot_mapping"], t["k"], t["v"])
     ws = None

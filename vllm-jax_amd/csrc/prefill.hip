@@ -8,9 +8,53 @@
 
 namespace pa {
 
-template <bool kSoftCap, int kPaging>
+// Output rows the prefill items do not write, for 64 tokens t0 .. t0 + 63
+// (one wave): rows outside all sequences (before cu_q[0], from cu_q[batch]
+// on) and rows at offset >= max_seqlen_q inside their sequence (the
+// reference drops those too: its scatter only covers the first
+// max_seqlen_bucket rows, prefill...:384-388) are zeroed.  A lane checks one
+// token; the wave zeroes the rows it found, one after the other.
+__device__ void prefill_zero_rows(const PrefillParams& p, int64_t t0) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = t0 + lane;
+  const int32_t* cu_q = p.cu_q;
+  const int batch = p.batch;
+  bool zero = t < p.num_tokens;
+  if (zero && batch > 0 && t >= cu_q[0] && t < cu_q[batch]) {
+    // last b with cu_q[b] <= t
+    int lo = 0, hi = batch;  // invariant: cu_q[lo] <= t < cu_q[hi]
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (cu_q[mid] <= t) lo = mid;
+      else hi = mid;
+    }
+    zero = t - cu_q[lo] >= p.max_seqlen_q;
+  }
+  uint64_t todo = __ballot(zero);
+  const int chunks = p.num_heads * (kPHeadDim / 8);
+  while (todo) {
+    const int k = __ffsll((unsigned long long)todo) - 1;
+    todo &= todo - 1;
+    uint16_t* row = p.out + (t0 + k) * p.o_ts;
+    for (int c = lane; c < chunks; c += 64) {
+      const int hh = c / (kPHeadDim / 8);
+      st16(row + hh * p.o_hs + (c - hh * (kPHeadDim / 8)) * 8, u32x4{0, 0, 0, 0});
+    }
+  }
+}
+
+// kZero (launches without a work list): workgroups past the items zero the
+// rows no item writes, 512 tokens each, in place of a launch of their own.
+template <bool kSoftCap, int kPaging, bool kZero = false>
 __global__ void __launch_bounds__(kThreads, 1)
 prefill_kernel(PrefillParams p) {
+  if constexpr (kZero) {
+    const int64_t items = (int64_t)p.n_qtiles * p.batch * p.num_kv_heads;
+    if (blockIdx.x >= items) {  // uniform over the workgroup
+      prefill_zero_rows(p, ((int64_t)blockIdx.x - items) * kThreads + 64 * (threadIdx.x >> 6));
+      return;
+    }
+  }
   prefill_body<kSoftCap, kPaging>(p, blockIdx.x);
 }
 
@@ -474,29 +518,34 @@ static int prefill_launch(const char* name, const uint16_t* q, int64_t q_tok_str
   const bool planned = workspace && batch > 0 && max_seqlen_q > 0 && batch <= kPlanMaxBatch &&
                        items >= kPrefillPlanMinItems;
   int32_t* plan = planned ? reinterpret_cast<int32_t*>(workspace) : nullptr;
-  {
-    const int64_t zero_blocks = (num_tokens + kPrepThreads / 64 - 1) / (kPrepThreads / 64) + (planned ? 1 : 0);
+  if (planned) {  // the list and the zero rows, ahead of the prefill
+    const int64_t zero_blocks = (num_tokens + kPrepThreads / 64 - 1) / (kPrepThreads / 64) + 1;
     prefill_prep_kernel<<<dim3((unsigned)zero_blocks), dim3(kPrepThreads), 0, s>>>(prm, plan);
     int rc = launch_status(name);
     if (rc) return rc;
   }
-  if (batch == 0 || max_seqlen_q == 0) return PA_OK;
   prm.plan = plan;
   // the pool pays off on long launches (the XCDs' finishing spread grows with
   // the launch; the extra workgroups cost a dispatch each)
   prm.pool = plan && num_kv_heads % 8 == 0 && items >= kPoolMinItems ? plan + 8 : nullptr;
   // with a list, items past its count return at once; with the pool, a
   // quarter more workgroups than items lets the XCDs that run ahead take up
-  // to twice their share of it
-  const int64_t blocks = prm.pool ? std::min<int64_t>(items + (items + 3) / 4, 0x7fffffff) : items;
+  // to twice their share of it; without a list, workgroups past the items
+  // zero the rows no item writes (512 tokens each: no launch of their own)
+  const int64_t blocks = prm.pool ? std::min<int64_t>(items + (items + 3) / 4, 0x7fffffff)
+                                  : items + (planned ? 0 : (num_tokens + kThreads - 1) / kThreads);
+  if (blocks > 0x7fffffff)
+    return fail(PA_ERR_UNSUPPORTED, "%s: grid of %lld workgroups too large", name, (long long)blocks);
+  if (blocks == 0) return PA_OK;
   const int paging = prefill_paging(page_size, slot_stride);
   const dim3 g((unsigned)blocks), b(kThreads);
-  // one instance per (soft cap, paging, pool)
+  // one instance per (soft cap, paging, pool | list | grid order with the zero rows)
   auto launch = [&](auto cap, auto pg) {
     constexpr bool kCap = decltype(cap)::value;
     constexpr int kPg = decltype(pg)::value;
     if (prm.pool) prefill_kernel_pooled<kCap, kPg><<<g, b, 0, s>>>(prm);
-    else prefill_kernel<kCap, kPg><<<g, b, 0, s>>>(prm);
+    else if (planned) prefill_kernel<kCap, kPg><<<g, b, 0, s>>>(prm);
+    else prefill_kernel<kCap, kPg, true><<<g, b, 0, s>>>(prm);
   };
   auto with_paging = [&](auto cap) {
     if (paging == kPageTile) launch(cap, std::integral_constant<int, kPageTile>{});
