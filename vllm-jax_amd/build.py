@@ -28,7 +28,7 @@ ARCH = "gfx950"
 
 SOURCES = ["pa_errors.cpp", "block_manager.cpp", "kv_store.hip", "decode.hip", "prefill.hip", "qk_norm_rope.hip",
            "mixed.hip", "any_head.hip"]
-PHASES_SOURCES = ["pa_errors.cpp", "prefill.hip"]
+PHASES_SOURCES = ["pa_errors.cpp", "prefill.hip", "any_head.hip"]  # any_head: the head-size check of the quantized entries
 
 # Packed-FP32 VALU forms are disabled for every device compile: the build
 # relies on scalar/float2 code only.  Without NaN semantics, fmaxf lowers to a
