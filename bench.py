@@ -142,6 +142,62 @@ def run_head_dims(args):
             "steps": args.steps, "warmup": args.warmup}
 
 
+def run_soft_cap(args):
+    """Attention with and without the logit soft cap (cap 50) on the
+    head-size shapes: prefill of 16 sequences of 2 048 new tokens and the
+    Qwen3-8B-shaped decode batch (256 sequences, contexts U[512, 8192]),
+    32 q / 8 kv heads, at head size 128 (tuned kernels) and 256 (generic
+    kernels).  Attention only; HIP events, the median of three rounds of
+    `steps` launches after at least 150 ms of warm-up launches per case."""
+    import torch
+    import __graft_entry__ as ge
+    pkg = ge.load_package()
+    import vllm_jax_amd.workloads as wl
+    dev = torch.device("cuda:0")
+    lens_d = np.random.default_rng(2).integers(512, 8193, size=256)
+    pre, dec = [], []
+    for d in (128, 256):
+        pb = wl.make_prefill([2048] * 16, num_heads=32, num_kv_heads=8, head_dim=d, rng=np.random.default_rng(9))
+        t = wl.materialize_prefill(pb, seed=9, device=dev, fill_pool=True)
+        kp, vp = t["kv_cache"][0].permute(2, 0, 1, 3), t["kv_cache"][1].permute(2, 0, 1, 3)
+        out = torch.empty_like(t["q"])
+        row = {"head_dim": d}
+        for cap in (None, 50.0):
+            def attn():
+                pkg.prefill_paged_attention(t["q"], kp, vp, t["block_tables"], t["cu_seqlens_q"], t["slot_mapping"],
+                                            t["input_positions"], max_seqlen_bucket=pb.max_seqlen_bucket,
+                                            cu_seqlens_k=t["cu_seqlens_k"], attn_logits_soft_cap=cap, out=out)
+            ms = _time_ms_warm(torch, attn, args)
+            tf = pb.flops() / (ms * 1e-3) / 1e12
+            row["soft_cap_ms" if cap else "ms"] = round(ms, 4)
+            row["soft_cap_tflops" if cap else "tflops"] = round(tf, 1)
+        row["soft_cap_over_plain"] = round(row["soft_cap_ms"] / row["ms"], 3)
+        pre.append(row)
+        del t, kp, vp, out
+        db = wl.make_decode(lens_d, num_heads=32, num_kv_heads=8, head_dim=d, rng=np.random.default_rng(2))
+        dd = wl.materialize_decode(db, seed=2, device=dev)
+        kv = dd["kv_cache"]
+        kpd, vpd = kv[0].permute(2, 0, 1, 3), kv[1].permute(2, 0, 1, 3)
+        outd = torch.empty_like(dd["q"])
+        row = {"head_dim": d}
+        for cap in (None, 50.0):
+            def dec_call():
+                pkg.decode_paged_attention(dd["q"], kpd, vpd, dd["block_tables"], dd["context_lens"],
+                                           attn_logits_soft_cap=cap, out=outd)
+            ms = _time_ms_warm(torch, dec_call, args)
+            gbs = db.hbm_bytes() / (ms * 1e-3) / 1e9
+            row["soft_cap_ms" if cap else "ms"] = round(ms, 4)
+            row["soft_cap_gbs" if cap else "gbs"] = round(gbs, 1)
+        row["soft_cap_over_plain"] = round(row["soft_cap_ms"] / row["ms"], 3)
+        dec.append(row)
+        del dd, kv, kpd, vpd, outd
+        torch.cuda.empty_cache()
+    return {"metric": "attention with the logit soft cap (50) against without, head sizes 128 and 256",
+            "prefill": {"workload": "16 x 2048 new tokens, 32 q / 8 kv heads, causal", "results": pre},
+            "decode": {"workload": "256 sequences, contexts U[512, 8192], 32 q / 8 kv heads", "results": dec},
+            "steps": args.steps, "warmup": args.warmup}
+
+
 def run_page_sizes(args):
     """Prefill and decode over pages of 16, 32, 64 and 256 tokens, the same
     tokens each time: the Qwen3-8B prefix-cached prefill (seed 3's lengths)
@@ -925,7 +981,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["prefill", "decode", "rope", "mixed", "decode_fp8", "prefix", "prefill_fp8",
                                        "long8", "g32",
-                                       "copy", "head_dims", "page_sizes", "small_decode"],
+                                       "copy", "head_dims", "page_sizes", "small_decode", "soft_cap"],
                     default=None,
                     help="profiling aid: run one kernel family only (the JSON line then covers that part)")
     args = ap.parse_args()
@@ -939,6 +995,9 @@ def main():
         return
     if args.only == "head_dims":
         print(json.dumps(run_head_dims(args)), flush=True)
+        return
+    if args.only == "soft_cap":
+        print(json.dumps(run_soft_cap(args)), flush=True)
         return
     if args.only == "page_sizes":
         print(json.dumps(run_page_sizes(args)), flush=True)

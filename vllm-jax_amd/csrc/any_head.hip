@@ -113,7 +113,7 @@ __device__ __forceinline__ void lds_st16(lds_char* a, const u32x4& v) {
 // cap * log2 e * tanh(x * scale / cap) (scale = logit_scale of the params).
 template <bool kSoftCap>
 __device__ __forceinline__ float any_logit(float x, float logit_scale, float cap) {
-  if constexpr (kSoftCap) return cap * kLog2e * tanhf(x * logit_scale / cap);
+  if constexpr (kSoftCap) return soft_cap_log2(x, soft_cap_s2(logit_scale, cap), soft_cap_c(cap));
   else return x;
 }
 
@@ -135,7 +135,7 @@ __device__ __forceinline__ bf16x8 any_q_operand(const u32x4& raw, float logit_sc
 // cap as above (decode, whose q is not scaled in bf16 first).
 template <bool kSoftCap>
 __device__ __forceinline__ float any_logit_f32(float x, float logit_scale, float cap) {
-  if constexpr (kSoftCap) return cap * kLog2e * tanhf(x * logit_scale / cap);
+  if constexpr (kSoftCap) return soft_cap_log2(x, soft_cap_s2(logit_scale, cap), soft_cap_c(cap));
   else return x * logit_scale;
 }
 

@@ -407,7 +407,7 @@ __device__ __forceinline__ void decode_item(const DecodeParams& p, int item, flo
     for (int r = 0; r < 4; ++r) {
       float v = sc[r];
       if constexpr (kFp8) v *= __uint_as_float(sb[j][0][r]);
-      if constexpr (kSoftCap) v = p.soft_cap * tanhf(v * p.logit_scale / p.soft_cap) * kLog2e;
+      if constexpr (kSoftCap) v = soft_cap_log2(v, soft_cap_s2(p.logit_scale, p.soft_cap), soft_cap_c(p.soft_cap));
       else v = v * p.logit_scale;
       v = t0 + 4 * g + r < len ? v : -INFINITY;
       x[r] = v;

@@ -136,6 +136,20 @@ __device__ __forceinline__ float sum_xor16(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Soft-capped logit in log2 units, cap * log2 e * tanh(x * scale / cap),
+// from tanh(y) = 1 - 2 / (e^(2y) + 1): c - 2c / (2^(x * s2) + 1) with
+// s2 = 2 log2(e) scale / cap and c = cap log2 e (soft_cap_s2, soft_cap_c).  One
+// v_exp_f32 and one v_rcp_f32 (about 1 ulp each) instead of the library
+// tanhf; for large |y| the power is +inf or 0 and the result exactly +-c.
+// The absolute error is a few 2^-24 c, below the bf16 rounding of P.
+__device__ __forceinline__ float soft_cap_log2(float x, float s2, float c) {
+  return c - (2.f * c) * __builtin_amdgcn_rcpf(fast_exp2(x * s2) + 1.f);
+}
+__device__ __forceinline__ float soft_cap_s2(float logit_scale, float cap) {
+  return 2.f * kLog2e * logit_scale / cap;
+}
+__device__ __forceinline__ float soft_cap_c(float cap) { return cap * kLog2e; }
+
 // Exclusive scan over the workgroup (blockDim.x == kScanThreads) of one
 // value per thread; `tmp` is kScanThreads ints of LDS.  Returns the sum of
 // the values of lower threads; `total` receives the sum of all.

@@ -610,6 +610,8 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
       }
     }
   };
+  const float cap_s2 = kSoftCap ? soft_cap_s2(p.logit_scale, p.soft_cap) : 0.f;
+  const float cap_c = kSoftCap ? soft_cap_c(p.soft_cap) : 0.f;
   auto softmax = [&](int t, auto&& between) __attribute__((always_inline)) {
     const int j0 = t * kTileN;
     if constexpr (kSoftCap) {
@@ -617,7 +619,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-          s_acc[mt][i] = p.soft_cap * kLog2e * tanhf(s_acc[mt][i] * p.logit_scale / p.soft_cap);
+          s_acc[mt][i] = soft_cap_log2(s_acc[mt][i], cap_s2, cap_c);
     }
     // s_acc[mt][i] = S[row n][token j0 + 32mt + 8(i/4) + 4h + i%4]
     if (t >= n_free) {
