@@ -116,6 +116,14 @@ def test_decode_qwen3_8b_full(pkg, dev):
     _run_and_check(pkg, dev, db, seed=2)
 
 
+def test_decode_qwen3_8b_full_soft_cap(pkg, dev):
+    """The full Qwen3-8B decode workload with a logit soft cap of 30 (the
+    kernels' exp2 / reciprocal evaluation of cap * tanh(logit / cap));
+    every sequence against the oracle's float64 tanh."""
+    db = wl.qwen3_8b_decode()
+    _run_and_check(pkg, dev, db, seed=2, soft_cap=30.0)
+
+
 def test_decode_through_attention_seam(pkg, dev):
     """attention() with DecodeAttentionMetadata: KV store of the new token, then decode."""
     import torch

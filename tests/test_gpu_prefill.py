@@ -150,6 +150,18 @@ def test_prefill_qwen3_8b_prefix_workload(pkg, dev):
     _prefill(pkg, dev, pb, seed=3, rows=rows)
 
 
+def test_prefill_qwen3_8b_prefix_workload_soft_cap(pkg, dev):
+    """The full Qwen3-8B prefix-cached workload with a logit soft cap of 30
+    (the soft-capped prefill kernel): first, last and edge rows of every
+    sequence against the oracle's float64 tanh."""
+    pb = wl.qwen3_8b_prefix_prefill()
+    prefix = np.diff(pb.cu_seqlens_k) - np.diff(pb.cu_seqlens_q)
+    rows = boundary_rows(pb.cu_seqlens_q, prefix, np.random.default_rng(6),
+                         tile_tokens=256 // (pb.num_heads // pb.num_kv_heads), per_seq=4)
+    print(f"qwen3-8b prefix-cached, soft cap 30: {rows.size} rows over {pb.batch} sequences", flush=True)
+    _prefill(pkg, dev, pb, seed=3, rows=rows, soft_cap=30.0, use_seam=False)
+
+
 def test_prefill_qwen3_06b_mixed_prefill_half(pkg, dev):
     """The 32 prefill sequences of the Qwen3-0.6B mixed step: first, last and
     edge rows of every sequence (>= 256 rows)."""
