@@ -145,6 +145,12 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ float soft_cap_log2(float x, float s2, float c) {
   return c - (2.f * c) * __builtin_amdgcn_rcpf(fast_exp2(x * s2) + 1.f);
 }
+// The same minus an offset m: (c - m) - 2c / (2^(x * s2) + 1), with
+// two_c = 2c and cm = c - m, so that logits relative to a reference max
+// cost no extra subtraction.
+__device__ __forceinline__ float soft_cap_log2_rel(float x, float s2, float two_c, float cm) {
+  return cm - two_c * __builtin_amdgcn_rcpf(fast_exp2(x * s2) + 1.f);
+}
 __device__ __forceinline__ float soft_cap_s2(float logit_scale, float cap) {
   return 2.f * kLog2e * logit_scale / cap;
 }

@@ -566,7 +566,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc_o[dt][i] = 0.f;
-  float m_ref = kSoftCap ? -1e30f : 0.f;  // reference max (log2 units) of the accumulators
+  float m_ref = 0.f;  // reference max (log2 units) of the accumulators
   f32x16 neg_mref = {};  // -m_ref in every element: the QK accumulators start from it
   // running row sums, one per quarter of a tile (four short add chains), of
   // the f32 exponentials: v_dot2c on the packed P would wait for the matrix
@@ -612,14 +612,17 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
   };
   const float cap_s2 = kSoftCap ? soft_cap_s2(p.logit_scale, p.soft_cap) : 0.f;
   const float cap_c = kSoftCap ? soft_cap_c(p.soft_cap) : 0.f;
+  const float cap_2c = 2.f * cap_c;
   auto softmax = [&](int t, auto&& between) __attribute__((always_inline)) {
     const int j0 = t * kTileN;
     if constexpr (kSoftCap) {
+      // capped logits relative to m_ref, as the uncapped S leaves the MFMAs
+      const float cap_cm = cap_c - m_ref;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-          s_acc[mt][i] = soft_cap_log2(s_acc[mt][i], cap_s2, cap_c);
+          s_acc[mt][i] = soft_cap_log2_rel(s_acc[mt][i], cap_s2, cap_2c, cap_cm);
     }
     // s_acc[mt][i] = S[row n][token j0 + 32mt + 8(i/4) + 4h + i%4]
     if (t >= n_free) {
@@ -646,7 +649,7 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
     }
     float mx = __builtin_fmaxf(__builtin_fmaxf(mq[0], mq[1]), __builtin_fmaxf(mq[2], mq[3]));
     mx = max_xor32(mx);  // log2 units: S is computed from the scaled Q (soft cap: capped logits)
-    if constexpr (!kSoftCap) {
+    {
       // S is already relative to m_ref.  The first tile sets m_ref to the row
       // max (a row that sees no key keeps 0); later the reference moves only
       // when a row max exceeds it by more than the slack (any lane).
@@ -665,14 +668,6 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
 #pragma unroll
         for (int mt = 0; mt < 2; ++mt) s_acc[mt] = s_acc[mt] - d;
       }
-    } else if (__any(mx > m_ref + kRescaleSlack)) {
-      const float m_new = fmaxf(m_ref, mx);
-      const float corr = fast_exp2(m_ref - m_new);
-      m_ref = m_new;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) l_part[u] *= corr;
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) acc_o[dt] = acc_o[dt] * corr;
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -682,8 +677,8 @@ __device__ __forceinline__ void prefill_run(const PrefillParams& p, const Prefil
       u32x4 w;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float a = fast_exp2(kSoftCap ? s_acc[mt][base + 2 * e] - m_ref : s_acc[mt][base + 2 * e]);
-        const float c = fast_exp2(kSoftCap ? s_acc[mt][base + 2 * e + 1] - m_ref : s_acc[mt][base + 2 * e + 1]);
+        const float a = fast_exp2(s_acc[mt][base + 2 * e]);
+        const float c = fast_exp2(s_acc[mt][base + 2 * e + 1]);
         w[e] = pack_bf16x2(a, c);
         l_part[u] += a + c;
       }
